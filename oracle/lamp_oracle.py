@@ -1,0 +1,443 @@
+"""Python face of the CPU oracle.  TEST INFRASTRUCTURE.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this module; it is the checker, never the thing measured or shipped.
+
+Two layers:
+  * numpy-level wrappers over liblamp_cpu.so (the C restatement of Lamp3's CPU
+    kernels, oracle/lamp_cpu.c);
+  * ``OVar``, a restatement of Lamp3's autograd over those kernels: the same
+    forward ops, the same backward formulas
+    (autograd/functions/expand_ops.cpp:15-40, unary_ops.cpp:16-28,
+    reduct_ops.cpp:11-16, matrix_ops.cpp:8-35), the same broadcast-gradient
+    reduction (autograd/utils/grad_utils.cpp:10-36), the same DFS topological
+    order and ones-seeded backward (autograd/variable.cpp:46-80), and
+    accumulation of every gradient contribution in place
+    (variable.cpp:30-35).  Inputs that are leaves created with
+    requires_grad=True start with a zero gradient (variable.hpp:24-28).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+DBL_MAX = sys.float_info.max
+
+BIN = dict(add=0, sub=1, mul=2, div=3, pow=4, eq=5, ne=6, ge=7, le=8, gt=9,
+           lt=10, abs_backward=11, clamp_backward=12)
+UN = dict(neg=0, exp=1, log=2, sqrt=3, abs=4, sin=5, cos=6, tan=7, clamp=8)
+RED = dict(sum=0, max=1, min=2, prod=3)
+
+_libs: dict[str, C.CDLL] = {}
+
+
+def load(fast: bool = False) -> C.CDLL:
+    """liblamp_cpu.so (strict IEEE, for parity) or liblamp_cpu_fast.so
+    (the reference's -ffast-math flags, for the timed CPU baseline)."""
+    name = "liblamp_cpu_fast.so" if fast else "liblamp_cpu.so"
+    if name not in _libs:
+        path = HERE / name
+        if not path.exists():
+            raise RuntimeError(f"{path} missing: run `python -m rushlite_amd.build oracle`")
+        lib = C.CDLL(str(path))
+        P = C.c_void_p
+        i64 = C.c_int64
+        lib.lcpu_binary_f32.argtypes = [C.c_int, P, P, P, C.c_int, P, P, P,
+                                        C.c_int, C.c_double, C.c_double]
+        lib.lcpu_unary_f32.argtypes = [C.c_int, P, P, i64, C.c_double, C.c_double]
+        lib.lcpu_reduce_f32.argtypes = [C.c_int, P, P, C.c_int, P, C.c_int]
+        lib.lcpu_matmul_f32.argtypes = [P, P, P, i64, i64, i64]
+        lib.lcpu_transpose_f32.argtypes = [P, P, i64, i64]
+        lib.lcpu_fill_f32.argtypes = [P, i64, C.c_double]
+        lib.lcpu_add_inplace_f32.argtypes = [P, P, i64]
+        lib.lcpu_num_threads.restype = C.c_int
+        for fn in ("lcpu_binary_f32", "lcpu_unary_f32", "lcpu_reduce_f32",
+                   "lcpu_matmul_f32", "lcpu_transpose_f32", "lcpu_fill_f32",
+                   "lcpu_add_inplace_f32"):
+            getattr(lib, fn).restype = None
+        _libs[name] = lib
+    return _libs[name]
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def broadcast_shape(a_shape, b_shape):
+    """Right-aligned broadcast (tensor/utils/align_utils.cpp:18-40)."""
+    nd = max(len(a_shape), len(b_shape))
+    out = []
+    for i in range(nd):
+        off = nd - 1 - i
+        ai = len(a_shape) - 1 - off
+        bi = len(b_shape) - 1 - off
+        av = a_shape[ai] if ai >= 0 else 1
+        bv = b_shape[bi] if bi >= 0 else 1
+        if not (av == 1 or bv == 1 or av == bv):
+            raise ValueError("calc_aligned_shape: Broadcast rule violation.")
+        out.append(av if av != 1 else bv)
+    return tuple(out)
+
+
+def padded_strides(in_shape, nd):
+    """Contiguous strides right-aligned to nd dims, 0 on size-1 dims
+    (cpu/offset_util.cpp:7-28)."""
+    contig, s = [0] * len(in_shape), 1
+    for i in range(len(in_shape) - 1, -1, -1):
+        contig[i] = s
+        s *= in_shape[i]
+    out = [0] * nd
+    for k in range(len(in_shape)):
+        if in_shape[len(in_shape) - 1 - k] != 1:
+            out[nd - 1 - k] = contig[len(in_shape) - 1 - k]
+    return out
+
+
+def binary(op: str, a, b, p0: float = 0.0, p1: float = 0.0, fast: bool = False):
+    a, b = _f32(a), _f32(b)
+    same = a.shape == b.shape
+    out_shape = a.shape if same else broadcast_shape(a.shape, b.shape)
+    out = np.empty(out_shape, np.float32)
+    nd = len(out_shape)
+    shp = np.array(out_shape if nd else [1], np.int64)
+    sa = np.array(padded_strides(a.shape, nd) if nd else [0], np.int64)
+    sb = np.array(padded_strides(b.shape, nd) if nd else [0], np.int64)
+    load(fast).lcpu_binary_f32(BIN[op], out.ctypes.data, a.ctypes.data,
+                               b.ctypes.data, max(nd, 1), shp.ctypes.data,
+                               sa.ctypes.data, sb.ctypes.data, int(same), p0, p1)
+    return out
+
+
+def unary(op: str, a, p0: float = 0.0, p1: float = 0.0, fast: bool = False):
+    a = _f32(a)
+    out = np.empty_like(a)
+    load(fast).lcpu_unary_f32(UN[op], out.ctypes.data, a.ctypes.data, a.size,
+                              p0, p1)
+    return out
+
+
+def reduce(op: str, a, axis: int, fast: bool = False):
+    a = _f32(a)
+    oshape = list(a.shape)
+    oshape[axis] = 1
+    out = np.empty(oshape, np.float32)
+    shp = np.array(a.shape, np.int64)
+    load(fast).lcpu_reduce_f32(RED[op], out.ctypes.data, a.ctypes.data, a.ndim,
+                               shp.ctypes.data, axis)
+    return out
+
+
+def matmul(a, b, fast: bool = False):
+    a, b = _f32(a), _f32(b)
+    if a.ndim != 2 or b.ndim != 2 or a.shape[1] != b.shape[0]:
+        raise ValueError("matmul: incompatible shapes")
+    out = np.empty((a.shape[0], b.shape[1]), np.float32)
+    load(fast).lcpu_matmul_f32(out.ctypes.data, a.ctypes.data, b.ctypes.data,
+                               a.shape[0], b.shape[1], a.shape[1])
+    return out
+
+
+def transpose(a, fast: bool = False):
+    a = _f32(a)
+    out = np.empty((a.shape[1], a.shape[0]), np.float32)
+    load(fast).lcpu_transpose_f32(out.ctypes.data, a.ctypes.data, a.shape[0],
+                                  a.shape[1])
+    return out
+
+
+def fill(shape, value: float, fast: bool = False):
+    out = np.empty(shape, np.float32)
+    load(fast).lcpu_fill_f32(out.ctypes.data, out.size, value)
+    return out
+
+
+def add_inplace(dst: np.ndarray, src, fast: bool = False) -> None:
+    src = _f32(src)
+    assert dst.dtype == np.float32 and dst.flags.c_contiguous and dst.shape == src.shape
+    load(fast).lcpu_add_inplace_f32(dst.ctypes.data, src.ctypes.data, dst.size)
+
+
+def num_threads(fast: bool = False) -> int:
+    return load(fast).lcpu_num_threads()
+
+
+# ----------------------------------------------------------------- autograd
+
+
+class OVar:
+    """Lamp3 Variable restated over the oracle kernels (fp32 only)."""
+
+    def __init__(self, data, requires_grad: bool = False, _fn=None):
+        self.data = _f32(data)
+        self.requires_grad = requires_grad
+        self.grad = fill(self.data.shape, 0.0) if requires_grad else None
+        self.grad_fn = _fn  # (backward callable, saved inputs)
+
+    # -- construction helpers
+    @staticmethod
+    def _scalar(v) -> "OVar":
+        # Python scalars become [1] tensors of the Variable's dtype
+        # (autograd/functions/overloads.hpp:16-29).
+        return OVar(np.array([v], np.float32))
+
+    @staticmethod
+    def _wrap(x) -> "OVar":
+        return x if isinstance(x, OVar) else OVar._scalar(x)
+
+    @staticmethod
+    def _make(data, inputs, backward) -> "OVar":
+        rg = any(i.requires_grad for i in inputs)
+        out = OVar(data, requires_grad=rg)
+        if rg:
+            out.grad_fn = (backward, inputs)
+        return out
+
+    def incr_grad(self, g) -> None:
+        g = _f32(g)
+        assert g.shape == self.grad.shape, (g.shape, self.grad.shape)
+        add_inplace(self.grad, g)
+
+    # -- operators
+    def __add__(self, o): return add(self, OVar._wrap(o))
+    def __radd__(self, o): return add(OVar._wrap(o), self)
+    def __sub__(self, o): return sub(self, OVar._wrap(o))
+    def __rsub__(self, o): return sub(OVar._wrap(o), self)
+    def __mul__(self, o): return mul(self, OVar._wrap(o))
+    def __rmul__(self, o): return mul(OVar._wrap(o), self)
+    def __truediv__(self, o): return div(self, OVar._wrap(o))
+    def __rtruediv__(self, o): return div(OVar._wrap(o), self)
+    def __neg__(self): return neg(self)
+    def __matmul__(self, o): return matmul_v(self, o)
+
+    def backward(self) -> None:
+        visited, topo = set(), []
+
+        def dfs(v):
+            if id(v) in visited:
+                return
+            visited.add(id(v))
+            if v.grad_fn is None:
+                topo.append(v)
+                return
+            for child in v.grad_fn[1]:
+                dfs(child)
+            topo.append(v)
+
+        dfs(self)
+        topo.reverse()
+        self.grad = fill(self.data.shape, 1.0)
+        for node in topo:
+            if node.grad_fn is not None:
+                node.grad_fn[0](node)
+
+
+def sum_broadcast_axis(grad: np.ndarray, orig_shape) -> np.ndarray:
+    """autograd/utils/grad_utils.cpp:10-36."""
+    orig_shape = tuple(orig_shape)
+    if grad.shape == orig_shape:
+        return grad
+    g = grad
+    while g.ndim > len(orig_shape):
+        g = reduce("sum", g, 0).reshape(g.shape[1:])
+    for i, n in enumerate(orig_shape):
+        if n == 1:
+            g = reduce("sum", g, i)
+    assert g.shape == orig_shape, (g.shape, orig_shape)
+    return g
+
+
+def _binary_var(op, a: OVar, b: OVar, grads):
+    out = binary(op, a.data, b.data)
+
+    def bw(node):
+        ga, gb = grads(node, a, b)
+        if a.requires_grad:
+            a.incr_grad(sum_broadcast_axis(ga(), a.data.shape))
+        if b.requires_grad:
+            b.incr_grad(sum_broadcast_axis(gb(), b.data.shape))
+
+    return OVar._make(out, [a, b], bw)
+
+
+def add(a, b):
+    return _binary_var("add", a, b, lambda n, a, b: (lambda: n.grad, lambda: n.grad))
+
+
+def sub(a, b):
+    return _binary_var("sub", a, b,
+                       lambda n, a, b: (lambda: n.grad, lambda: unary("neg", n.grad)))
+
+
+def mul(a, b):
+    return _binary_var("mul", a, b, lambda n, a, b: (
+        lambda: binary("mul", b.data, n.grad),
+        lambda: binary("mul", a.data, n.grad)))
+
+
+def div(a, b):
+    # d/da = g / b ; d/db = (-1.0) * (out * g / b)   (expand_ops.cpp:27-32)
+    return _binary_var("div", a, b, lambda n, a, b: (
+        lambda: binary("div", n.grad, b.data),
+        lambda: binary("mul", np.array([-1.0], np.float32),
+                       binary("div", binary("mul", n.data, n.grad), b.data))))
+
+
+def pow_(a, b):
+    # g * b * a^(b-1) ; g * out * log(a)   (expand_ops.cpp:33-40)
+    return _binary_var("pow", a, b, lambda n, a, b: (
+        lambda: binary("mul", binary("mul", n.grad, b.data),
+                       binary("pow", a.data,
+                              binary("sub", b.data, np.array([1.0], np.float32)))),
+        lambda: binary("mul", binary("mul", n.grad, n.data), unary("log", a.data))))
+
+
+def _unary_var(op, a: OVar, grad, p0=0.0, p1=0.0):
+    out = unary(op, a.data, p0, p1)
+
+    def bw(node):
+        if a.requires_grad:
+            a.incr_grad(grad(node, a))
+
+    return OVar._make(out, [a], bw)
+
+
+def neg(a):
+    return _unary_var("neg", a, lambda n, a: unary("neg", n.grad))
+
+
+def exp(a):
+    return _unary_var("exp", a, lambda n, a: binary("mul", n.data, n.grad))
+
+
+def log(a):
+    return _unary_var("log", a, lambda n, a: binary("div", n.grad, a.data))
+
+
+def sqrt(a):
+    return _unary_var("sqrt", a, lambda n, a: binary(
+        "div", n.grad, binary("add", n.data, n.data)))
+
+
+def abs_(a):
+    return _unary_var("abs", a, lambda n, a: binary("abs_backward", a.data, n.grad))
+
+
+def sin(a):
+    return _unary_var("sin", a, lambda n, a: binary("mul", n.grad, unary("cos", a.data)))
+
+
+def cos(a):
+    return _unary_var("cos", a, lambda n, a: binary(
+        "mul", unary("neg", unary("sin", a.data)), n.grad))
+
+
+def tan(a):
+    return _unary_var("tan", a, lambda n, a: binary(
+        "add", n.grad, binary("mul", binary("mul", n.grad, n.data), n.data)))
+
+
+def clamp(a, lo, hi):
+    return _unary_var("clamp", a,
+                      lambda n, a: binary("clamp_backward", a.data, n.grad, lo, hi),
+                      lo, hi)
+
+
+def relu(a):
+    """ReLU = clamp(x, 0, DBL_MAX) (nets/layers/activation.cpp:13-15)."""
+    return clamp(a, 0.0, DBL_MAX)
+
+
+def _reduct_var(op, a: OVar, axis: int, grad):
+    out = reduce(op, a.data, axis)
+
+    def bw(node):
+        if a.requires_grad:
+            a.incr_grad(grad(node, a))
+
+    return OVar._make(out, [a], bw)
+
+
+def sum_(a, axis):
+    # ones_like(x) * grad   (reduct_ops.cpp:13)
+    return _reduct_var("sum", a, axis, lambda n, a: binary(
+        "mul", fill(a.data.shape, 1.0), n.grad))
+
+
+def max_(a, axis):
+    # grad * eq(x, out)   (reduct_ops.cpp:14)
+    return _reduct_var("max", a, axis, lambda n, a: binary(
+        "mul", n.grad, binary("eq", a.data, n.data)))
+
+
+def min_(a, axis):
+    return _reduct_var("min", a, axis, lambda n, a: binary(
+        "mul", n.grad, binary("eq", a.data, n.data)))
+
+
+def prod(a, axis):
+    return _reduct_var("prod", a, axis, lambda n, a: binary(
+        "mul", n.grad, binary("div", n.data, a.data)))
+
+
+def matmul_v(a: OVar, b: OVar):
+    out = matmul(a.data, b.data)
+
+    def bw(node):
+        # dA = g @ B^T ; dB = A^T @ g   (functions/matrix_ops.cpp:8-24)
+        if a.requires_grad:
+            a.incr_grad(matmul(node.grad, transpose(b.data)))
+        if b.requires_grad:
+            b.incr_grad(matmul(transpose(a.data), node.grad))
+
+    return OVar._make(out, [a, b], bw)
+
+
+def transpose_v(a: OVar):
+    out = transpose(a.data)
+
+    def bw(node):
+        if a.requires_grad:
+            a.incr_grad(transpose(node.grad))
+
+    return OVar._make(out, [a], bw)
+
+
+def softmax(x: OVar, dim: int) -> OVar:
+    """nets/layers/activation.cpp:31-43."""
+    d = dim if dim >= 0 else x.data.ndim + dim
+    m = max_(x, d)
+    e = exp(x - m)
+    return e / sum_(e, d)
+
+
+# ------------------------------------------------------------------- MLP
+
+
+def mlp_train(weights, biases, x, y, steps: int, lr: float = 1e-3):
+    """Train Linear-ReLU-...-Linear-Softmax with the README loop
+    (README.md:116-126): loss = sum(sum(-y * log(p + 1e-3), 1), 0), full
+    backward, then p <- p.data - lr * p.grad rebuilt as a fresh leaf.
+    Returns (per-step losses, final weights, final biases)."""
+    W = [OVar(w, True) for w in weights]
+    B = [OVar(b, True) for b in biases]
+    xv, yv = OVar(x), OVar(y)
+    losses = []
+    for _ in range(steps):
+        h = xv
+        for i in range(len(W)):
+            h = (h @ W[i]) + B[i]
+            if i < len(W) - 1:
+                h = relu(h)
+        p = softmax(h, -1)
+        loss = sum_(sum_((-yv) * log(p + 1e-3), 1), 0)
+        loss.backward()
+        losses.append(float(loss.data.reshape(-1)[0]))
+        W = [OVar(binary("sub", w.data, binary("mul", np.array([lr], np.float32), w.grad)), True)
+             for w in W]
+        B = [OVar(binary("sub", b.data, binary("mul", np.array([lr], np.float32), b.grad)), True)
+             for b in B]
+    return losses, [w.data for w in W], [b.data for b in B]

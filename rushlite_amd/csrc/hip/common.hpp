@@ -1,0 +1,106 @@
+// Internal helpers shared by the HIP translation units of liblmp_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "lmp_hip.h"
+
+namespace lmp_hip {
+
+// Thread-local message behind lmp_rt_last_error().
+void set_error(const std::string& msg);
+int fail(int status, const std::string& msg);
+
+// Runtime state of the library: one device, one in-order stream.
+struct Runtime {
+  int device = -1;
+  hipStream_t stream = nullptr;
+  int cu_count = 0;
+  int max_threads_per_cu = 2048;
+  size_t lds_per_cu = 0;
+};
+
+// Initialise lazily on device 0 when a kernel entry runs before lmp_rt_init.
+// Returns nullptr (with the error set) when no device is usable.
+Runtime* runtime();
+
+// Scratch allocation for kernels that need a workspace (split-K partials,
+// two-pass reductions).  Memory comes from the pool and is returned to it
+// by the matching release; ordering on the single stream makes reuse safe.
+void* scratch_alloc(size_t bytes);
+void scratch_free(void* ptr);
+
+inline size_t dtype_size(int dtype) {
+  switch (dtype) {
+    case LMP_BOOL: return 1;
+    case LMP_INT16: return 2;
+    case LMP_INT32: return 4;
+    case LMP_INT64: return 8;
+    case LMP_FLOAT32: return 4;
+    case LMP_FLOAT64: return 8;
+    default: return 0;
+  }
+}
+
+inline const char* dtype_name(int dtype) {
+  switch (dtype) {
+    case LMP_BOOL: return "Bool";
+    case LMP_INT16: return "Int16";
+    case LMP_INT32: return "Int32";
+    case LMP_INT64: return "Int64";
+    case LMP_FLOAT32: return "Float32";
+    case LMP_FLOAT64: return "Float64";
+    default: return "Unknown";
+  }
+}
+
+// Magic-number unsigned 32-bit division (Granlund & Montgomery, "Division by
+// Invariant Integers using Multiplication", PLDI 1994): for d >= 1,
+// n / d == (umulhi(n, m) + n) >> s with s = ceil(log2 d) and
+// m = floor(2^32 * (2^s - d) / d) + 1, exact for all n < 2^32.
+struct FastDiv {
+  uint32_t d = 1, m = 0, s = 0;
+  FastDiv() = default;
+  explicit FastDiv(uint32_t divisor) : d(divisor) {
+    s = 0;
+    while ((uint64_t(1) << s) < divisor) ++s;
+    m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << s) - divisor)) /
+                     divisor + 1);
+  }
+  __host__ __device__ __forceinline__ uint32_t div(uint32_t n) const {
+#if defined(__HIP_DEVICE_COMPILE__)
+    uint32_t hi = __umulhi(n, m);
+#else
+    uint32_t hi = uint32_t((uint64_t(n) * m) >> 32);
+#endif
+    return uint32_t((uint64_t(hi) + n) >> s);
+  }
+};
+
+#define LMP_HIP_TRY(expr)                                                   \
+  do {                                                                      \
+    hipError_t _e = (expr);                                                 \
+    if (_e != hipSuccess)                                                   \
+      return ::lmp_hip::fail(LMP_ERR_RUNTIME,                               \
+                             std::string(#expr) + ": " + hipGetErrorString(_e)); \
+  } while (0)
+
+// Check the launch that was just issued.
+#define LMP_LAUNCH_CHECK(name)                                              \
+  do {                                                                      \
+    hipError_t _e = hipGetLastError();                                      \
+    if (_e != hipSuccess)                                                   \
+      return ::lmp_hip::fail(LMP_ERR_RUNTIME,                               \
+                             std::string("launch of ") + (name) + ": " +    \
+                                 hipGetErrorString(_e));                    \
+  } while (0)
+
+#define LMP_RUNTIME_OR_FAIL(rt)                                             \
+  ::lmp_hip::Runtime* rt = ::lmp_hip::runtime();                            \
+  if (!rt) return LMP_ERR_RUNTIME
+
+}  // namespace lmp_hip

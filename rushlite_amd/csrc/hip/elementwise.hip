@@ -1,0 +1,531 @@
+// Elementwise kernels: broadcast binary, unary, fill, cast, add-in-place.
+//
+// fp32 fast path.  Every binary problem is first coalesced on the host into
+// the fewest dimensions (merging dims over which both operands are laid out
+// contiguously, or both broadcast).  Almost every real case then becomes a
+// 2-D problem out[R, C] where each operand has an outer (row) stride and an
+// inner stride of 1 (contiguous) or 0 (broadcast along the row): same-shape
+// ops are R = 1, `[M,N] + [M,1]` has b's inner stride 0, `[M,N] + [N]` has b's
+// outer stride 0, `x + scalar` has both 0.  One kernel template covers all of
+// them with 128-bit loads and nontemporal 128-bit stores, each lane handling
+// four float4 per grid-stride step so a wave keeps 4 KiB of loads in flight.
+// Row/column indices come from a magic-number divide, not a 64-bit div/mod per
+// element (the reference's CUDAOffsetUtil::get, offset_util.cu:32-55).
+// Everything else (rank >= 3 after coalescing, misaligned views, other
+// dtypes) runs a generic scalar kernel with per-dimension magic division.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <string>
+
+#include "common.hpp"
+#include "ops.hpp"
+
+namespace lmp_hip {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+
+// ------------------------------------------------------------ shape helpers
+
+struct Coalesced {
+  int nd = 0;                 // dims kept, innermost first
+  int64_t shape[LMP_MAX_DIMS];
+  int64_t sa[LMP_MAX_DIMS];
+  int64_t sb[LMP_MAX_DIMS];
+};
+
+// Drop size-1 dims and merge neighbours that both operands traverse with one
+// linear stride.  Output order: innermost first.
+Coalesced coalesce(const lmp_bcast& d) {
+  Coalesced c;
+  for (int i = d.ndim - 1; i >= 0; --i) {
+    const int64_t n = d.shape[i];
+    if (n == 1) continue;
+    if (c.nd > 0) {
+      const int j = c.nd - 1;
+      if (d.stride_a[i] == c.sa[j] * c.shape[j] &&
+          d.stride_b[i] == c.sb[j] * c.shape[j]) {
+        c.shape[j] *= n;
+        continue;
+      }
+    }
+    c.shape[c.nd] = n;
+    c.sa[c.nd] = d.stride_a[i];
+    c.sb[c.nd] = d.stride_b[i];
+    ++c.nd;
+  }
+  return c;
+}
+
+int grid_for(int64_t work_items, int per_block) {
+  Runtime* rt = runtime();
+  const int64_t cap = int64_t(rt ? rt->cu_count : 256) * 16;
+  int64_t g = (work_items + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  return static_cast<int>(std::min(g, cap));
+}
+
+bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// ------------------------------------------------------------ fp32 2-D path
+
+// out[r, c] = op(a[r*a_row + c*a_in], b[r*b_row + c*b_in]) with a_in, b_in
+// in {0, 1} fixed at compile time; work item v is one float4 of the output.
+template <int OP, bool A_IN, bool B_IN, bool ROWS>
+__global__ __launch_bounds__(kBlock) void bin2d_f32(
+    float* __restrict__ out, const float* __restrict__ a,
+    const float* __restrict__ b, uint32_t nvec, FastDiv cols4, int64_t a_row,
+    int64_t b_row, float lo, float hi) {
+  const uint32_t stride = gridDim.x * kBlock;
+  uint32_t v = blockIdx.x * kBlock + threadIdx.x;
+  for (; v < nvec; v += stride * kUnroll) {
+    v4f xa[kUnroll], xb[kUnroll];
+    uint32_t idx[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      uint32_t w = v + u * stride;
+      idx[u] = w;
+      if (w >= nvec) w = v;  // keep the load in bounds; result is discarded
+      uint32_t r = ROWS ? cols4.div(w) : 0;
+      uint32_t c4 = w - r * cols4.d;
+      const int64_t ca = A_IN ? int64_t(c4) * 4 : 0;
+      const int64_t cb = B_IN ? int64_t(c4) * 4 : 0;
+      const float* pa = a + int64_t(r) * a_row + ca;
+      const float* pb = b + int64_t(r) * b_row + cb;
+      if constexpr (A_IN) xa[u] = *reinterpret_cast<const v4f*>(pa);
+      else xa[u] = v4f(*pa);
+      if constexpr (B_IN) xb[u] = *reinterpret_cast<const v4f*>(pb);
+      else xb[u] = v4f(*pb);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (idx[u] < nvec) {
+        v4f o;
+        o.x = binary_apply<OP, float>(xa[u].x, xb[u].x, lo, hi);
+        o.y = binary_apply<OP, float>(xa[u].y, xb[u].y, lo, hi);
+        o.z = binary_apply<OP, float>(xa[u].z, xb[u].z, lo, hi);
+        o.w = binary_apply<OP, float>(xa[u].w, xb[u].w, lo, hi);
+        __builtin_nontemporal_store(o, reinterpret_cast<v4f*>(out) + idx[u]);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ generic path
+
+struct NdDesc {
+  int nd;                      // innermost first
+  FastDiv div[LMP_MAX_DIMS];   // extents (as 32-bit magic dividers)
+  int64_t sa[LMP_MAX_DIMS];
+  int64_t sb[LMP_MAX_DIMS];
+};
+
+template <int OP, typename T>
+__global__ __launch_bounds__(kBlock) void bin_nd(T* __restrict__ out,
+                                                 const T* __restrict__ a,
+                                                 const T* __restrict__ b,
+                                                 uint64_t n, NdDesc d, T lo,
+                                                 T hi) {
+  const uint64_t stride = uint64_t(gridDim.x) * kBlock;
+  for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n;
+       i += stride) {
+    // Each extent is < 2^32 and every per-dim remainder fits 32 bits; the
+    // running quotient may not, so peel the innermost dims with 64-bit math
+    // only when the flat index itself exceeds 32 bits.
+    uint64_t rest = i;
+    int64_t oa = 0, ob = 0;
+    for (int k = 0; k < d.nd; ++k) {
+      uint64_t q;
+      if (rest <= 0xffffffffull) q = d.div[k].div(uint32_t(rest));
+      else q = rest / d.div[k].d;
+      const uint64_t coord = rest - q * d.div[k].d;
+      oa += int64_t(coord) * d.sa[k];
+      ob += int64_t(coord) * d.sb[k];
+      rest = q;
+    }
+    out[i] = binary_apply<OP, T>(a[oa], b[ob], lo, hi);
+  }
+}
+
+template <int OP, typename T>
+int launch_bin_nd(T* out, const T* a, const T* b, const Coalesced& c,
+                  double p0, double p1) {
+  LMP_RUNTIME_OR_FAIL(rt);
+  NdDesc d{};
+  d.nd = c.nd;
+  uint64_t n = 1;
+  for (int k = 0; k < c.nd; ++k) {
+    if (c.shape[k] > 0xffffffffll)
+      return fail(LMP_ERR_UNSUPPORTED, "binary: extent above 2^32");
+    d.div[k] = FastDiv(uint32_t(c.shape[k]));
+    d.sa[k] = c.sa[k];
+    d.sb[k] = c.sb[k];
+    n *= uint64_t(c.shape[k]);
+  }
+  if (n == 0) return LMP_OK;
+  const int grid = grid_for(int64_t(std::min<uint64_t>(n, 1ull << 40)), kBlock);
+  hipLaunchKernelGGL((bin_nd<OP, T>), dim3(grid), dim3(kBlock), 0, rt->stream,
+                     out, a, b, n, d, static_cast<T>(p0), static_cast<T>(p1));
+  LMP_LAUNCH_CHECK("bin_nd");
+  return LMP_OK;
+}
+
+template <int OP>
+int launch_bin_f32(float* out, const float* a, const float* b,
+                   const Coalesced& c, double p0, double p1) {
+  LMP_RUNTIME_OR_FAIL(rt);
+  const float lo = static_cast<float>(p0), hi = static_cast<float>(p1);
+  if (c.nd == 0) {  // a single element
+    Coalesced one = c;
+    return launch_bin_nd<OP, float>(out, a, b, one, p0, p1);
+  }
+  if (c.nd <= 2) {
+    const int64_t cols = c.shape[0];
+    const int64_t rows = c.nd == 2 ? c.shape[1] : 1;
+    const int64_t a_in = c.sa[0], b_in = c.sb[0];
+    const int64_t a_row = c.nd == 2 ? c.sa[1] : 0;
+    const int64_t b_row = c.nd == 2 ? c.sb[1] : 0;
+    const bool inner_ok = (a_in == 0 || a_in == 1) && (b_in == 0 || b_in == 1);
+    const bool vec_ok =
+        inner_ok && cols % 4 == 0 && aligned16(out) &&
+        (a_in == 0 || (aligned16(a) && a_row % 4 == 0)) &&
+        (b_in == 0 || (aligned16(b) && b_row % 4 == 0)) &&
+        rows * (cols / 4) <= 0xffffffffll && cols / 4 <= 0xffffffffll;
+    if (vec_ok) {
+      const uint32_t nvec = uint32_t(rows * (cols / 4));
+      const FastDiv cols4(uint32_t(cols / 4));
+      const int grid = grid_for(nvec, kBlock * kUnroll);
+      const bool rws = rows > 1;
+#define LMP_BIN2D(AI, BI, RW)                                                  \
+  hipLaunchKernelGGL((bin2d_f32<OP, AI, BI, RW>), dim3(grid), dim3(kBlock), 0, \
+                     rt->stream, out, a, b, nvec, cols4, a_row, b_row, lo, hi)
+      if (a_in == 1 && b_in == 1) {
+        if (rws) LMP_BIN2D(true, true, true); else LMP_BIN2D(true, true, false);
+      } else if (a_in == 1) {
+        if (rws) LMP_BIN2D(true, false, true); else LMP_BIN2D(true, false, false);
+      } else if (b_in == 1) {
+        if (rws) LMP_BIN2D(false, true, true); else LMP_BIN2D(false, true, false);
+      } else {
+        return launch_bin_nd<OP, float>(out, a, b, c, p0, p1);
+      }
+#undef LMP_BIN2D
+      LMP_LAUNCH_CHECK("bin2d_f32");
+      return LMP_OK;
+    }
+  }
+  return launch_bin_nd<OP, float>(out, a, b, c, p0, p1);
+}
+
+template <typename T>
+int dispatch_bin(int op, T* out, const T* a, const T* b, const Coalesced& c,
+                 double p0, double p1) {
+  switch (op) {
+#define LMP_CASE(OPV)                                                     \
+  case OPV:                                                               \
+    if constexpr (std::is_same_v<T, float>)                               \
+      return launch_bin_f32<OPV>(out, a, b, c, p0, p1);                    \
+    else                                                                  \
+      return launch_bin_nd<OPV, T>(out, a, b, c, p0, p1);
+    LMP_CASE(LMP_BIN_ADD)
+    LMP_CASE(LMP_BIN_SUB)
+    LMP_CASE(LMP_BIN_MUL)
+    LMP_CASE(LMP_BIN_DIV)
+    LMP_CASE(LMP_BIN_POW)
+    LMP_CASE(LMP_BIN_EQ)
+    LMP_CASE(LMP_BIN_NE)
+    LMP_CASE(LMP_BIN_GE)
+    LMP_CASE(LMP_BIN_LE)
+    LMP_CASE(LMP_BIN_GT)
+    LMP_CASE(LMP_BIN_LT)
+    LMP_CASE(LMP_BIN_ABS_BACKWARD)
+    LMP_CASE(LMP_BIN_CLAMP_BACKWARD)
+#undef LMP_CASE
+    default:
+      return fail(LMP_ERR_INVALID, "lmp_k_binary: unknown op " + std::to_string(op));
+  }
+}
+
+// ------------------------------------------------------------------ unary
+
+template <int OP>
+__global__ __launch_bounds__(kBlock) void unary_f32_vec(
+    float* __restrict__ out, const float* __restrict__ in, uint32_t nvec,
+    float lo, float hi) {
+  const uint32_t stride = gridDim.x * kBlock;
+  for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nvec;
+       v += stride * kUnroll) {
+    v4f x[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      uint32_t w = v + u * stride;
+      x[u] = reinterpret_cast<const v4f*>(in)[w < nvec ? w : v];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      uint32_t w = v + u * stride;
+      if (w < nvec) {
+        v4f o;
+        o.x = unary_apply<OP, float>(x[u].x, lo, hi);
+        o.y = unary_apply<OP, float>(x[u].y, lo, hi);
+        o.z = unary_apply<OP, float>(x[u].z, lo, hi);
+        o.w = unary_apply<OP, float>(x[u].w, lo, hi);
+        __builtin_nontemporal_store(o, reinterpret_cast<v4f*>(out) + w);
+      }
+    }
+  }
+}
+
+template <int OP, typename T>
+__global__ __launch_bounds__(kBlock) void unary_scalar(T* __restrict__ out,
+                                                       const T* __restrict__ in,
+                                                       uint64_t n, T lo, T hi) {
+  const uint64_t stride = uint64_t(gridDim.x) * kBlock;
+  for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n;
+       i += stride)
+    out[i] = unary_apply<OP, T>(in[i], lo, hi);
+}
+
+template <int OP, typename T>
+int launch_unary(T* out, const T* in, size_t n, double p0, double p1) {
+  LMP_RUNTIME_OR_FAIL(rt);
+  if (n == 0) return LMP_OK;
+  if constexpr (std::is_same_v<T, float>) {
+    if (n % 4 == 0 && aligned16(out) && aligned16(in) && n / 4 <= 0xffffffffull) {
+      const uint32_t nvec = uint32_t(n / 4);
+      const int grid = grid_for(nvec, kBlock * kUnroll);
+      hipLaunchKernelGGL((unary_f32_vec<OP>), dim3(grid), dim3(kBlock), 0,
+                         rt->stream, out, in, nvec, static_cast<float>(p0),
+                         static_cast<float>(p1));
+      LMP_LAUNCH_CHECK("unary_f32_vec");
+      return LMP_OK;
+    }
+  }
+  const int grid = grid_for(int64_t(std::min<size_t>(n, 1ull << 40)), kBlock);
+  hipLaunchKernelGGL((unary_scalar<OP, T>), dim3(grid), dim3(kBlock), 0,
+                     rt->stream, out, in, uint64_t(n), static_cast<T>(p0),
+                     static_cast<T>(p1));
+  LMP_LAUNCH_CHECK("unary_scalar");
+  return LMP_OK;
+}
+
+template <typename T>
+int dispatch_unary(int op, T* out, const T* in, size_t n, double p0, double p1) {
+  switch (op) {
+#define LMP_CASE(OPV) \
+  case OPV:           \
+    return launch_unary<OPV, T>(out, in, n, p0, p1);
+    LMP_CASE(LMP_UN_NEG)
+    LMP_CASE(LMP_UN_EXP)
+    LMP_CASE(LMP_UN_LOG)
+    LMP_CASE(LMP_UN_SQRT)
+    LMP_CASE(LMP_UN_ABS)
+    LMP_CASE(LMP_UN_SIN)
+    LMP_CASE(LMP_UN_COS)
+    LMP_CASE(LMP_UN_TAN)
+    LMP_CASE(LMP_UN_CLAMP)
+#undef LMP_CASE
+    default:
+      return fail(LMP_ERR_INVALID, "lmp_k_unary: unknown op " + std::to_string(op));
+  }
+}
+
+// ------------------------------------------------------ fill / cast / add
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void fill_scalar(T* __restrict__ out,
+                                                      uint64_t n, T value) {
+  const uint64_t stride = uint64_t(gridDim.x) * kBlock;
+  for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n;
+       i += stride)
+    out[i] = value;
+}
+
+__global__ __launch_bounds__(kBlock) void fill_f32_vec(float* __restrict__ out,
+                                                       uint32_t nvec,
+                                                       float value) {
+  const uint32_t stride = gridDim.x * kBlock;
+  const v4f val(value);
+  for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride)
+    __builtin_nontemporal_store(val, reinterpret_cast<v4f*>(out) + v);
+}
+
+template <typename S, typename D>
+__global__ __launch_bounds__(kBlock) void cast_kernel(D* __restrict__ dst,
+                                                      const S* __restrict__ src,
+                                                      uint64_t n) {
+  const uint64_t stride = uint64_t(gridDim.x) * kBlock;
+  for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n;
+       i += stride)
+    dst[i] = static_cast<D>(src[i]);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void add_inplace_scalar(
+    T* __restrict__ dst, const T* __restrict__ src, uint64_t n) {
+  const uint64_t stride = uint64_t(gridDim.x) * kBlock;
+  for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n;
+       i += stride)
+    dst[i] = dst[i] + src[i];
+}
+
+__global__ __launch_bounds__(kBlock) void add_inplace_f32_vec(
+    float* __restrict__ dst, const float* __restrict__ src, uint32_t nvec) {
+  const uint32_t stride = gridDim.x * kBlock;
+  for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nvec;
+       v += stride * kUnroll) {
+    v4f x[kUnroll], y[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      uint32_t w = v + u * stride;
+      w = w < nvec ? w : v;
+      x[u] = reinterpret_cast<const v4f*>(dst)[w];
+      y[u] = reinterpret_cast<const v4f*>(src)[w];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      uint32_t w = v + u * stride;
+      if (w < nvec) reinterpret_cast<v4f*>(dst)[w] = x[u] + y[u];
+    }
+  }
+}
+
+template <typename F>
+int with_dtype(int dtype, F&& f) {
+  switch (dtype) {
+    case LMP_BOOL: return f(static_cast<bool*>(nullptr));
+    case LMP_INT16: return f(static_cast<int16_t*>(nullptr));
+    case LMP_INT32: return f(static_cast<int32_t*>(nullptr));
+    case LMP_INT64: return f(static_cast<int64_t*>(nullptr));
+    case LMP_FLOAT32: return f(static_cast<float*>(nullptr));
+    case LMP_FLOAT64: return f(static_cast<double*>(nullptr));
+    default:
+      return fail(LMP_ERR_INVALID, "unknown dtype " + std::to_string(dtype));
+  }
+}
+
+}  // namespace
+}  // namespace lmp_hip
+
+using namespace lmp_hip;
+
+extern "C" {
+
+int lmp_k_binary(int op, int dtype, void* out, const void* a, const void* b,
+                 const lmp_bcast* desc, double p0, double p1) {
+  if (!desc) return fail(LMP_ERR_INVALID, "lmp_k_binary: null descriptor");
+  if (desc->ndim < 0 || desc->ndim > LMP_MAX_DIMS)
+    return fail(LMP_ERR_INVALID, "lmp_k_binary: ndim out of range");
+  int64_t n = 1;
+  for (int i = 0; i < desc->ndim; ++i) {
+    if (desc->shape[i] < 0) return fail(LMP_ERR_INVALID, "negative extent");
+    n *= desc->shape[i];
+  }
+  if (n == 0) return LMP_OK;
+  if (!out || !a || !b) return fail(LMP_ERR_INVALID, "lmp_k_binary: null buffer");
+  const Coalesced c = coalesce(*desc);
+  return with_dtype(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    if constexpr (std::is_same_v<T, bool>) {
+      if (op == LMP_BIN_POW || op == LMP_BIN_DIV)
+        return fail(LMP_ERR_UNSUPPORTED, "pow/div on Bool tensors");
+    }
+    return dispatch_bin<T>(op, static_cast<T*>(out), static_cast<const T*>(a),
+                           static_cast<const T*>(b), c, p0, p1);
+  });
+}
+
+int lmp_k_unary(int op, int dtype, void* out, const void* in, size_t n,
+                double p0, double p1) {
+  if (n == 0) return LMP_OK;
+  if (!out || !in) return fail(LMP_ERR_INVALID, "lmp_k_unary: null buffer");
+  return with_dtype(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    if constexpr (std::is_same_v<T, bool>) {
+      return fail(LMP_ERR_UNSUPPORTED, "unary ops on Bool tensors");
+    } else {
+      return dispatch_unary<T>(op, static_cast<T*>(out), static_cast<const T*>(in),
+                               n, p0, p1);
+    }
+  });
+}
+
+int lmp_k_fill(int dtype, void* out, size_t n, double value) {
+  if (n == 0) return LMP_OK;
+  if (!out) return fail(LMP_ERR_INVALID, "lmp_k_fill: null buffer");
+  LMP_RUNTIME_OR_FAIL(rt);
+  return with_dtype(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    if constexpr (std::is_same_v<T, float>) {
+      if (n % 4 == 0 && aligned16(out) && n / 4 <= 0xffffffffull) {
+        const uint32_t nvec = uint32_t(n / 4);
+        hipLaunchKernelGGL(fill_f32_vec, dim3(grid_for(nvec, kBlock)),
+                           dim3(kBlock), 0, rt->stream, static_cast<float*>(out),
+                           nvec, static_cast<float>(value));
+        LMP_LAUNCH_CHECK("fill_f32_vec");
+        return LMP_OK;
+      }
+    }
+    hipLaunchKernelGGL((fill_scalar<T>),
+                       dim3(grid_for(int64_t(std::min<size_t>(n, 1ull << 40)), kBlock)),
+                       dim3(kBlock), 0, rt->stream, static_cast<T*>(out),
+                       uint64_t(n), static_cast<T>(value));
+    LMP_LAUNCH_CHECK("fill_scalar");
+    return LMP_OK;
+  });
+}
+
+int lmp_k_cast(int src_dtype, int dst_dtype, void* dst, const void* src,
+               size_t n) {
+  if (n == 0) return LMP_OK;
+  if (!dst || !src) return fail(LMP_ERR_INVALID, "lmp_k_cast: null buffer");
+  LMP_RUNTIME_OR_FAIL(rt);
+  if (src_dtype == dst_dtype)
+    return lmp_rt_memcpy_d2d(dst, src, n * dtype_size(src_dtype));
+  const int grid = grid_for(int64_t(std::min<size_t>(n, 1ull << 40)), kBlock);
+  return with_dtype(src_dtype, [&](auto* stag) -> int {
+    using S = std::remove_pointer_t<decltype(stag)>;
+    return with_dtype(dst_dtype, [&](auto* dtag) -> int {
+      using D = std::remove_pointer_t<decltype(dtag)>;
+      hipLaunchKernelGGL((cast_kernel<S, D>), dim3(grid), dim3(kBlock), 0,
+                         rt->stream, static_cast<D*>(dst),
+                         static_cast<const S*>(src), uint64_t(n));
+      LMP_LAUNCH_CHECK("cast_kernel");
+      return LMP_OK;
+    });
+  });
+}
+
+int lmp_k_add_inplace(int dtype, void* dst, const void* src, size_t n) {
+  if (n == 0) return LMP_OK;
+  if (!dst || !src) return fail(LMP_ERR_INVALID, "lmp_k_add_inplace: null buffer");
+  LMP_RUNTIME_OR_FAIL(rt);
+  return with_dtype(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    if constexpr (std::is_same_v<T, float>) {
+      if (n % 4 == 0 && aligned16(dst) && aligned16(src) && n / 4 <= 0xffffffffull) {
+        const uint32_t nvec = uint32_t(n / 4);
+        hipLaunchKernelGGL(add_inplace_f32_vec,
+                           dim3(grid_for(nvec, kBlock * kUnroll)), dim3(kBlock),
+                           0, rt->stream, static_cast<float*>(dst),
+                           static_cast<const float*>(src), nvec);
+        LMP_LAUNCH_CHECK("add_inplace_f32_vec");
+        return LMP_OK;
+      }
+    }
+    hipLaunchKernelGGL((add_inplace_scalar<T>),
+                       dim3(grid_for(int64_t(std::min<size_t>(n, 1ull << 40)), kBlock)),
+                       dim3(kBlock), 0, rt->stream, static_cast<T*>(dst),
+                       static_cast<const T*>(src), uint64_t(n));
+    LMP_LAUNCH_CHECK("add_inplace_scalar");
+    return LMP_OK;
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,434 @@
+// fp32 GEMM on CDNA4 matrix cores (v_mfma_f32_32x32x2_f32) and transpose.
+//
+// C[m,n] (+)= sum_k opA(A)[m,k] * opB(B)[k,n], row-major, any of the four
+// operand orientations, so Linear's backward (dY*W^T and X^T*dY) needs no
+// materialised transpose (the reference transposes then multiplies,
+// functions/matrix_ops.cpp:8-24, with a SIMT kernel, matrix.cu:21-145).
+//
+// Tiling.  A workgroup of 4 waves owns a BM x BN tile of C; the waves form a
+// WGM x WGN grid and each wave owns TM x TN blocks of 32x32, accumulated by
+// one MFMA chain per block.  K advances BK = 32 at a time through two LDS
+// buffers: the next tile's global loads are issued into registers before the
+// MFMAs on the current tile and written to the other LDS buffer afterwards,
+// so one barrier per K step suffices.
+//
+// MFMA operand layout.  For 32x32x2 a lane l supplies A[i][kk] and B[kk][j]
+// with i = j = l % 32 and kk = l / 32.  Within a BK tile, MFMA step s pairs
+// k = s (lanes 0-31) with k = s + BK/2 (lanes 32-63), so a lane's 16 A values
+// (and B values) for one tile are contiguous in k: a row-major-in-k LDS tile
+// is read with four 128-bit LDS loads per 32-row block.  Sum order over k is a
+// permutation of the serial order, which the 1e-4 tolerance admits.
+// Accumulator layout: register r of a lane holds row 8*(r/4) + 4*(l/32) + r%4,
+// column l % 32.
+//
+// Grid.  Workgroup ids are first regrouped so each of the 8 XCDs (which
+// receive ids round-robin) processes a contiguous run of tiles, then tiles
+// are walked in groups of 8 tile-rows so neighbours share A and B panels in
+// that XCD's L2.  When the tile count cannot fill the chip, K is split over
+// blockIdx.z into fp32 partials folded in split order by a second kernel.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <string>
+
+#include "common.hpp"
+
+namespace lmp_hip {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kBK = 32;
+constexpr int kPad = 4;
+
+template <int WGM_, int WGN_, int TM_, int TN_>
+struct Cfg {
+  static constexpr int WGM = WGM_, WGN = WGN_, TM = TM_, TN = TN_;
+  static constexpr int BM = WGM * TM * 32;
+  static constexpr int BN = WGN * TN * 32;
+  static_assert(WGM * WGN == 4, "four waves per workgroup");
+};
+
+using CfgLarge = Cfg<2, 2, 2, 2>;   // 128 x 128
+using CfgSkinny = Cfg<1, 4, 1, 2>;  // 32 x 256
+
+template <class C, bool TA>
+constexpr int a_lds_floats() {
+  return TA ? kBK * (C::BM + kPad) : C::BM * (kBK + kPad);
+}
+template <class C, bool TB>
+constexpr int b_lds_floats() {
+  return TB ? C::BN * (kBK + kPad) : kBK * (C::BN + kPad);
+}
+
+struct GemmArgs {
+  const float* a;
+  const float* b;
+  float* c;        // final output (split == 1) or partial buffer base
+  int m, n, k;
+  int lda, ldb, ldc;
+  int tiles_m, tiles_n;
+  int k_tiles_per_split;
+  int accumulate;  // only honoured when writing the final output
+};
+
+// Load one [rows x cols] panel of a row-major matrix (leading dim ld) starting
+// at (r0, c0) into registers as float4, bounds-checked against (R, Cn).
+// VEC requires ld % 4 == 0, 16-byte base alignment and Cn % 4 == 0, so each
+// float4 is either fully inside or fully outside.
+template <int ROWS, int COLS, bool VEC>
+struct Panel {
+  static constexpr int kVec = ROWS * COLS / 4;
+  static constexpr int kPer = kVec / kThreads;
+  static_assert(kVec % kThreads == 0, "panel must split evenly over threads");
+  v4f v[kPer];
+
+  __device__ __forceinline__ void load(const float* __restrict__ p, int ld,
+                                       int r0, int c0, int R, int Cn) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int f = threadIdx.x + j * kThreads;
+      const int r = f / (COLS / 4);
+      const int c = (f % (COLS / 4)) * 4;
+      const int gr = r0 + r, gc = c0 + c;
+      if constexpr (VEC) {
+        if (gr < R && gc < Cn)
+          v[j] = *reinterpret_cast<const v4f*>(p + int64_t(gr) * ld + gc);
+        else
+          v[j] = v4f(0.0f);
+      } else {
+        const float* q = p + int64_t(gr) * ld + gc;
+        v[j].x = (gr < R && gc + 0 < Cn) ? q[0] : 0.0f;
+        v[j].y = (gr < R && gc + 1 < Cn) ? q[1] : 0.0f;
+        v[j].z = (gr < R && gc + 2 < Cn) ? q[2] : 0.0f;
+        v[j].w = (gr < R && gc + 3 < Cn) ? q[3] : 0.0f;
+      }
+    }
+  }
+  // Store to an LDS array with row pitch COLS + kPad.
+  __device__ __forceinline__ void store(float* lds) const {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int f = threadIdx.x + j * kThreads;
+      const int r = f / (COLS / 4);
+      const int c = (f % (COLS / 4)) * 4;
+      *reinterpret_cast<v4f*>(lds + r * (COLS + kPad) + c) = v[j];
+    }
+  }
+};
+
+template <class C, bool TA, bool TB, bool VEC>
+__global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma(GemmArgs g) {
+  constexpr int BM = C::BM, BN = C::BN;
+  constexpr int HK = kBK / 2;
+  constexpr int A_SZ = a_lds_floats<C, TA>();
+  constexpr int B_SZ = b_lds_floats<C, TB>();
+  __shared__ __attribute__((aligned(16))) float smem[2 * (A_SZ + B_SZ)];
+
+  // XCD-aware regrouping of the tile id, then grouped tile-row walk.
+  const int ntiles = g.tiles_m * g.tiles_n;
+  int bid = blockIdx.x;
+  if (ntiles % 8 == 0) bid = (bid % 8) * (ntiles / 8) + bid / 8;
+  constexpr int kGroup = 8;
+  const int per_group = kGroup * g.tiles_n;
+  const int group = bid / per_group;
+  const int first_m = group * kGroup;
+  const int gsize = min(g.tiles_m - first_m, kGroup);
+  const int in_group = bid - group * per_group;
+  const int tile_m = first_m + in_group % gsize;
+  const int tile_n = in_group / gsize;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+
+  const int split = blockIdx.z;
+  const int k_tiles = (g.k + kBK - 1) / kBK;
+  const int kt0 = split * g.k_tiles_per_split;
+  const int kt1 = min(k_tiles, kt0 + g.k_tiles_per_split);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
+  const int li = lane & 31, lh = lane >> 5;
+
+  // A panel: !TA -> [BM rows of m] x [BK cols of k]; TA -> [BK rows] x [BM cols]
+  using PA = std::conditional_t<TA, Panel<kBK, BM, VEC>, Panel<BM, kBK, VEC>>;
+  using PB = std::conditional_t<TB, Panel<BN, kBK, VEC>, Panel<kBK, BN, VEC>>;
+  PA pa;
+  PB pb;
+
+  auto load_tile = [&](int kt) {
+    const int k0 = kt * kBK;
+    if constexpr (TA) pa.load(g.a, g.lda, k0, m0, g.k, g.m);
+    else pa.load(g.a, g.lda, m0, k0, g.m, g.k);
+    if constexpr (TB) pb.load(g.b, g.ldb, n0, k0, g.n, g.k);
+    else pb.load(g.b, g.ldb, k0, n0, g.k, g.n);
+  };
+
+  v16f acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) acc[i][j] = v16f(0.0f);
+
+  if (kt0 < kt1) {
+    load_tile(kt0);
+    pa.store(smem);
+    pb.store(smem + A_SZ);
+  }
+  __syncthreads();
+
+  for (int kt = kt0; kt < kt1; ++kt) {
+    const int cur = (kt - kt0) & 1;
+    const float* As = smem + cur * (A_SZ + B_SZ);
+    const float* Bs = As + A_SZ;
+    const bool more = kt + 1 < kt1;
+    if (more) load_tile(kt + 1);
+
+    // Fragments: a[i][s] = A_tile[row_i][s + lh*HK], b[j][s] likewise.
+    float af[C::TM][HK], bf[C::TN][HK];
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+      const int row = (wm * C::TM + i) * 32 + li;
+      if constexpr (!TA) {
+        const float* src = As + row * (kBK + kPad) + lh * HK;
+#pragma unroll
+        for (int q = 0; q < HK / 4; ++q) {
+          const v4f t = *reinterpret_cast<const v4f*>(src + 4 * q);
+          af[i][4 * q + 0] = t.x;
+          af[i][4 * q + 1] = t.y;
+          af[i][4 * q + 2] = t.z;
+          af[i][4 * q + 3] = t.w;
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < HK; ++s) af[i][s] = As[(s + lh * HK) * (BM + kPad) + row];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+      const int col = (wn * C::TN + j) * 32 + li;
+      if constexpr (TB) {
+        const float* src = Bs + col * (kBK + kPad) + lh * HK;
+#pragma unroll
+        for (int q = 0; q < HK / 4; ++q) {
+          const v4f t = *reinterpret_cast<const v4f*>(src + 4 * q);
+          bf[j][4 * q + 0] = t.x;
+          bf[j][4 * q + 1] = t.y;
+          bf[j][4 * q + 2] = t.z;
+          bf[j][4 * q + 3] = t.w;
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < HK; ++s) bf[j][s] = Bs[(s + lh * HK) * (BN + kPad) + col];
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < HK; ++s)
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s],
+                                                           acc[i][j], 0, 0, 0);
+
+    if (more) {
+      float* nxt = smem + (cur ^ 1) * (A_SZ + B_SZ);
+      pa.store(nxt);
+      pb.store(nxt + A_SZ);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue.
+  const bool partial = gridDim.z > 1;
+  float* out = g.c;
+  int64_t ld = g.ldc;
+  if (partial) {
+    out = g.c + int64_t(split) * g.m * g.n;
+    ld = g.n;
+  }
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+      const int col = n0 + (wn * C::TN + j) * 32 + li;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + (wm * C::TM + i) * 32 + (r / 4) * 8 + lh * 4 + (r % 4);
+        if (row < g.m && col < g.n) {
+          float* p = out + int64_t(row) * ld + col;
+          const float v = acc[i][j][r];
+          if (!partial && g.accumulate) *p = *p + v;
+          else *p = v;
+        }
+      }
+    }
+  }
+}
+
+// c[row, col] (+)= sum over splits of part[s, row, col], in split order.
+__global__ __launch_bounds__(256) void fold_splits(float* __restrict__ c,
+                                                   const float* __restrict__ part,
+                                                   int m, int n, int ldc,
+                                                   int splits, int accumulate) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t mn = int64_t(m) * n;
+  if (i >= mn) return;
+  const int row = int(i / n), col = int(i - int64_t(row) * n);
+  float acc = part[i];
+  for (int s = 1; s < splits; ++s) acc += part[int64_t(s) * mn + i];
+  float* p = c + int64_t(row) * ldc + col;
+  *p = accumulate ? *p + acc : acc;
+}
+
+template <class C, bool TA, bool TB>
+int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec) {
+  g.tiles_m = (g.m + C::BM - 1) / C::BM;
+  g.tiles_n = (g.n + C::BN - 1) / C::BN;
+  const int tiles = g.tiles_m * g.tiles_n;
+  const int k_tiles = (g.k + kBK - 1) / kBK;
+  // Split K when the tiles alone cannot occupy every CU twice; keep at least
+  // four K tiles per split.
+  int splits = 1;
+  const int want = 2 * rt->cu_count;
+  if (tiles < want && k_tiles >= 8)
+    splits = std::min((want + tiles - 1) / tiles, std::max(1, k_tiles / 4));
+  splits = std::max(1, std::min(splits, 64));
+  g.k_tiles_per_split = (k_tiles + splits - 1) / splits;
+  splits = std::max(1, (k_tiles + g.k_tiles_per_split - 1) / g.k_tiles_per_split);
+
+  float* final_c = g.c;
+  float* part = nullptr;
+  if (splits > 1) {
+    part = static_cast<float*>(
+        scratch_alloc(size_t(splits) * size_t(g.m) * size_t(g.n) * sizeof(float)));
+    if (!part) return LMP_ERR_OOM;
+    g.c = part;
+  }
+  const dim3 grid{uint32_t(tiles), 1u, uint32_t(splits)};
+  if (vec)
+    hipLaunchKernelGGL((gemm_f32_mfma<C, TA, TB, true>), grid, dim3(kThreads), 0,
+                       rt->stream, g);
+  else
+    hipLaunchKernelGGL((gemm_f32_mfma<C, TA, TB, false>), grid, dim3(kThreads), 0,
+                       rt->stream, g);
+  LMP_LAUNCH_CHECK("gemm_f32_mfma");
+  if (splits > 1) {
+    const int64_t mn = int64_t(g.m) * g.n;
+    hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
+                       rt->stream, final_c, part, g.m, g.n, g.ldc, splits,
+                       g.accumulate);
+    LMP_LAUNCH_CHECK("fold_splits");
+    scratch_free(part);
+  }
+  return LMP_OK;
+}
+
+template <bool TA, bool TB>
+int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec) {
+  if (g.m <= 64) return launch_gemm_cfg<CfgSkinny, TA, TB>(rt, g, vec);
+  return launch_gemm_cfg<CfgLarge, TA, TB>(rt, g, vec);
+}
+
+bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// ------------------------------------------------------------- transpose
+
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_tiled(T* __restrict__ out,
+                                                       const T* __restrict__ in,
+                                                       int64_t m, int64_t n) {
+  __shared__ T tile[64][65];
+  const int64_t r0 = int64_t(blockIdx.y) * 64, c0 = int64_t(blockIdx.x) * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+#pragma unroll
+  for (int k = 0; k < 64; k += 4) {
+    const int64_t r = r0 + ty + k, c = c0 + tx;
+    if (r < m && c < n) tile[ty + k][tx] = in[r * n + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 64; k += 4) {
+    const int64_t r = c0 + ty + k, c = r0 + tx;  // out is [n, m]
+    if (r < n && c < m) out[r * m + c] = tile[tx][ty + k];
+  }
+}
+
+}  // namespace
+}  // namespace lmp_hip
+
+using namespace lmp_hip;
+
+extern "C" int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n,
+                              size_t k, const float* a, size_t lda,
+                              const float* b, size_t ldb, float* c, size_t ldc,
+                              int accumulate) {
+  if (m == 0 || n == 0) return LMP_OK;
+  if (!c) return fail(LMP_ERR_INVALID, "gemm: null output");
+  if (k == 0) {
+    if (accumulate) return LMP_OK;
+    if (ldc != n) return fail(LMP_ERR_UNSUPPORTED, "gemm: k == 0 with ldc != n");
+    return lmp_k_fill(LMP_FLOAT32, c, m * n, 0.0);
+  }
+  if (!a || !b) return fail(LMP_ERR_INVALID, "gemm: null input");
+  const size_t lim = 0x7fffffff;
+  if (m > lim || n > lim || k > lim || lda > lim || ldb > lim || ldc > lim)
+    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension above 2^31");
+  if ((trans_a ? lda < m : lda < k) || (trans_b ? ldb < k : ldb < n) || ldc < n)
+    return fail(LMP_ERR_INVALID, "gemm: leading dimension too small");
+  LMP_RUNTIME_OR_FAIL(rt);
+  GemmArgs g{};
+  g.a = a;
+  g.b = b;
+  g.c = c;
+  g.m = int(m);
+  g.n = int(n);
+  g.k = int(k);
+  g.lda = int(lda);
+  g.ldb = int(ldb);
+  g.ldc = int(ldc);
+  g.accumulate = accumulate ? 1 : 0;
+  // 128-bit panel loads need 16-byte rows and a contiguous extent that is a
+  // multiple of four.
+  const size_t a_contig = trans_a ? m : k;
+  const size_t b_contig = trans_b ? k : n;
+  const bool vec = lda % 4 == 0 && ldb % 4 == 0 && a_contig % 4 == 0 &&
+                   b_contig % 4 == 0 && aligned16(a) && aligned16(b);
+  if (!trans_a && !trans_b) return launch_gemm<false, false>(rt, g, vec);
+  if (!trans_a && trans_b) return launch_gemm<false, true>(rt, g, vec);
+  if (trans_a && !trans_b) return launch_gemm<true, false>(rt, g, vec);
+  return launch_gemm<true, true>(rt, g, vec);
+}
+
+extern "C" int lmp_k_transpose(int dtype, void* out, const void* in, size_t m,
+                               size_t n) {
+  if (m == 0 || n == 0) return LMP_OK;
+  if (!out || !in) return fail(LMP_ERR_INVALID, "transpose: null buffer");
+  LMP_RUNTIME_OR_FAIL(rt);
+  const uint64_t gx = (n + 63) / 64, gy = (m + 63) / 64;
+  if (gx > 0x7fffffffull || gy > 65535)
+    return fail(LMP_ERR_UNSUPPORTED, "transpose: matrix too large");
+  const dim3 grid{uint32_t(gx), uint32_t(gy), 1u};
+  switch (dtype) {
+#define LMP_CASE(CODE, T)                                                     \
+  case CODE:                                                                  \
+    hipLaunchKernelGGL((transpose_tiled<T>), grid, dim3(256), 0, rt->stream,  \
+                       static_cast<T*>(out), static_cast<const T*>(in),       \
+                       int64_t(m), int64_t(n));                               \
+    LMP_LAUNCH_CHECK("transpose_tiled");                                      \
+    return LMP_OK;
+    LMP_CASE(LMP_BOOL, bool)
+    LMP_CASE(LMP_INT16, int16_t)
+    LMP_CASE(LMP_INT32, int32_t)
+    LMP_CASE(LMP_INT64, int64_t)
+    LMP_CASE(LMP_FLOAT32, float)
+    LMP_CASE(LMP_FLOAT64, double)
+#undef LMP_CASE
+    default:
+      return fail(LMP_ERR_INVALID, "transpose: unknown dtype");
+  }
+}

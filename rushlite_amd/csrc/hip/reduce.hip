@@ -1,0 +1,348 @@
+// Keep-dims reductions over the middle axis of a contiguous [outer, len,
+// inner] view (Lamp3: cpu/reduct.cpp:7-49 for the semantics, reduct.cu:213-260
+// for the CUDA dispatcher this replaces).
+//
+// Row case (inner == 1, e.g. sum/max over dim 1 of [16384,16384]):
+//   long fp32 rows  -> one 256-thread workgroup per row segment, 128-bit
+//                      loads, 16 independent accumulators per lane, wave64
+//                      butterfly (__shfl_xor) then LDS across the 4 waves;
+//                      a row is split over several workgroups only when
+//                      there are too few rows to fill 256 CUs, and the
+//                      partials are folded by a second pass in fixed order.
+//   short rows      -> one wave per row (softmax/loss rows like [512,1000]).
+// Column case (inner > 1, e.g. sum over dim 0, the bias-gradient reduction):
+//   each lane owns four adjacent columns (one float4), a workgroup covers
+//   1024 columns, and the reduced axis is cut into S chunks so the grid has
+//   thousands of workgroups; chunk partials [outer, S, inner] are folded in
+//   chunk order by a second pass.  No atomics: results are deterministic.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <string>
+
+#include "common.hpp"
+#include "ops.hpp"
+
+namespace lmp_hip {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / 64;
+
+template <int OP, typename T>
+__device__ __forceinline__ T wave_reduce(T v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1)
+    v = Reducer<OP, T>::combine(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+template <int OP>
+__device__ __forceinline__ v4f combine4(v4f a, v4f b) {
+  v4f r;
+  r.x = Reducer<OP, float>::combine(a.x, b.x);
+  r.y = Reducer<OP, float>::combine(a.y, b.y);
+  r.z = Reducer<OP, float>::combine(a.z, b.z);
+  r.w = Reducer<OP, float>::combine(a.w, b.w);
+  return r;
+}
+
+// Block (row, part) reduces float4 [part*seg4, min(len4, (part+1)*seg4)) of
+// its row and writes one value to out[row * parts + part].
+template <int OP>
+__global__ __launch_bounds__(kBlock) void row_reduce_f32(
+    float* __restrict__ out, const float* __restrict__ in, uint32_t len4,
+    uint32_t seg4, FastDiv parts) {
+  using R = Reducer<OP, float>;
+  const uint32_t row = parts.div(blockIdx.x);
+  const uint32_t part = blockIdx.x - row * parts.d;
+  const v4f* src = reinterpret_cast<const v4f*>(in) + uint64_t(row) * len4;
+  const uint32_t beg = part * seg4;
+  const uint32_t end = min(len4, beg + seg4);
+  const v4f id = v4f(R::identity());
+  v4f acc0 = id, acc1 = id, acc2 = id, acc3 = id;
+  uint32_t i = beg + threadIdx.x;
+  for (; i + 3 * kBlock < end; i += 4 * kBlock) {
+    v4f x0 = src[i], x1 = src[i + kBlock], x2 = src[i + 2 * kBlock],
+        x3 = src[i + 3 * kBlock];
+    acc0 = combine4<OP>(acc0, x0);
+    acc1 = combine4<OP>(acc1, x1);
+    acc2 = combine4<OP>(acc2, x2);
+    acc3 = combine4<OP>(acc3, x3);
+  }
+  for (; i < end; i += kBlock) acc0 = combine4<OP>(acc0, src[i]);
+  v4f acc = combine4<OP>(combine4<OP>(acc0, acc1), combine4<OP>(acc2, acc3));
+  float v = R::combine(R::combine(acc.x, acc.y), R::combine(acc.z, acc.w));
+  v = wave_reduce<OP, float>(v);
+  __shared__ float lds[kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) lds[wave] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float r = lds[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) r = R::combine(r, lds[w]);
+    out[blockIdx.x] = r;
+  }
+}
+
+// One wave per row, any dtype, any length.
+template <int OP, typename T>
+__global__ __launch_bounds__(kBlock) void row_reduce_wave(
+    T* __restrict__ out, const T* __restrict__ in, uint64_t rows,
+    uint64_t len) {
+  using R = Reducer<OP, T>;
+  const uint64_t row = uint64_t(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const T* src = in + row * len;
+  T acc = R::identity();
+  for (uint64_t j = lane; j < len; j += 64) acc = R::combine(acc, src[j]);
+  acc = wave_reduce<OP, T>(acc);
+  if (lane == 0) out[row] = acc;
+}
+
+// Fold `parts` consecutive partials per output in order.
+template <int OP, typename T>
+__global__ __launch_bounds__(kBlock) void fold_parts(T* __restrict__ out,
+                                                     const T* __restrict__ part,
+                                                     uint64_t n,
+                                                     uint32_t parts) {
+  using R = Reducer<OP, T>;
+  const uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= n) return;
+  T acc = R::identity();
+  for (uint32_t p = 0; p < parts; ++p) acc = R::combine(acc, part[i * parts + p]);
+  out[i] = acc;
+}
+
+// Column reduction, fp32, four columns per lane.  grid = (ceil(inner4/256),
+// S, outer); chunk s covers rows [s*chunk, min(len, (s+1)*chunk)).
+// dst layout: [outer, S, inner] (S == 1 writes the final result).
+template <int OP>
+__global__ __launch_bounds__(kBlock) void col_reduce_f32(
+    float* __restrict__ dst, const float* __restrict__ in, uint32_t inner4,
+    uint32_t len, uint32_t chunk) {
+  using R = Reducer<OP, float>;
+  const uint32_t c4 = blockIdx.x * kBlock + threadIdx.x;
+  if (c4 >= inner4) return;
+  const uint32_t s = blockIdx.y, S = gridDim.y, o = blockIdx.z;
+  const uint32_t r0 = s * chunk;
+  const uint32_t r1 = min(len, r0 + chunk);
+  const v4f* src = reinterpret_cast<const v4f*>(in) +
+                   (uint64_t(o) * len + r0) * inner4 + c4;
+  const v4f id = v4f(R::identity());
+  v4f acc0 = id, acc1 = id, acc2 = id, acc3 = id;
+  uint32_t r = r0;
+  for (; r + 3 < r1; r += 4) {
+    v4f x0 = src[0], x1 = src[uint64_t(inner4)], x2 = src[2 * uint64_t(inner4)],
+        x3 = src[3 * uint64_t(inner4)];
+    acc0 = combine4<OP>(acc0, x0);
+    acc1 = combine4<OP>(acc1, x1);
+    acc2 = combine4<OP>(acc2, x2);
+    acc3 = combine4<OP>(acc3, x3);
+    src += 4 * uint64_t(inner4);
+  }
+  for (; r < r1; ++r) {
+    acc0 = combine4<OP>(acc0, src[0]);
+    src += inner4;
+  }
+  const v4f acc = combine4<OP>(combine4<OP>(acc0, acc1), combine4<OP>(acc2, acc3));
+  reinterpret_cast<v4f*>(dst)[(uint64_t(o) * S + s) * inner4 + c4] = acc;
+}
+
+// Column reduction for any dtype / alignment: one lane per column.
+template <int OP, typename T>
+__global__ __launch_bounds__(kBlock) void col_reduce_scalar(
+    T* __restrict__ dst, const T* __restrict__ in, uint64_t inner,
+    uint64_t len, uint64_t chunk) {
+  using R = Reducer<OP, T>;
+  const uint64_t c = uint64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (c >= inner) return;
+  const uint64_t s = blockIdx.y, S = gridDim.y, o = blockIdx.z;
+  const uint64_t r0 = s * chunk;
+  const uint64_t r1 = min(len, r0 + chunk);
+  const T* src = in + (o * len + r0) * inner + c;
+  T acc = R::identity();
+  for (uint64_t r = r0; r < r1; ++r, src += inner) acc = R::combine(acc, *src);
+  dst[(o * S + s) * inner + c] = acc;
+}
+
+// Fold S chunk partials [outer, S, inner] -> [outer, inner] in chunk order.
+template <int OP, typename T>
+__global__ __launch_bounds__(kBlock) void fold_chunks(T* __restrict__ out,
+                                                      const T* __restrict__ part,
+                                                      uint64_t outer,
+                                                      uint64_t inner,
+                                                      uint32_t S) {
+  using R = Reducer<OP, T>;
+  const uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= outer * inner) return;
+  const uint64_t o = i / inner, c = i - o * inner;
+  const T* src = part + o * S * inner + c;
+  T acc = R::identity();
+  for (uint32_t s = 0; s < S; ++s) acc = R::combine(acc, src[uint64_t(s) * inner]);
+  out[i] = acc;
+}
+
+bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+uint32_t blocks_for(uint64_t n) { return uint32_t((n + kBlock - 1) / kBlock); }
+
+template <int OP, typename T>
+int reduce_rows(Runtime* rt, T* out, const T* in, uint64_t rows, uint64_t len) {
+  if constexpr (std::is_same_v<T, float>) {
+    if (len >= 2048 && len % 4 == 0 && aligned16(in) && len / 4 <= 0xffffffffull) {
+      const uint64_t len4 = len / 4;
+      // Enough workgroups to fill the chip twice over; split long rows only
+      // when rows alone cannot.
+      const uint64_t target = uint64_t(rt->cu_count) * 8;
+      uint64_t parts = 1;
+      if (rows < target) parts = std::min<uint64_t>((target + rows - 1) / rows,
+                                                    std::max<uint64_t>(1, len4 / 1024));
+      const uint64_t seg4 = (len4 + parts - 1) / parts;
+      parts = (len4 + seg4 - 1) / seg4;
+      if (rows * parts > 0x7fffffffull)
+        return fail(LMP_ERR_UNSUPPORTED, "reduce: too many rows");
+      float* dst = out;
+      float* tmp = nullptr;
+      if (parts > 1) {
+        tmp = static_cast<float*>(scratch_alloc(rows * parts * sizeof(float)));
+        if (!tmp) return LMP_ERR_OOM;
+        dst = tmp;
+      }
+      hipLaunchKernelGGL((row_reduce_f32<OP>), dim3(uint32_t(rows * parts)),
+                         dim3(kBlock), 0, rt->stream, dst, in, uint32_t(len4),
+                         uint32_t(seg4), FastDiv(uint32_t(parts)));
+      LMP_LAUNCH_CHECK("row_reduce_f32");
+      if (parts > 1) {
+        hipLaunchKernelGGL((fold_parts<OP, float>), dim3(blocks_for(rows)),
+                           dim3(kBlock), 0, rt->stream, out, tmp, rows,
+                           uint32_t(parts));
+        LMP_LAUNCH_CHECK("fold_parts");
+        scratch_free(tmp);
+      }
+      return LMP_OK;
+    }
+  }
+  const uint64_t blocks = (rows + kWaves - 1) / kWaves;
+  if (blocks > 0x7fffffffull) return fail(LMP_ERR_UNSUPPORTED, "reduce: too many rows");
+  hipLaunchKernelGGL((row_reduce_wave<OP, T>), dim3(uint32_t(blocks)),
+                     dim3(kBlock), 0, rt->stream, out, in, rows, len);
+  LMP_LAUNCH_CHECK("row_reduce_wave");
+  return LMP_OK;
+}
+
+template <int OP, typename T>
+int reduce_cols(Runtime* rt, T* out, const T* in, uint64_t outer, uint64_t len,
+                uint64_t inner) {
+  const bool vec = std::is_same_v<T, float> && inner % 4 == 0 && aligned16(in) &&
+                   aligned16(out) && inner / 4 <= 0xffffffffull &&
+                   len <= 0xffffffffull;
+  const uint64_t lanes = vec ? inner / 4 : inner;
+  const uint64_t gx = (lanes + kBlock - 1) / kBlock;
+  if (gx > 0x7fffffffull || outer > 65535)
+    return fail(LMP_ERR_UNSUPPORTED, "reduce: grid too large");
+  // Chunk the reduced axis until the grid reaches ~8 workgroups per CU,
+  // keeping at least 16 rows per chunk.
+  const uint64_t target = uint64_t(rt->cu_count) * 8;
+  uint64_t S = 1;
+  const uint64_t base = gx * outer;
+  if (base < target) S = std::min<uint64_t>((target + base - 1) / base,
+                                            std::max<uint64_t>(1, len / 16));
+  S = std::min<uint64_t>(S, 65535);
+  const uint64_t chunk = (len + S - 1) / S;
+  S = (len + chunk - 1) / chunk;
+  T* dst = out;
+  T* tmp = nullptr;
+  if (S > 1) {
+    tmp = static_cast<T*>(scratch_alloc(outer * S * inner * sizeof(T)));
+    if (!tmp) return LMP_ERR_OOM;
+    dst = tmp;
+  }
+  const dim3 grid{uint32_t(gx), uint32_t(S), uint32_t(outer)};
+  if constexpr (std::is_same_v<T, float>) {
+    if (vec) {
+      hipLaunchKernelGGL((col_reduce_f32<OP>), grid, dim3(kBlock), 0,
+                         rt->stream, dst, in, uint32_t(inner / 4),
+                         uint32_t(len), uint32_t(chunk));
+      LMP_LAUNCH_CHECK("col_reduce_f32");
+    }
+  }
+  if (!vec) {
+    hipLaunchKernelGGL((col_reduce_scalar<OP, T>), grid, dim3(kBlock), 0,
+                       rt->stream, dst, in, inner, len, chunk);
+    LMP_LAUNCH_CHECK("col_reduce_scalar");
+  }
+  if (S > 1) {
+    const uint64_t n = outer * inner;
+    hipLaunchKernelGGL((fold_chunks<OP, T>), dim3(blocks_for(n)), dim3(kBlock),
+                       0, rt->stream, out, tmp, outer, inner, uint32_t(S));
+    LMP_LAUNCH_CHECK("fold_chunks");
+    scratch_free(tmp);
+  }
+  return LMP_OK;
+}
+
+template <typename T>
+int dispatch_reduce(int op, Runtime* rt, T* out, const T* in, uint64_t outer,
+                    uint64_t len, uint64_t inner) {
+  switch (op) {
+#define LMP_CASE(OPV)                                                      \
+  case OPV:                                                                \
+    return inner == 1 ? reduce_rows<OPV, T>(rt, out, in, outer, len)       \
+                      : reduce_cols<OPV, T>(rt, out, in, outer, len, inner);
+    LMP_CASE(LMP_RED_SUM)
+    LMP_CASE(LMP_RED_MAX)
+    LMP_CASE(LMP_RED_MIN)
+    LMP_CASE(LMP_RED_PROD)
+#undef LMP_CASE
+    default:
+      return fail(LMP_ERR_INVALID, "lmp_k_reduce: unknown op " + std::to_string(op));
+  }
+}
+
+}  // namespace
+}  // namespace lmp_hip
+
+using namespace lmp_hip;
+
+extern "C" int lmp_k_reduce(int op, int dtype, void* out, const void* in,
+                            size_t outer, size_t len, size_t inner) {
+  if (outer == 0 || inner == 0) return LMP_OK;
+  if (!out || !in) return fail(LMP_ERR_INVALID, "lmp_k_reduce: null buffer");
+  if (len == 0) {
+    // Empty reduced axis: every output is the identity.
+    double id = 0.0;
+    if (op == LMP_RED_PROD) id = 1.0;
+    else if (op == LMP_RED_MAX || op == LMP_RED_MIN)
+      return fail(LMP_ERR_INVALID, "max/min over an empty axis");
+    return lmp_k_fill(dtype, out, outer * inner, id);
+  }
+  LMP_RUNTIME_OR_FAIL(rt);
+  switch (dtype) {
+    case LMP_FLOAT32:
+      return dispatch_reduce<float>(op, rt, static_cast<float*>(out),
+                                    static_cast<const float*>(in), outer, len, inner);
+    case LMP_FLOAT64:
+      return dispatch_reduce<double>(op, rt, static_cast<double*>(out),
+                                     static_cast<const double*>(in), outer, len, inner);
+    case LMP_INT32:
+      return dispatch_reduce<int32_t>(op, rt, static_cast<int32_t*>(out),
+                                      static_cast<const int32_t*>(in), outer, len, inner);
+    case LMP_INT64:
+      return dispatch_reduce<int64_t>(op, rt, static_cast<int64_t*>(out),
+                                      static_cast<const int64_t*>(in), outer, len, inner);
+    case LMP_INT16:
+      return dispatch_reduce<int16_t>(op, rt, static_cast<int16_t*>(out),
+                                      static_cast<const int16_t*>(in), outer, len, inner);
+    default:
+      return fail(LMP_ERR_UNSUPPORTED,
+                  std::string("lmp_k_reduce: dtype ") + dtype_name(dtype));
+  }
+}

@@ -1,0 +1,289 @@
+// Runtime half of the C ABI: device selection, the pooled allocator, copies,
+// synchronisation and timing events.  These are the only hip* runtime calls
+// of the backend apart from kernel launches and the hipRTC module loader.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "arena.hpp"
+#include "common.hpp"
+
+namespace lmp_hip {
+
+namespace {
+
+thread_local std::string t_error;
+
+// Segment granularity: with 288 GB of HBM per MI355X a large minimum keeps the
+// segment count low; requests above it get a segment of their own size.
+constexpr size_t kAlign = 256;
+constexpr size_t kMinSegment = 128ull << 20;
+
+struct Pool {
+  std::mutex mu;
+  Arena arena{kAlign};
+  uint64_t allocs = 0;
+  uint64_t device_mallocs = 0;
+};
+
+Pool& pool() {
+  // Immortal: tensors held by static objects may be freed during exit.
+  static Pool* p = new Pool();
+  return *p;
+}
+
+std::mutex g_init_mu;
+Runtime g_rt;
+bool g_ready = false;
+
+int init_locked(int device) {
+  if (g_ready) {
+    if (device != g_rt.device)
+      return fail(LMP_ERR_INVALID,
+                  "lmp_rt_init: library already bound to device " +
+                      std::to_string(g_rt.device));
+    return LMP_OK;
+  }
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0)
+    return fail(LMP_ERR_RUNTIME,
+                std::string("no HIP device available: ") +
+                    (e == hipSuccess ? "device count is 0"
+                                     : hipGetErrorString(e)));
+  if (device < 0 || device >= count)
+    return fail(LMP_ERR_INVALID, "lmp_rt_init: device index out of range");
+  LMP_HIP_TRY(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  LMP_HIP_TRY(hipGetDeviceProperties(&prop, device));
+  // Default priority: the stream is created without a priority argument.
+  LMP_HIP_TRY(hipStreamCreateWithFlags(&g_rt.stream, hipStreamNonBlocking));
+  g_rt.device = device;
+  g_rt.cu_count = prop.multiProcessorCount;
+  g_rt.max_threads_per_cu = prop.maxThreadsPerMultiProcessor;
+  g_rt.lds_per_cu = prop.maxSharedMemoryPerMultiProcessor;
+  g_ready = true;
+  return LMP_OK;
+}
+
+int grow_and_allocate(Pool& p, size_t bytes, void** out) {
+  const size_t need = p.arena.round_up(bytes);
+  const size_t seg = std::max(kMinSegment, need);
+  void* base = nullptr;
+  hipError_t e = hipMalloc(&base, seg);
+  if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) {
+    (void)hipGetLastError();
+    // Release cached segments once, then retry (allocator.cu:101-125).
+    hipError_t se = hipStreamSynchronize(g_rt.stream);
+    if (se != hipSuccess)
+      return fail(LMP_ERR_RUNTIME, std::string("hipStreamSynchronize: ") +
+                                       hipGetErrorString(se));
+    for (const Arena::Span& s : p.arena.take_free_segments())
+      (void)hipFree(reinterpret_cast<void*>(s.addr));
+    e = hipMalloc(&base, seg);
+  }
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(LMP_ERR_OOM, "hipMalloc of " + std::to_string(seg) +
+                                 " bytes failed: " + hipGetErrorString(e));
+  }
+  ++p.device_mallocs;
+  if (!p.arena.add_segment(reinterpret_cast<Arena::Addr>(base), seg))
+    return fail(LMP_ERR_RUNTIME, "allocator: hipMalloc returned a misaligned "
+                                 "or overlapping segment");
+  auto span = p.arena.allocate(bytes);
+  if (!span)
+    return fail(LMP_ERR_RUNTIME, "allocator: new segment cannot serve request");
+  *out = reinterpret_cast<void*>(span->addr);
+  return LMP_OK;
+}
+
+}  // namespace
+
+void set_error(const std::string& msg) { t_error = msg; }
+
+int fail(int status, const std::string& msg) {
+  t_error = msg;
+  return status;
+}
+
+Runtime* runtime() {
+  std::lock_guard<std::mutex> lock(g_init_mu);
+  if (!g_ready && init_locked(0) != LMP_OK) return nullptr;
+  return &g_rt;
+}
+
+void* scratch_alloc(size_t bytes) {
+  void* p = nullptr;
+  if (lmp_rt_malloc(&p, bytes) != LMP_OK) return nullptr;
+  return p;
+}
+
+void scratch_free(void* ptr) { (void)lmp_rt_free(ptr); }
+
+}  // namespace lmp_hip
+
+using namespace lmp_hip;
+
+extern "C" {
+
+int lmp_rt_abi_version(void) { return LMP_HIP_ABI_VERSION; }
+
+const char* lmp_rt_last_error(void) { return t_error.c_str(); }
+
+int lmp_rt_init(int device) {
+  std::lock_guard<std::mutex> lock(g_init_mu);
+  return init_locked(device);
+}
+
+int lmp_rt_device_count(int* count) {
+  if (!count) return fail(LMP_ERR_INVALID, "null count");
+  *count = 0;
+  hipError_t e = hipGetDeviceCount(count);
+  if (e != hipSuccess) {
+    *count = 0;
+    (void)hipGetLastError();
+  }
+  return LMP_OK;
+}
+
+int lmp_rt_device_info(lmp_rt_info* info) {
+  if (!info) return fail(LMP_ERR_INVALID, "null info");
+  LMP_RUNTIME_OR_FAIL(rt);
+  hipDeviceProp_t prop;
+  LMP_HIP_TRY(hipGetDeviceProperties(&prop, rt->device));
+  std::memset(info, 0, sizeof(*info));
+  info->device = rt->device;
+  info->cu_count = prop.multiProcessorCount;
+  info->simd_per_cu = 4;
+  info->wave_size = prop.warpSize;
+  info->lds_bytes_per_cu = static_cast<int64_t>(prop.maxSharedMemoryPerMultiProcessor);
+  info->total_mem_bytes = static_cast<int64_t>(prop.totalGlobalMem);
+  info->clock_khz = prop.clockRate;
+  info->mem_clock_khz = prop.memoryClockRate;
+  info->mem_bus_width = prop.memoryBusWidth;
+  std::strncpy(info->arch, prop.gcnArchName, sizeof(info->arch) - 1);
+  std::strncpy(info->name, prop.name, sizeof(info->name) - 1);
+  return LMP_OK;
+}
+
+int lmp_rt_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail(LMP_ERR_INVALID, "lmp_rt_malloc: null out pointer");
+  *ptr = nullptr;
+  if (bytes == 0) return LMP_OK;
+  LMP_RUNTIME_OR_FAIL(rt);
+  (void)rt;
+  Pool& p = pool();
+  std::lock_guard<std::mutex> lock(p.mu);
+  ++p.allocs;
+  if (auto span = p.arena.allocate(bytes)) {
+    *ptr = reinterpret_cast<void*>(span->addr);
+    return LMP_OK;
+  }
+  return grow_and_allocate(p, bytes, ptr);
+}
+
+int lmp_rt_free(void* ptr) {
+  if (!ptr) return LMP_OK;
+  Pool& p = pool();
+  std::lock_guard<std::mutex> lock(p.mu);
+  if (!p.arena.release(reinterpret_cast<Arena::Addr>(ptr)))
+    return fail(LMP_ERR_INVALID, "lmp_rt_free: pointer not owned by the pool");
+  return LMP_OK;
+}
+
+int lmp_rt_empty_cache(void) {
+  LMP_RUNTIME_OR_FAIL(rt);
+  Pool& p = pool();
+  std::lock_guard<std::mutex> lock(p.mu);
+  LMP_HIP_TRY(hipStreamSynchronize(rt->stream));
+  for (const Arena::Span& s : p.arena.take_free_segments())
+    LMP_HIP_TRY(hipFree(reinterpret_cast<void*>(s.addr)));
+  return LMP_OK;
+}
+
+int lmp_rt_pool_stats_get(lmp_rt_pool_stats* stats) {
+  if (!stats) return fail(LMP_ERR_INVALID, "null stats");
+  Pool& p = pool();
+  std::lock_guard<std::mutex> lock(p.mu);
+  stats->reserved_bytes = p.arena.reserved_bytes();
+  stats->allocated_bytes = p.arena.in_use_bytes();
+  stats->segments = p.arena.segment_count();
+  stats->allocs = p.allocs;
+  stats->device_mallocs = p.device_mallocs;
+  return LMP_OK;
+}
+
+int lmp_rt_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return LMP_OK;
+  if (!dst || !src) return fail(LMP_ERR_INVALID, "memcpy_h2d: null pointer");
+  LMP_RUNTIME_OR_FAIL(rt);
+  LMP_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, rt->stream));
+  // The source may be pageable memory the caller reuses right away.
+  LMP_HIP_TRY(hipStreamSynchronize(rt->stream));
+  return LMP_OK;
+}
+
+int lmp_rt_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return LMP_OK;
+  if (!dst || !src) return fail(LMP_ERR_INVALID, "memcpy_d2h: null pointer");
+  LMP_RUNTIME_OR_FAIL(rt);
+  LMP_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, rt->stream));
+  LMP_HIP_TRY(hipStreamSynchronize(rt->stream));
+  return LMP_OK;
+}
+
+int lmp_rt_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return LMP_OK;
+  if (!dst || !src) return fail(LMP_ERR_INVALID, "memcpy_d2d: null pointer");
+  LMP_RUNTIME_OR_FAIL(rt);
+  LMP_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, rt->stream));
+  return LMP_OK;
+}
+
+int lmp_rt_synchronize(void) {
+  LMP_RUNTIME_OR_FAIL(rt);
+  LMP_HIP_TRY(hipStreamSynchronize(rt->stream));
+  return LMP_OK;
+}
+
+void* lmp_rt_stream(void) {
+  Runtime* rt = runtime();
+  return rt ? static_cast<void*>(rt->stream) : nullptr;
+}
+
+int lmp_rt_event_create(void** event) {
+  if (!event) return fail(LMP_ERR_INVALID, "null event");
+  LMP_RUNTIME_OR_FAIL(rt);
+  (void)rt;
+  hipEvent_t e;
+  LMP_HIP_TRY(hipEventCreate(&e));
+  *event = e;
+  return LMP_OK;
+}
+
+int lmp_rt_event_record(void* event) {
+  if (!event) return fail(LMP_ERR_INVALID, "null event");
+  LMP_RUNTIME_OR_FAIL(rt);
+  LMP_HIP_TRY(hipEventRecord(static_cast<hipEvent_t>(event), rt->stream));
+  return LMP_OK;
+}
+
+int lmp_rt_event_elapsed_ms(void* start, void* stop, float* ms) {
+  if (!start || !stop || !ms) return fail(LMP_ERR_INVALID, "null argument");
+  LMP_HIP_TRY(hipEventSynchronize(static_cast<hipEvent_t>(stop)));
+  LMP_HIP_TRY(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
+                                  static_cast<hipEvent_t>(stop)));
+  return LMP_OK;
+}
+
+int lmp_rt_event_destroy(void* event) {
+  if (!event) return LMP_OK;
+  LMP_HIP_TRY(hipEventDestroy(static_cast<hipEvent_t>(event)));
+  return LMP_OK;
+}
+
+}  // extern "C"

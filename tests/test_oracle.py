@@ -1,0 +1,348 @@
+"""Pin the CPU oracle before trusting it (CPU only).
+
+Every oracle function is checked against something that does not share its
+code: the reference gtests' known answers (tests/golden), numpy's IEEE float32
+ops (one rounding per op, bit-exact), correctly rounded values (float64
+evaluation rounded to float32) for transcendentals, brute-force sequential
+folds in pure Python for the reduction / matmul order, float64 numpy for sums
+and products, and torch float64 autograd for the gradient formulas.
+"""
+import json
+import zlib
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from _helpers import ulp_dist
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "lamp3_known_answers.json").read_text())
+ATOL = GOLDEN["tolerance"]["atol"]
+
+
+def _num(v):
+    return float(v) if not isinstance(v, str) else float(v.replace("inf", "inf"))
+
+
+def correctly_rounded(fn, *args):
+    return fn(*[np.asarray(a, np.float64) for a in args]).astype(np.float32)
+
+
+# ------------------------------------------------------------ golden vectors
+
+@pytest.mark.parametrize("case", GOLDEN["tensor"], ids=lambda c: c["name"])
+def test_known_answers_binary(oracle, case):
+    out = oracle.binary(case["op"], np.array(case["a"], np.float32),
+                        np.array(case["b"], np.float32))
+    assert list(out.shape) == case["shape"]
+    np.testing.assert_allclose(out.reshape(-1), np.array(case["expect"], np.float64),
+                               atol=case.get("atol", ATOL), rtol=0)
+
+
+@pytest.mark.parametrize("case", GOLDEN["reduce"], ids=lambda c: c["name"])
+def test_known_answers_reduce(oracle, case):
+    out = oracle.reduce(case["op"], np.array(case["a"], np.float32), case["axis"])
+    assert list(out.shape) == case["shape"]
+    np.testing.assert_allclose(out.reshape(-1), case["expect"], atol=ATOL, rtol=0)
+
+
+def _close(got, want):
+    want = np.array([_num(v) for v in want], np.float64)
+    got = np.asarray(got, np.float64).reshape(-1)
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isinf(got), np.isinf(want))
+    assert np.array_equal(np.sign(got[~fin]), np.sign(want[~fin]))
+    np.testing.assert_allclose(got[fin], want[fin], atol=ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("case", GOLDEN["autograd"], ids=lambda c: c["name"])
+def test_known_answers_autograd(oracle, case):
+    O = oracle
+    a = O.OVar(np.array(GOLDEN["inputs"]["a"], np.float32), True)
+    b = O.OVar(np.array(GOLDEN["inputs"]["b"], np.float32), True)
+    extra = {}
+    e = case["expr"]
+    if e == "a + b": out = a + b
+    elif e == "a - b": out = a - b
+    elif e == "a * b": out = a * b
+    elif e == "a / b":
+        with np.errstate(divide="ignore", invalid="ignore"):
+            out = a / b
+    elif e == "exp(b)": out = O.exp(b)
+    elif e == "log(a)": out = O.log(a)
+    elif e == "a @ m":
+        extra["m"] = O.OVar(np.array(case["m"], np.float32), True)
+        out = a @ extra["m"]
+    elif e == "transpose(a)": out = O.transpose_v(a)
+    elif e == "sum(a, 1)": out = O.sum_(a, 1)
+    elif e == "max(a, 1)": out = O.max_(a, 1)
+    elif e == "min(a, 1)": out = O.min_(a, 1)
+    elif e == "a + r":
+        extra["r"] = O.OVar(np.array(case["r"], np.float32), True)
+        out = a + extra["r"]
+    else:
+        raise AssertionError(e)
+    _close(out.data, case["out"])
+    out.backward()
+    if "grad_a" in case: _close(a.grad, case["grad_a"])
+    if "grad_b" in case: _close(b.grad, case["grad_b"])
+    if "grad_m" in case: _close(extra["m"].grad, case["grad_m"])
+    if "grad_r" in case:
+        _close(extra["r"].grad, case["grad_r"])
+        assert extra["r"].grad.shape == (1, 2)
+
+
+@pytest.mark.parametrize("case", GOLDEN["autograd_unary"], ids=lambda c: c["name"])
+def test_known_answers_unary_grads(oracle, case):
+    O = oracle
+    x = O.OVar(np.array(case["x"], np.float32), True)
+    fn = case["fn"]
+    out = {"sqrt": O.sqrt, "cos": O.cos, "tan": O.tan, "abs": O.abs_}.get(fn)
+    out = out(x) if out else O.clamp(x, case["lo"], case["hi"])
+    out.backward()
+    _close(x.grad, case["grad"])
+
+
+def test_repeated_backward_accumulates(oracle):
+    a = oracle.OVar(np.array(GOLDEN["inputs"]["a"], np.float32), True)
+    r = a * 2.0
+    r.backward()
+    r.backward()
+    _close(a.grad, GOLDEN["repeated_backward"]["grad_a"])
+
+
+def test_functional_sgd(oracle):
+    g = GOLDEN["functional_sgd"]
+    w = oracle.OVar(np.array(g["w"], np.float32), True)
+    x, y = oracle.OVar(np.array(g["x"], np.float32)), oracle.OVar(np.array(g["y"], np.float32))
+    err = x * w - y
+    (oracle.sum_(err * err, 0)).backward()
+    new = w.data - np.float32(g["lr"]) * w.grad
+    np.testing.assert_allclose(new, g["expect"], rtol=1e-6)
+
+
+# ------------------------------------------------- independent closed forms
+
+SHAPES = [((7, 9), (7, 9)), ((64, 33), (64, 1)), ((64, 33), (33,)),
+          ((64, 33), (1, 33)), ((5, 6, 7), (6, 1)), ((4, 1, 3), (1, 5, 3)),
+          ((13,), (1,)), ((2, 3, 4, 5), (3, 1, 5))]
+
+
+@pytest.mark.parametrize("op,npf", [("add", np.add), ("sub", np.subtract),
+                                    ("mul", np.multiply), ("div", np.divide)])
+@pytest.mark.parametrize("sa,sb", SHAPES)
+def test_binary_bitexact_vs_numpy(oracle, op, npf, sa, sb):
+    rng = np.random.default_rng(zlib.crc32(repr((op, sa, sb)).encode()))
+    a = rng.standard_normal(sa, dtype=np.float32)
+    b = rng.standard_normal(sb, dtype=np.float32) + np.float32(3.0)
+    got = oracle.binary(op, a, b)
+    want = npf(a, b)
+    assert got.shape == want.shape
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    got_r = oracle.binary(op, b, a)  # reversed operand order
+    assert np.array_equal(got_r.view(np.uint32), npf(b, a).view(np.uint32))
+
+
+@pytest.mark.parametrize("op,npf", [("eq", np.equal), ("ne", np.not_equal),
+                                    ("ge", np.greater_equal), ("le", np.less_equal),
+                                    ("gt", np.greater), ("lt", np.less)])
+def test_compare_vs_numpy(oracle, op, npf):
+    rng = np.random.default_rng(3)
+    a = rng.integers(-3, 4, (40, 17)).astype(np.float32)
+    b = rng.integers(-3, 4, (1, 17)).astype(np.float32)
+    got = oracle.binary(op, a, b)
+    assert np.array_equal(got, npf(a, b).astype(np.float32))
+
+
+def test_unary_exact_ops(oracle):
+    x = np.array([-2.5, -0.0, 0.0, 1.5, np.inf, -np.inf, np.nan, 1e-40, -3e38],
+                 np.float32)
+    assert np.array_equal(oracle.unary("neg", x).view(np.uint32), (-x).view(np.uint32))
+    assert np.array_equal(oracle.unary("abs", x).view(np.uint32),
+                          np.abs(x).view(np.uint32))
+    pos = np.abs(x[np.isfinite(x)])
+    assert np.array_equal(oracle.unary("sqrt", pos), np.sqrt(pos))
+    # ReLU = clamp(x, 0, DBL_MAX): -0.0 stays -0.0, NaN stays NaN, +inf stays.
+    r = oracle.unary("clamp", x, 0.0, oracle.DBL_MAX)
+    want = np.where(x < 0, np.float32(0), x)
+    assert np.array_equal(r.view(np.uint32), want.view(np.uint32))
+    assert np.signbit(r[1]) and np.isnan(r[6])
+
+
+@pytest.mark.parametrize("op,fn", [("exp", np.exp), ("log", np.log), ("sin", np.sin),
+                                   ("cos", np.cos), ("tan", np.tan)])
+def test_transcendentals_within_1ulp_of_correctly_rounded(oracle, op, fn):
+    rng = np.random.default_rng(11)
+    x = rng.uniform(-20, 20, 20000).astype(np.float32)
+    if op == "log":
+        x = np.abs(x) + np.float32(1e-3)
+    got = oracle.unary(op, x)
+    assert ulp_dist(got, correctly_rounded(fn, x)).max() <= 1
+
+
+def test_pow_within_1ulp(oracle):
+    rng = np.random.default_rng(5)
+    a = rng.uniform(0.01, 10, 5000).astype(np.float32)
+    b = rng.uniform(-4, 4, 5000).astype(np.float32)
+    got = oracle.binary("pow", a, b)
+    assert ulp_dist(got, correctly_rounded(np.power, a, b)).max() <= 1
+
+
+def test_reduction_order_is_sequential(oracle):
+    """The oracle folds each output in index order from the identity: compare
+    with a pure-Python float32 fold (small case, bit-exact)."""
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal((4, 37, 5), dtype=np.float32)
+    for axis in range(3):
+        got = oracle.reduce("sum", a, axis)
+        moved = np.moveaxis(a, axis, -1)
+        want = np.zeros(moved.shape[:-1], np.float32)
+        for idx in np.ndindex(*moved.shape[:-1]):
+            acc = np.float32(0)
+            for v in moved[idx]:
+                acc = np.float32(acc + v)
+            want[idx] = acc
+        assert np.array_equal(got.reshape(-1), np.expand_dims(want, axis).reshape(-1))
+
+
+@pytest.mark.parametrize("axis", [0, 1])
+def test_reduce_vs_numpy(oracle, axis):
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal((300, 257), dtype=np.float32)
+    for op, fn in (("max", np.max), ("min", np.min)):
+        assert np.array_equal(oracle.reduce(op, a, axis), fn(a, axis=axis, keepdims=True))
+    s = oracle.reduce("sum", a, axis).astype(np.float64)
+    t = a.astype(np.float64).sum(axis=axis, keepdims=True)
+    assert np.max(np.abs(s - t)) / np.max(np.abs(t)) < 1e-5
+    p = oracle.reduce("prod", (a[:8] * 0.5 + 1).astype(np.float32), axis)
+    tp = np.prod((a[:8] * 0.5 + 1).astype(np.float64), axis=axis, keepdims=True)
+    np.testing.assert_allclose(p, tp, rtol=1e-5)
+
+
+def test_matmul_order_and_value(oracle):
+    rng = np.random.default_rng(4)
+    a = rng.standard_normal((5, 11), dtype=np.float32)
+    b = rng.standard_normal((11, 3), dtype=np.float32)
+    got = oracle.matmul(a, b)
+    want = np.zeros((5, 3), np.float32)
+    for i in range(5):
+        for j in range(3):
+            s = np.float32(0)
+            for t in range(11):
+                s = np.float32(s + np.float32(a[i, t] * b[t, j]))
+            want[i, j] = s
+    assert np.array_equal(got, want)
+    a = rng.standard_normal((64, 300), dtype=np.float32)
+    b = rng.standard_normal((300, 40), dtype=np.float32)
+    t = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.max(np.abs(oracle.matmul(a, b) - t)) / np.max(np.abs(t)) < 1e-5
+
+
+def test_transpose_fill_add_inplace(oracle):
+    a = np.arange(12, dtype=np.float32).reshape(3, 4)
+    assert np.array_equal(oracle.transpose(a), a.T)
+    f = oracle.fill((3, 5), 2.5)
+    assert np.array_equal(f, np.full((3, 5), 2.5, np.float32))
+    d = a.copy()
+    oracle.add_inplace(d, a)
+    assert np.array_equal(d, a + a)
+
+
+def test_planted_stride_mistake_is_caught(oracle):
+    """Sensitivity check: transposing the broadcast operand's padded strides
+    (a plausible indexing bug) must break agreement with numpy."""
+    a = np.arange(12, dtype=np.float32).reshape(3, 4)
+    b = np.arange(4, dtype=np.float32).reshape(1, 4)
+    good = oracle.binary("add", a, b)
+    assert np.array_equal(good, a + b)
+    orig = oracle.padded_strides
+    try:
+        oracle.padded_strides = lambda s, nd: list(reversed(orig(s, nd)))
+        bad = oracle.binary("add", a, b)
+    finally:
+        oracle.padded_strides = orig
+    assert not np.array_equal(bad, a + b)
+
+
+# ----------------------------------------------- autograd vs torch float64
+
+torch = pytest.importorskip("torch")
+
+
+def _torch_softmax_lamp(x, dim):
+    # Lamp3's softmax graph: max with an eq-mask gradient (reduct_ops.cpp:14),
+    # so torch must rebuild it from primitives rather than use torch.softmax.
+    m = x.max(dim=dim, keepdim=True).values
+    mask_src = x.detach()
+    class LampMax(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, inp):
+            out = inp.max(dim=dim, keepdim=True).values
+            ctx.save_for_backward(inp, out)
+            return out
+        @staticmethod
+        def backward(ctx, g):
+            inp, out = ctx.saved_tensors
+            return g * (inp == out).to(g.dtype)
+    m = LampMax.apply(x)
+    e = torch.exp(x - m)
+    return e / e.sum(dim=dim, keepdim=True)
+
+
+def test_autograd_graph_vs_torch(oracle):
+    rng = np.random.default_rng(7)
+    x0 = rng.uniform(0.5, 2.0, (6, 5)).astype(np.float32)
+    w0 = rng.standard_normal((5, 4), dtype=np.float32)
+    b0 = rng.standard_normal((4,), dtype=np.float32)
+    O = oracle
+    x, w, b = O.OVar(x0, True), O.OVar(w0, True), O.OVar(b0, True)
+    h = O.relu(x @ w + b)
+    s = O.softmax(O.sqrt(O.exp(O.sin(h)) * 2.0) / (O.log(x @ w * 0.1 + 3.0) + 1.0), -1)
+    loss = O.sum_(O.sum_(s * O.tan(O.cos(h) * 0.5), 1), 0)
+    loss.backward()
+
+    tx = torch.tensor(x0, dtype=torch.float64, requires_grad=True)
+    tw = torch.tensor(w0, dtype=torch.float64, requires_grad=True)
+    tb = torch.tensor(b0, dtype=torch.float64, requires_grad=True)
+    th = torch.clamp(tx @ tw + tb, min=0.0)
+    ts = _torch_softmax_lamp(torch.sqrt(torch.exp(torch.sin(th)) * 2.0)
+                             / (torch.log(tx @ tw * 0.1 + 3.0) + 1.0), -1)
+    tl = (ts * torch.tan(torch.cos(th) * 0.5)).sum(1, keepdim=True).sum(0, keepdim=True)
+    tl.backward()
+    for mine, ref in ((loss.data, tl.detach()), (x.grad, tx.grad), (w.grad, tw.grad),
+                      (b.grad, tb.grad)):
+        ref = ref.numpy()
+        assert np.max(np.abs(mine - ref)) / (np.max(np.abs(ref)) + 1e-10) < 1e-4
+
+
+def test_mlp_trajectory_vs_torch(oracle):
+    """README MLP (config 0) shapes, 5 steps: oracle vs a torch float64
+    restatement of the same graph."""
+    rng = np.random.default_rng(0)
+    x = rng.random((32, 256), dtype=np.float32)
+    y = rng.random((32, 10), dtype=np.float32)
+    ws = [rng.standard_normal((256, 64), dtype=np.float32),
+          rng.standard_normal((64, 10), dtype=np.float32)]
+    bs = [rng.standard_normal((64,), dtype=np.float32),
+          rng.standard_normal((10,), dtype=np.float32)]
+    losses, fw, fb = oracle.mlp_train(ws, bs, x, y, steps=5)
+
+    tw = [torch.tensor(w, dtype=torch.float64) for w in ws]
+    tb = [torch.tensor(b, dtype=torch.float64) for b in bs]
+    tx, ty = torch.tensor(x, dtype=torch.float64), torch.tensor(y, dtype=torch.float64)
+    tl = []
+    for _ in range(5):
+        for t in tw + tb:
+            t.requires_grad_(True)
+        h = torch.clamp(tx @ tw[0] + tb[0], min=0.0)
+        p = _torch_softmax_lamp(h @ tw[1] + tb[1], -1)
+        loss = (-ty * torch.log(p + 1e-3)).sum(1, keepdim=True).sum(0, keepdim=True)
+        loss.backward()
+        tl.append(float(loss))
+        tw = [(w - 1e-3 * w.grad).detach() for w in tw]
+        tb = [(b - 1e-3 * b.grad).detach() for b in tb]
+    np.testing.assert_allclose(losses, tl, rtol=1e-4)
+    for mine, ref in zip(fw + fb, tw + tb):
+        ref = ref.numpy()
+        assert np.max(np.abs(mine - ref)) / np.max(np.abs(ref)) < 1e-4
