@@ -417,6 +417,22 @@ def softmax(x: OVar, dim: int) -> OVar:
 # ------------------------------------------------------------------- MLP
 
 
+def mlp_step(weights, biases, x, y):
+    """One forward + backward of the README MLP from the given parameters.
+    Returns (loss, weight grads, bias grads)."""
+    W = [OVar(w, True) for w in weights]
+    B = [OVar(b, True) for b in biases]
+    h = OVar(x)
+    for i in range(len(W)):
+        h = (h @ W[i]) + B[i]
+        if i < len(W) - 1:
+            h = relu(h)
+    p = softmax(h, -1)
+    loss = sum_(sum_((-OVar(y)) * log(p + 1e-3), 1), 0)
+    loss.backward()
+    return float(loss.data.reshape(-1)[0]), [w.grad for w in W], [b.grad for b in B]
+
+
 def mlp_train(weights, biases, x, y, steps: int, lr: float = 1e-3):
     """Train Linear-ReLU-...-Linear-Softmax with the README loop
     (README.md:116-126): loss = sum(sum(-y * log(p + 1e-3), 1), 0), full

@@ -1,0 +1,379 @@
+// Autograd engine and per-op backward formulas.
+//
+// Formulas are Lamp3's (autograd/functions/expand_ops.cpp:15-40,
+// unary_ops.cpp:16-28, reduct_ops.cpp:11-16, matrix_ops.cpp:8-35,
+// view_ops.cpp:12-24), including its choices that differ from other
+// libraries: the max/min gradient flows to every position equal to the
+// result, clamp's gradient uses strict bounds, and the root of backward()
+// need not be a scalar (it is seeded with ones).  Linear's backward products
+// dY*W^T and X^T*dY run as transposed-operand GEMMs instead of a transpose
+// followed by a GEMM.
+#include "autograd.hpp"
+
+#include <algorithm>
+#include <random>
+#include <unordered_set>
+
+namespace lmp::autograd {
+
+using tensor::detail::UnsafeTensorAccessor;
+namespace tops = tensor::ops;
+
+// ---------------------------------------------------------------- grad mode
+
+namespace {
+thread_local bool t_grad = true;
+}
+bool is_grad_enabled() { return t_grad; }
+void set_grad_enabled(bool enable) { t_grad = enable; }
+GradGuard::GradGuard(bool enable) : prev_(t_grad) { t_grad = enable; }
+GradGuard::~GradGuard() { t_grad = prev_; }
+
+// ----------------------------------------------------------------- Variable
+
+Variable::Variable(const Tensor& data, bool requires_grad)
+    : impl_(std::make_shared<VariableImpl>()) {
+  impl_->data = data;
+  impl_->requires_grad = requires_grad;
+  if (requires_grad) impl_->grad = tensor::zeros_like(data);
+}
+
+Variable Variable::op_result(const Tensor& data, bool requires_grad) {
+  Variable v;
+  v.impl_ = std::make_shared<VariableImpl>();
+  v.impl_->data = data;
+  v.impl_->requires_grad = requires_grad;
+  return v;
+}
+
+const Tensor& Variable::grad() const {
+  LMP_CHECK(impl_->requires_grad) << "Cannot access grad() if requires_grad = false";
+  if (!impl_->grad.defined()) impl_->grad = tensor::zeros_like(impl_->data);
+  return impl_->grad;
+}
+
+void Variable::zero_grad() {
+  LMP_CHECK(requires_grad()) << "Cannot access grad() if requires_grad = false";
+  impl_->grad = tensor::zeros_like(impl_->data);
+  impl_->grad_fn = nullptr;  // variable.cpp:25-29
+}
+
+namespace {
+// Per-(device, dtype) [1] zero used to start a deferred gradient as 0 + g.
+const Tensor& zero_scalar(DeviceType dev, DataType dt) {
+  static std::vector<Tensor> cache(static_cast<size_t>(DeviceType::Count) * 6);
+  Tensor& z = cache[static_cast<size_t>(dev) * 6 + static_cast<size_t>(dt)];
+  if (!z.defined()) z = Tensor(std::vector<Scalar>{0.0}, {1}, dev, dt);
+  return z;
+}
+}  // namespace
+
+void Variable::incr_grad(const Tensor& g) {
+  LMP_CHECK(requires_grad()) << "Cannot access grad() if requires_grad = false";
+  if (!impl_->grad.defined()) {
+    LMP_INTERNAL_ASSERT(g.shape() == impl_->data.shape())
+        << "There should be no broadcasting in incr_grad";
+    impl_->grad = tops::add(zero_scalar(g.device(), g.type()), g);
+    return;
+  }
+  LMP_INTERNAL_ASSERT(g.shape() == impl_->grad.shape())
+      << "There should be no broadcasting in incr_grad";
+  tops::add_inplace(impl_->grad, g);  // variable.cpp:30-35
+}
+
+void Variable::set_grad_fn(std::shared_ptr<Function> fn) {
+  LMP_CHECK(requires_grad()) << "Cannot access grad() if requires_grad = false";
+  impl_->grad_fn = std::move(fn);
+}
+
+void Variable::copy(const Variable& other) { impl_->data.copy(other.data()); }
+void Variable::fill(Scalar value) { impl_->data.fill(value); }
+void Variable::realize() { impl_->data.realize(); }
+
+void Variable::backward() {
+  LMP_CHECK(requires_grad()) << "Must be declared with requires_grad";
+  // Depth-first post-order over saved inputs, then reversed
+  // (variable.cpp:57-80), iteratively so deep graphs cannot overflow.
+  std::vector<Variable> topo;
+  std::unordered_set<const VariableImpl*> seen;
+  struct Frame {
+    Variable v;
+    size_t next;
+  };
+  std::vector<Frame> stack;
+  seen.insert(id());
+  stack.push_back({*this, 0});
+  while (!stack.empty()) {
+    Frame& f = stack.back();
+    const auto& fn = f.v.impl_->grad_fn;
+    if (fn && f.next < fn->saved_inputs->size()) {
+      const Variable& child = (*fn->saved_inputs)[f.next++];
+      if (seen.insert(child.id()).second) stack.push_back({child, 0});
+      continue;
+    }
+    topo.push_back(f.v);
+    stack.pop_back();
+  }
+  std::reverse(topo.begin(), topo.end());
+  impl_->grad = tensor::ones_like(impl_->data);
+  for (Variable& node : topo)
+    if (node.impl_->grad_fn) node.impl_->grad_fn->apply({node});
+}
+
+// ------------------------------------------------------------ op recording
+
+namespace {
+
+using Backward = std::function<void(const Variable& out, variable_list& ins)>;
+
+struct LambdaFunction : Function {
+  Backward fn;
+  variable_list apply(const variable_list& g) override {
+    LMP_INTERNAL_ASSERT(g.size() == 1) << "Output size mismatch.";
+    fn(g[0], *saved_inputs);
+    return {};
+  }
+};
+
+Variable record(const Tensor& result, variable_list inputs, const char* name,
+                Backward bw) {
+  bool rg = false;
+  if (is_grad_enabled())
+    for (const Variable& v : inputs) rg = rg || v.requires_grad();
+  Variable out = Variable::op_result(result, rg);
+  if (rg) {
+    auto f = std::make_shared<LambdaFunction>();
+    f->name = name;
+    f->saved_inputs = std::make_unique<variable_list>(std::move(inputs));
+    f->fn = std::move(bw);
+    out.set_grad_fn(std::move(f));
+  }
+  return out;
+}
+
+Tensor sba(const Tensor& g, const Variable& like) {
+  return detail::sum_broadcast_axis(g, like.data().shape());
+}
+
+[[noreturn]] void no_grad_formula(const char* op) {
+  throw std::runtime_error(std::string("backward of ") + op + " is not implemented");
+}
+
+}  // namespace
+
+namespace detail {
+Tensor sum_broadcast_axis(const Tensor& grad, const std::vector<size_t>& orig) {
+  if (grad.shape() == orig) return grad;
+  Tensor g = grad;
+  while (g.shape().size() > orig.size()) g = tops::sum(g, 0).squeeze(0);
+  for (size_t i = 0; i < orig.size(); ++i)
+    if (orig[i] == 1) g = tops::sum(g, i);
+  LMP_INTERNAL_ASSERT(g.shape() == orig)
+      << "Shape not correct: " << g.shape() << ". Expected: " << orig;
+  return g;
+}
+}  // namespace detail
+
+Variable scalar_var(const Variable& like, Scalar s) {
+  return Variable(tensor::scalar_like(like.data(), s));
+}
+
+namespace ops {
+
+#define LMP_BW_ARGS const Variable &out, variable_list &in
+#define SELF in[0]
+#define OTHER in[1]
+#define G out.grad()
+
+Variable add(const Variable& a, const Variable& b) {
+  return record(tops::add(a.data(), b.data()), {a, b}, "AddBackward", [](LMP_BW_ARGS) {
+    if (SELF.requires_grad()) SELF.incr_grad(sba(G, SELF));
+    if (OTHER.requires_grad()) OTHER.incr_grad(sba(G, OTHER));
+  });
+}
+
+Variable sub(const Variable& a, const Variable& b) {
+  return record(tops::sub(a.data(), b.data()), {a, b}, "SubtractBackward", [](LMP_BW_ARGS) {
+    if (SELF.requires_grad()) SELF.incr_grad(sba(G, SELF));
+    if (OTHER.requires_grad()) OTHER.incr_grad(sba(-G, OTHER));
+  });
+}
+
+Variable mul(const Variable& a, const Variable& b) {
+  return record(tops::mul(a.data(), b.data()), {a, b}, "MultiplyBackward", [](LMP_BW_ARGS) {
+    if (SELF.requires_grad()) SELF.incr_grad(sba(OTHER.data() * G, SELF));
+    if (OTHER.requires_grad()) OTHER.incr_grad(sba(SELF.data() * G, OTHER));
+  });
+}
+
+Variable div(const Variable& a, const Variable& b) {
+  return record(tops::div(a.data(), b.data()), {a, b}, "DivideBackward", [](LMP_BW_ARGS) {
+    if (SELF.requires_grad()) SELF.incr_grad(sba(G / OTHER.data(), SELF));
+    if (OTHER.requires_grad())
+      OTHER.incr_grad(sba((-1.0) * (out.data() * G / OTHER.data()), OTHER));
+  });
+}
+
+Variable pow(const Variable& a, const Variable& b) {
+  return record(tops::pow(a.data(), b.data()), {a, b}, "PowerBackward", [](LMP_BW_ARGS) {
+    if (SELF.requires_grad())
+      SELF.incr_grad(sba(G * OTHER.data() * tops::pow(SELF.data(), OTHER.data() - 1.0),
+                         SELF));
+    if (OTHER.requires_grad())
+      OTHER.incr_grad(sba(G * out.data() * tops::log(SELF.data()), OTHER));
+  });
+}
+
+#define LMP_AG_COMPARE(name, label)                                              \
+  Variable name(const Variable& a, const Variable& b) {                          \
+    return record(tops::name(a.data(), b.data()), {a, b}, label "Backward",      \
+                  [](LMP_BW_ARGS) { no_grad_formula(label); });                  \
+  }
+LMP_AG_COMPARE(eq, "Equal")
+LMP_AG_COMPARE(ne, "NotEqual")
+LMP_AG_COMPARE(ge, "GreaterEqual")
+LMP_AG_COMPARE(le, "LessEqual")
+LMP_AG_COMPARE(gt, "Greater")
+LMP_AG_COMPARE(lt, "Less")
+#undef LMP_AG_COMPARE
+
+#define LMP_AG_UNARY_DEF(name, label, formula)                                  \
+  Variable name(const Variable& a) {                                           \
+    return record(tops::name(a.data()), {a}, label, [](LMP_BW_ARGS) {          \
+      if (SELF.requires_grad()) SELF.incr_grad(formula);                       \
+    });                                                                        \
+  }
+LMP_AG_UNARY_DEF(neg, "NegationBackward", -G)
+LMP_AG_UNARY_DEF(exp, "ExponentialBackward", out.data() * G)
+LMP_AG_UNARY_DEF(log, "LogarithmBackward", G / SELF.data())
+LMP_AG_UNARY_DEF(sqrt, "SquareRootBackward", G / (out.data() + out.data()))
+LMP_AG_UNARY_DEF(abs, "AbsoluteValueBackward", tops::abs_backward(SELF.data(), G))
+LMP_AG_UNARY_DEF(sin, "SineBackward", G * tops::cos(SELF.data()))
+LMP_AG_UNARY_DEF(cos, "CosineBackward", (-tops::sin(SELF.data())) * G)
+LMP_AG_UNARY_DEF(tan, "TangentBackward", G + (G * out.data() * out.data()))
+#undef LMP_AG_UNARY_DEF
+
+Variable clamp(const Variable& a, Scalar lo, Scalar hi) {
+  return record(tops::clamp(a.data(), lo, hi), {a}, "ClampBackward",
+                [lo, hi](LMP_BW_ARGS) {
+                  if (SELF.requires_grad())
+                    SELF.incr_grad(tops::clamp_backward(SELF.data(), G, lo, hi));
+                });
+}
+
+Variable sum(const Variable& a, size_t axis) {
+  return record(tops::sum(a.data(), axis), {a}, "SummationBackward", [](LMP_BW_ARGS) {
+    if (SELF.requires_grad()) SELF.incr_grad(tensor::ones_like(SELF.data()) * G);
+  });
+}
+
+Variable max(const Variable& a, size_t axis) {
+  return record(tops::max(a.data(), axis), {a}, "MaximumBackward", [](LMP_BW_ARGS) {
+    if (SELF.requires_grad()) SELF.incr_grad(G * tops::eq(SELF.data(), out.data()));
+  });
+}
+
+Variable min(const Variable& a, size_t axis) {
+  return record(tops::min(a.data(), axis), {a}, "MinimumBackward", [](LMP_BW_ARGS) {
+    if (SELF.requires_grad()) SELF.incr_grad(G * tops::eq(SELF.data(), out.data()));
+  });
+}
+
+Variable prod(const Variable& a, size_t axis) {
+  return record(tops::prod(a.data(), axis), {a}, "ProductBackward", [](LMP_BW_ARGS) {
+    if (SELF.requires_grad()) SELF.incr_grad(G * (out.data() / SELF.data()));
+  });
+}
+
+Variable matmul(const Variable& a, const Variable& b) {
+  return record(tops::matmul(a.data(), b.data()), {a, b}, "MatrixMultiplicationBackward",
+                [](LMP_BW_ARGS) {
+                  if (SELF.requires_grad())
+                    SELF.incr_grad(tops::matmul_t(G, OTHER.data(), false, true));
+                  if (OTHER.requires_grad())
+                    OTHER.incr_grad(tops::matmul_t(SELF.data(), G, true, false));
+                });
+}
+
+Variable transpose(const Variable& a) {
+  return record(tops::transpose(a.data()), {a}, "TransposeBackward", [](LMP_BW_ARGS) {
+    if (SELF.requires_grad()) SELF.incr_grad(tops::transpose(G));
+  });
+}
+
+Variable reshape(const Variable& a, const std::vector<size_t>& shape) {
+  return record(tops::reshape(a.data(), shape), {a}, "ReshapeBackward", [](LMP_BW_ARGS) {
+    if (SELF.requires_grad()) SELF.incr_grad(G.reshape(SELF.data().shape()));
+  });
+}
+
+Variable squeeze(const Variable& a, size_t axis) {
+  return record(tops::squeeze(a.data(), axis), {a}, "SqueezeBackward",
+                [axis](LMP_BW_ARGS) {
+                  if (SELF.requires_grad()) SELF.incr_grad(G.expand_dims(axis));
+                });
+}
+
+Variable expand_dims(const Variable& a, size_t axis) {
+  return record(tops::expand_dims(a.data(), axis), {a}, "ExpandDimsBackward",
+                [axis](LMP_BW_ARGS) {
+                  if (SELF.requires_grad()) SELF.incr_grad(G.squeeze(axis));
+                });
+}
+
+Variable to(const Variable& a, DeviceType device) {
+  return record(tops::to(a.data(), device), {a}, "ToBackward", [](LMP_BW_ARGS) {
+    if (SELF.requires_grad()) SELF.incr_grad(G.to(SELF.data().device()));
+  });
+}
+
+#undef G
+#undef SELF
+#undef OTHER
+#undef LMP_BW_ARGS
+
+}  // namespace ops
+
+// ------------------------------------------------------------- constructors
+
+namespace {
+std::mt19937_64& rng() {
+  static std::mt19937_64 g{std::random_device{}()};
+  return g;
+}
+Variable from_values(const std::vector<Scalar>& v, const std::vector<size_t>& shape,
+                     bool rg, DeviceType dev, DataType dt) {
+  return Variable(Tensor(v, shape, dev, dt), rg);
+}
+}  // namespace
+
+void manual_seed(uint64_t seed) { rng().seed(seed); }
+
+Variable zeros(const std::vector<size_t>& shape, bool rg, DeviceType dev, DataType dt) {
+  Tensor t = tensor::empty(shape, dev, dt);
+  t.fill(0.0);
+  return Variable(t, rg);
+}
+
+Variable ones(const std::vector<size_t>& shape, bool rg, DeviceType dev, DataType dt) {
+  Tensor t = tensor::empty(shape, dev, dt);
+  t.fill(1.0);
+  return Variable(t, rg);
+}
+
+Variable rand(const std::vector<size_t>& shape, bool rg, DeviceType dev, DataType dt) {
+  std::vector<Scalar> v(tensor::shape_numel(shape));
+  std::uniform_real_distribution<double> d(0.0, 1.0);
+  for (Scalar& x : v) x = d(rng());
+  return from_values(v, shape, rg, dev, dt);
+}
+
+Variable randn(Scalar mean, Scalar stddev, const std::vector<size_t>& shape, bool rg,
+               DeviceType dev, DataType dt) {
+  std::vector<Scalar> v(tensor::shape_numel(shape));
+  std::normal_distribution<double> d(mean, stddev);
+  for (Scalar& x : v) x = d(rng());
+  return from_values(v, shape, rg, dev, dt);
+}
+
+}  // namespace lmp::autograd

@@ -31,6 +31,13 @@ class CheckFailure {
     os_ << v;
     return *this;
   }
+  template <typename T>
+  CheckFailure& operator<<(const std::vector<T>& v) {
+    os_ << "[";
+    for (size_t i = 0; i < v.size(); ++i) os_ << (i ? ", " : "") << v[i];
+    os_ << "]";
+    return *this;
+  }
   [[noreturn]] void raise() const { throw std::runtime_error(os_.str()); }
 
  private:

@@ -1,0 +1,335 @@
+// Op frontends, the capture flag, lazy nodes, record and realize.
+// Lamp3 counterparts: native/*.cpp, lazy/*.cpp, lazy/functions/*.cpp.
+#include <array>
+#include <cstring>
+#include <iomanip>
+#include <limits>
+#include <sstream>
+
+#include "ops.hpp"
+
+namespace lmp::tensor {
+
+BackendStats& backend_stats() {
+  static BackendStats s;
+  return s;
+}
+
+namespace ops {
+
+#define LMP_DEF_STUB_BINARY(name) LMP_DEFINE_DISPATCH(binary_fn, name##_stub)
+#define LMP_DEF_STUB_UNARY(name) LMP_DEFINE_DISPATCH(unary_fn, name##_stub)
+#define LMP_DEF_STUB_REDUCT(name) LMP_DEFINE_DISPATCH(reduct_fn, name##_stub)
+LMP_FOR_BINARY_OPS(LMP_DEF_STUB_BINARY)
+LMP_FOR_UNARY_OPS(LMP_DEF_STUB_UNARY)
+LMP_FOR_REDUCT_OPS(LMP_DEF_STUB_REDUCT)
+LMP_DEFINE_DISPATCH(clamp_fn, clamp_stub)
+LMP_DEFINE_DISPATCH(abs_backward_fn, abs_backward_stub)
+LMP_DEFINE_DISPATCH(clamp_backward_fn, clamp_backward_stub)
+LMP_DEFINE_DISPATCH(matmul_fn, matmul_stub)
+LMP_DEFINE_DISPATCH(transpose_fn, transpose_stub)
+LMP_DEFINE_DISPATCH(matmul_t_fn, matmul_t_stub)
+
+namespace {
+using Acc = detail::UnsafeTensorAccessor;
+
+Tensor wrap(TensorImpl&& t) {
+  return Acc::fromImpl(std::make_shared<TensorImpl>(std::move(t)));
+}
+}  // namespace
+
+// Binary ops: record under capture, else run the device stub.
+#define LMP_DEF_BINARY(name, CODE)                                           \
+  Tensor name(const Tensor& a, const Tensor& b) {                            \
+    LMP_CHECK(a.device() == b.device()) << "Tensors are on different devices"; \
+    const auto& ai = Acc::getImpl(a);                                        \
+    const auto& bi = Acc::getImpl(b);                                        \
+    if (lazy::should_capture(a.device()))                                    \
+      return Acc::fromImpl(lazy::record(lazy::make_binary(CODE, ai, bi)));   \
+    return wrap(name##_stub()(a.device(), *ai, *bi));                        \
+  }
+LMP_DEF_BINARY(add, LMP_BIN_ADD)
+LMP_DEF_BINARY(sub, LMP_BIN_SUB)
+LMP_DEF_BINARY(mul, LMP_BIN_MUL)
+LMP_DEF_BINARY(div, LMP_BIN_DIV)
+LMP_DEF_BINARY(pow, LMP_BIN_POW)
+LMP_DEF_BINARY(eq, LMP_BIN_EQ)
+LMP_DEF_BINARY(ne, LMP_BIN_NE)
+LMP_DEF_BINARY(ge, LMP_BIN_GE)
+LMP_DEF_BINARY(le, LMP_BIN_LE)
+LMP_DEF_BINARY(gt, LMP_BIN_GT)
+LMP_DEF_BINARY(lt, LMP_BIN_LT)
+#undef LMP_DEF_BINARY
+
+#define LMP_DEF_UNARY(name, CODE)                                         \
+  Tensor name(const Tensor& a) {                                          \
+    const auto& ai = Acc::getImpl(a);                                     \
+    if (lazy::should_capture(a.device()))                                 \
+      return Acc::fromImpl(lazy::record(lazy::make_unary(CODE, ai)));     \
+    return wrap(name##_stub()(a.device(), *ai));                          \
+  }
+LMP_DEF_UNARY(neg, LMP_UN_NEG)
+LMP_DEF_UNARY(exp, LMP_UN_EXP)
+LMP_DEF_UNARY(log, LMP_UN_LOG)
+LMP_DEF_UNARY(sqrt, LMP_UN_SQRT)
+LMP_DEF_UNARY(abs, LMP_UN_ABS)
+LMP_DEF_UNARY(sin, LMP_UN_SIN)
+LMP_DEF_UNARY(cos, LMP_UN_COS)
+LMP_DEF_UNARY(tan, LMP_UN_TAN)
+#undef LMP_DEF_UNARY
+
+Tensor clamp(const Tensor& a, Scalar lo, Scalar hi) {
+  const auto& ai = Acc::getImpl(a);
+  if (lazy::should_capture(a.device()))
+    return Acc::fromImpl(lazy::record(lazy::make_unary(LMP_UN_CLAMP, ai, lo, hi)));
+  return wrap(clamp_stub()(a.device(), *ai, lo, hi));
+}
+
+Tensor abs_backward(const Tensor& input, const Tensor& grad) {
+  LMP_CHECK(input.device() == grad.device())
+      << "abs_backward requires tensors on the same device";
+  LMP_CHECK(input.shape() == grad.shape())
+      << "abs_backward requires tensors with identical shapes";
+  LMP_CHECK(input.type() == grad.type())
+      << "abs_backward requires tensors with identical dtypes";
+  return wrap(abs_backward_stub()(input.device(), *Acc::getImpl(input),
+                                  *Acc::getImpl(grad)));
+}
+
+Tensor clamp_backward(const Tensor& input, const Tensor& grad, Scalar lo, Scalar hi) {
+  LMP_CHECK(input.device() == grad.device())
+      << "clamp_backward requires tensors on the same device";
+  LMP_CHECK(input.shape() == grad.shape())
+      << "clamp_backward requires tensors with identical shapes";
+  LMP_CHECK(input.type() == grad.type())
+      << "clamp_backward requires tensors with identical dtypes";
+  return wrap(clamp_backward_stub()(input.device(), *Acc::getImpl(input),
+                                    *Acc::getImpl(grad), lo, hi));
+}
+
+#define LMP_DEF_REDUCT(name)                                               \
+  Tensor name(const Tensor& a, size_t axis) {                              \
+    return wrap(name##_stub()(a.device(), *Acc::getImpl(a), axis));        \
+  }
+LMP_FOR_REDUCT_OPS(LMP_DEF_REDUCT)
+#undef LMP_DEF_REDUCT
+
+Tensor matmul(const Tensor& a, const Tensor& b) {
+  LMP_CHECK(a.device() == b.device()) << "Tensors must be on the same device";
+  return wrap(matmul_stub()(a.device(), *Acc::getImpl(a), *Acc::getImpl(b)));
+}
+
+Tensor matmul_t(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b) {
+  LMP_CHECK(a.device() == b.device()) << "Tensors must be on the same device";
+  if (!matmul_t_stub().has(a.device())) {
+    // Backends without the fused form: materialise the transposes.
+    return matmul(trans_a ? transpose(a) : a, trans_b ? transpose(b) : b);
+  }
+  return wrap(matmul_t_stub()(a.device(), *Acc::getImpl(a), *Acc::getImpl(b),
+                              trans_a, trans_b));
+}
+
+Tensor transpose(const Tensor& a) {
+  return wrap(transpose_stub()(a.device(), *Acc::getImpl(a)));
+}
+
+Tensor reshape(const Tensor& a, std::vector<size_t> shape) {
+  return wrap(Acc::getImpl(a)->reshape(std::move(shape)));
+}
+Tensor squeeze(const Tensor& a, size_t dim) { return wrap(Acc::getImpl(a)->squeeze(dim)); }
+Tensor expand_dims(const Tensor& a, size_t dim) {
+  return wrap(Acc::getImpl(a)->expand_dims(dim));
+}
+
+Tensor to(const Tensor& a, DeviceType device) {
+  LMP_CHECK(a.device() != device)
+      << "Device argument must be different from current device.";
+  Tensor out = empty(a.shape(), device, a.type());
+  if (a.numel()) {
+    void* src = const_cast<Tensor&>(a).data();
+    copy_stub()(a.device(), device, src, out.data(), a.numel(), a.type(), a.type());
+  }
+  return out;
+}
+
+void add_inplace(Tensor& dst, const Tensor& src) {
+  LMP_CHECK(dst.device() == src.device())
+      << "add_inplace requires tensors on the same device";
+  LMP_CHECK(dst.shape() == src.shape())
+      << "add_inplace requires tensors with identical shapes";
+  LMP_CHECK(dst.type() == src.type())
+      << "add_inplace requires tensors with identical dtypes";
+  void* s = const_cast<Tensor&>(src).data();
+  add_inplace_stub()(dst.device(), dst.data(), s, dst.numel(), dst.type());
+}
+
+}  // namespace ops
+
+// --------------------------------------------------------------------- lazy
+
+namespace lazy {
+
+namespace {
+thread_local bool t_capture = false;
+
+std::array<LazyBackend*, static_cast<size_t>(DeviceType::Count)>& registry() {
+  static std::array<LazyBackend*, static_cast<size_t>(DeviceType::Count)> r{};
+  return r;
+}
+
+// A Scalar bound converted to float on the host, as the eager launch does,
+// and spelled by its bit pattern so inf (from DBL_MAX) and -0.0 survive.
+std::string float_literal(Scalar v) {
+  const float f = static_cast<float>(v);
+  uint32_t bits;
+  std::memcpy(&bits, &f, sizeof bits);
+  std::ostringstream os;
+  os << "__uint_as_float(0x" << std::hex << bits << "u)";
+  return os.str();
+}
+
+struct BinaryFn : LazyFunction {
+  int op;
+  BinaryFn(int code, std::vector<std::shared_ptr<TensorImpl>> ins)
+      : LazyFunction(std::move(ins)), op(code) {}
+  std::shared_ptr<TensorImpl> infer_output() const override {
+    OpMeta m = infer_binary(*inputs[0], *inputs[1]);
+    return std::make_shared<TensorImpl>(Storage(0, inputs[0]->device()), m.shape,
+                                        m.dtype);
+  }
+  // Broadcast-compatible operands fuse too (the reference fuses only
+  // equal shapes, elementwise_binary.cpp:11-13).
+  bool is_fusible() const override { return true; }
+  OpKind kind() const override { return OpKind::Binary; }
+  int code() const override { return op; }
+  void run_eager(TensorImpl& out) override {
+    using namespace ops;
+    const DeviceType d = inputs[0]->device();
+    TensorImpl r = [&]() -> TensorImpl {
+      switch (op) {
+        case LMP_BIN_ADD: return add_stub()(d, *inputs[0], *inputs[1]);
+        case LMP_BIN_SUB: return sub_stub()(d, *inputs[0], *inputs[1]);
+        case LMP_BIN_MUL: return mul_stub()(d, *inputs[0], *inputs[1]);
+        case LMP_BIN_DIV: return div_stub()(d, *inputs[0], *inputs[1]);
+        case LMP_BIN_POW: return pow_stub()(d, *inputs[0], *inputs[1]);
+        case LMP_BIN_EQ: return eq_stub()(d, *inputs[0], *inputs[1]);
+        case LMP_BIN_NE: return ne_stub()(d, *inputs[0], *inputs[1]);
+        case LMP_BIN_GE: return ge_stub()(d, *inputs[0], *inputs[1]);
+        case LMP_BIN_LE: return le_stub()(d, *inputs[0], *inputs[1]);
+        case LMP_BIN_GT: return gt_stub()(d, *inputs[0], *inputs[1]);
+        default: return lt_stub()(d, *inputs[0], *inputs[1]);
+      }
+    }();
+    out.set_realized(r.storage());
+  }
+  std::string codegen_expr() const override {
+    switch (op) {
+      case LMP_BIN_ADD: return "({0} + {1})";
+      case LMP_BIN_SUB: return "({0} - {1})";
+      case LMP_BIN_MUL: return "({0} * {1})";
+      case LMP_BIN_DIV: return "({0} / {1})";
+      case LMP_BIN_POW: return "powf({0}, {1})";
+      case LMP_BIN_EQ: return "({0} == {1} ? 1.0f : 0.0f)";
+      case LMP_BIN_NE: return "({0} != {1} ? 1.0f : 0.0f)";
+      case LMP_BIN_GE: return "({0} >= {1} ? 1.0f : 0.0f)";
+      case LMP_BIN_LE: return "({0} <= {1} ? 1.0f : 0.0f)";
+      case LMP_BIN_GT: return "({0} > {1} ? 1.0f : 0.0f)";
+      default: return "({0} < {1} ? 1.0f : 0.0f)";
+    }
+  }
+};
+
+struct UnaryFn : LazyFunction {
+  int op;
+  Scalar lo, hi;
+  UnaryFn(int code, std::vector<std::shared_ptr<TensorImpl>> ins, Scalar p0, Scalar p1)
+      : LazyFunction(std::move(ins)), op(code), lo(p0), hi(p1) {}
+  std::shared_ptr<TensorImpl> infer_output() const override {
+    return std::make_shared<TensorImpl>(Storage(0, inputs[0]->device()),
+                                        inputs[0]->shape(), inputs[0]->type());
+  }
+  bool is_fusible() const override { return true; }
+  OpKind kind() const override { return OpKind::Unary; }
+  int code() const override { return op; }
+  Scalar param0() const override { return lo; }
+  Scalar param1() const override { return hi; }
+  void run_eager(TensorImpl& out) override {
+    using namespace ops;
+    const DeviceType d = inputs[0]->device();
+    TensorImpl r = [&]() -> TensorImpl {
+      switch (op) {
+        case LMP_UN_NEG: return neg_stub()(d, *inputs[0]);
+        case LMP_UN_EXP: return exp_stub()(d, *inputs[0]);
+        case LMP_UN_LOG: return log_stub()(d, *inputs[0]);
+        case LMP_UN_SQRT: return sqrt_stub()(d, *inputs[0]);
+        case LMP_UN_ABS: return abs_stub()(d, *inputs[0]);
+        case LMP_UN_SIN: return sin_stub()(d, *inputs[0]);
+        case LMP_UN_COS: return cos_stub()(d, *inputs[0]);
+        case LMP_UN_TAN: return tan_stub()(d, *inputs[0]);
+        default: return clamp_stub()(d, *inputs[0], lo, hi);
+      }
+    }();
+    out.set_realized(r.storage());
+  }
+  // Same functions as the eager kernels.  abs is fabsf (the eager CPU and
+  // GPU functor), which maps -0.0 to +0.0; the reference's fused spelling
+  // `x < 0 ? -x : x` would keep -0.0 and disagree with its own eager path.
+  std::string codegen_expr() const override {
+    switch (op) {
+      case LMP_UN_NEG: return "(-{0})";
+      case LMP_UN_EXP: return "expf({0})";
+      case LMP_UN_LOG: return "logf({0})";
+      case LMP_UN_SQRT: return "sqrtf({0})";
+      case LMP_UN_ABS: return "fabsf({0})";
+      case LMP_UN_SIN: return "sinf({0})";
+      case LMP_UN_COS: return "cosf({0})";
+      case LMP_UN_TAN: return "tanf({0})";
+      default:
+        return "lmp_clamp({0}, " + float_literal(lo) + ", " + float_literal(hi) + ")";
+    }
+  }
+};
+
+}  // namespace
+
+bool is_capture_enabled() { return t_capture; }
+void set_capture_enabled(bool enable) { t_capture = enable; }
+bool should_capture(DeviceType device) {
+  return t_capture && backend(device) != nullptr;
+}
+CaptureGuard::CaptureGuard(bool enable) : prev_(t_capture) { t_capture = enable; }
+CaptureGuard::~CaptureGuard() { t_capture = prev_; }
+
+LazyBackend* backend(DeviceType dev) { return registry()[static_cast<size_t>(dev)]; }
+void register_backend(DeviceType dev, LazyBackend* b) {
+  registry()[static_cast<size_t>(dev)] = b;
+}
+
+std::shared_ptr<TensorImpl> record(std::shared_ptr<LazyFunction> fn) {
+  std::shared_ptr<TensorImpl> out = fn->infer_output();
+  out->set_deferred(std::move(fn));
+  return out;
+}
+
+void realize(TensorImpl* t) {
+  if (!t->is_deferred()) return;
+  LazyBackend* b = backend(t->device());
+  LMP_CHECK(b != nullptr) << "no lazy backend registered for device";
+  b->realize(t);
+}
+
+std::shared_ptr<LazyFunction> make_binary(int code, std::shared_ptr<TensorImpl> a,
+                                          std::shared_ptr<TensorImpl> b) {
+  LMP_CHECK(a->device() == b->device()) << "Tensors are on different devices";
+  return std::make_shared<BinaryFn>(
+      code, std::vector<std::shared_ptr<TensorImpl>>{std::move(a), std::move(b)});
+}
+
+std::shared_ptr<LazyFunction> make_unary(int code, std::shared_ptr<TensorImpl> a,
+                                         Scalar p0, Scalar p1) {
+  return std::make_shared<UnaryFn>(code, std::vector<std::shared_ptr<TensorImpl>>{std::move(a)},
+                                   p0, p1);
+}
+
+}  // namespace lazy
+}  // namespace lmp::tensor

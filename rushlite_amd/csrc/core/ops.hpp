@@ -1,0 +1,191 @@
+// Native op frontend, broadcast metadata and the lazy-capture layer.
+//
+// Each elementwise frontend checks the capture mode, then either records a
+// LazyFunction node (deferred tensor) or calls its device stub
+// (native/expand_ops.cpp:28-39, native/unary_ops.cpp:23-33).  Reductions,
+// matmul, transpose, views and memory ops are never captured; reading their
+// inputs realises any pending graph (tensor_impl.cpp:33-36).
+#pragma once
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "tensor.hpp"
+
+namespace lmp::tensor {
+
+// ------------------------------------------------------------- metadata
+
+// Right-aligned broadcast of two shapes (align_utils.cpp:18-40).
+std::vector<size_t> broadcast_shapes(const std::vector<size_t>& a,
+                                     const std::vector<size_t>& b);
+// Contiguous strides of `in` aligned to `nd` output dims, 0 on size-1 dims
+// (cpu/offset_util.cpp:7-28).
+std::vector<stride_t> padded_strides(const std::vector<size_t>& in, size_t nd);
+
+struct OpMeta {  // infer_meta.cpp:10-44
+  DataType dtype;
+  std::vector<size_t> shape;
+  size_t size;
+  bool expand;
+};
+OpMeta infer_unary(const TensorImpl& a);
+OpMeta infer_binary(const TensorImpl& a, const TensorImpl& b);
+OpMeta infer_reduct(const TensorImpl& a, size_t axis);
+
+// ------------------------------------------------------------ dispatch
+
+namespace ops {
+
+using binary_fn = TensorImpl (*)(const TensorImpl&, const TensorImpl&);
+using unary_fn = TensorImpl (*)(const TensorImpl&);
+using clamp_fn = TensorImpl (*)(const TensorImpl&, Scalar, Scalar);
+using abs_backward_fn = TensorImpl (*)(const TensorImpl&, const TensorImpl&);
+using clamp_backward_fn = TensorImpl (*)(const TensorImpl&, const TensorImpl&,
+                                         Scalar, Scalar);
+using reduct_fn = TensorImpl (*)(const TensorImpl&, size_t);
+using matmul_fn = TensorImpl (*)(const TensorImpl&, const TensorImpl&);
+using transpose_fn = TensorImpl (*)(const TensorImpl&);
+// C = op(A) * op(B) with either operand transposed in place of a
+// materialised transpose; the reference spells these transpose + matmul
+// (functions/matrix_ops.cpp:15-20).
+using matmul_t_fn = TensorImpl (*)(const TensorImpl&, const TensorImpl&, bool,
+                                   bool);
+
+#define LMP_FOR_BINARY_OPS(_) \
+  _(add) _(sub) _(mul) _(div) _(pow) _(eq) _(ne) _(ge) _(le) _(gt) _(lt)
+#define LMP_FOR_UNARY_OPS(_) _(neg) _(exp) _(log) _(sqrt) _(abs) _(sin) _(cos) _(tan)
+#define LMP_FOR_REDUCT_OPS(_) _(sum) _(max) _(min) _(prod)
+
+#define LMP_DECL_BINARY(name)                     \
+  LMP_DECLARE_DISPATCH(binary_fn, name##_stub)    \
+  Tensor name(const Tensor& a, const Tensor& b);
+#define LMP_DECL_UNARY(name)                   \
+  LMP_DECLARE_DISPATCH(unary_fn, name##_stub)  \
+  Tensor name(const Tensor& a);
+#define LMP_DECL_REDUCT(name)                  \
+  LMP_DECLARE_DISPATCH(reduct_fn, name##_stub) \
+  Tensor name(const Tensor& a, size_t axis);
+
+LMP_FOR_BINARY_OPS(LMP_DECL_BINARY)
+LMP_FOR_UNARY_OPS(LMP_DECL_UNARY)
+LMP_FOR_REDUCT_OPS(LMP_DECL_REDUCT)
+#undef LMP_DECL_BINARY
+#undef LMP_DECL_UNARY
+#undef LMP_DECL_REDUCT
+
+LMP_DECLARE_DISPATCH(clamp_fn, clamp_stub)
+LMP_DECLARE_DISPATCH(abs_backward_fn, abs_backward_stub)
+LMP_DECLARE_DISPATCH(clamp_backward_fn, clamp_backward_stub)
+LMP_DECLARE_DISPATCH(matmul_fn, matmul_stub)
+LMP_DECLARE_DISPATCH(transpose_fn, transpose_stub)
+LMP_DECLARE_DISPATCH(matmul_t_fn, matmul_t_stub)
+
+Tensor clamp(const Tensor& a, Scalar lo, Scalar hi);
+Tensor abs_backward(const Tensor& input, const Tensor& grad);
+Tensor clamp_backward(const Tensor& input, const Tensor& grad, Scalar lo, Scalar hi);
+Tensor matmul(const Tensor& a, const Tensor& b);
+// op(a) @ op(b): trans_a uses a^T, trans_b uses b^T (2-D only).
+Tensor matmul_t(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b);
+Tensor transpose(const Tensor& a);
+Tensor reshape(const Tensor& a, std::vector<size_t> shape);
+Tensor squeeze(const Tensor& a, size_t dim);
+Tensor expand_dims(const Tensor& a, size_t dim);
+Tensor to(const Tensor& a, DeviceType device);
+void add_inplace(Tensor& dst, const Tensor& src);
+
+}  // namespace ops
+
+// Tensor-level operators with scalar overloads; a scalar becomes a [1] tensor
+// of the other operand's dtype and device (native/overloads.hpp:16-28).
+Tensor scalar_like(const Tensor& t, Scalar s);
+#define LMP_TENSOR_OPERATOR(sym, fn)                                        \
+  inline Tensor operator sym(const Tensor& a, const Tensor& b) { return ops::fn(a, b); } \
+  inline Tensor operator sym(const Tensor& a, Scalar s) {                   \
+    return ops::fn(a, scalar_like(a, s));                                   \
+  }                                                                         \
+  inline Tensor operator sym(Scalar s, const Tensor& a) {                   \
+    return ops::fn(scalar_like(a, s), a);                                   \
+  }
+LMP_TENSOR_OPERATOR(+, add)
+LMP_TENSOR_OPERATOR(-, sub)
+LMP_TENSOR_OPERATOR(*, mul)
+LMP_TENSOR_OPERATOR(/, div)
+LMP_TENSOR_OPERATOR(==, eq)
+LMP_TENSOR_OPERATOR(!=, ne)
+LMP_TENSOR_OPERATOR(>=, ge)
+LMP_TENSOR_OPERATOR(<=, le)
+LMP_TENSOR_OPERATOR(>, gt)
+LMP_TENSOR_OPERATOR(<, lt)
+#undef LMP_TENSOR_OPERATOR
+inline Tensor operator-(const Tensor& a) { return ops::neg(a); }
+
+// ---------------------------------------------------------------- lazy
+
+namespace lazy {
+
+// Capture flag, thread-local (capture_mode.cpp:7-22).
+bool is_capture_enabled();
+void set_capture_enabled(bool enable);
+bool should_capture(DeviceType device);
+class CaptureGuard {
+ public:
+  explicit CaptureGuard(bool enable);
+  ~CaptureGuard();
+
+ private:
+  bool prev_;
+};
+
+// Elementwise op codes shared by the lazy nodes, the structural graph hash
+// and the code generator; values equal lmp_binary_op / lmp_unary_op.
+enum class OpKind : uint8_t { Binary, Unary };
+
+// A deferred elementwise node (lazy_function.hpp:11-22).  codegen_expr()
+// returns the node's expression with {0}/{1} for its operands, in the HIP
+// spelling that matches the eager kernels' functors bit for bit.
+struct LazyFunction {
+  std::vector<std::shared_ptr<TensorImpl>> inputs;
+  explicit LazyFunction(std::vector<std::shared_ptr<TensorImpl>> ins)
+      : inputs(std::move(ins)) {}
+  virtual ~LazyFunction() = default;
+  virtual std::shared_ptr<TensorImpl> infer_output() const = 0;
+  virtual void run_eager(TensorImpl& out) = 0;
+  virtual std::string codegen_expr() const = 0;
+  virtual bool is_fusible() const = 0;
+  virtual OpKind kind() const = 0;
+  virtual int code() const = 0;  // lmp_binary_op or lmp_unary_op value
+  virtual Scalar param0() const { return 0; }
+  virtual Scalar param1() const { return 0; }
+};
+
+struct LazyBackend {  // lazy_backend.hpp:15-35
+  virtual ~LazyBackend() = default;
+  virtual void realize(TensorImpl* t) = 0;
+};
+LazyBackend* backend(DeviceType dev);
+void register_backend(DeviceType dev, LazyBackend* b);
+
+std::shared_ptr<TensorImpl> record(std::shared_ptr<LazyFunction> fn);
+void realize(TensorImpl* t);
+
+std::shared_ptr<LazyFunction> make_binary(int code,
+                                          std::shared_ptr<TensorImpl> a,
+                                          std::shared_ptr<TensorImpl> b);
+std::shared_ptr<LazyFunction> make_unary(int code, std::shared_ptr<TensorImpl> a,
+                                         Scalar p0 = 0, Scalar p1 = 0);
+
+}  // namespace lazy
+
+// Backend counters (launches and JIT activity), exposed for tests/bench.
+struct BackendStats {
+  uint64_t eager_launches = 0;
+  uint64_t fused_launches = 0;
+  uint64_t fused_nodes = 0;
+  uint64_t jit_compiles = 0;
+  uint64_t jit_cache_hits = 0;
+};
+BackendStats& backend_stats();
+
+}  // namespace lmp::tensor
