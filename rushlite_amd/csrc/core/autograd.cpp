@@ -35,7 +35,6 @@ Variable::Variable(const Tensor& data, bool requires_grad)
     : impl_(std::make_shared<VariableImpl>()) {
   impl_->data = data;
   impl_->requires_grad = requires_grad;
-  if (requires_grad) impl_->grad = tensor::zeros_like(data);
 }
 
 Variable Variable::op_result(const Tensor& data, bool requires_grad) {
@@ -54,8 +53,11 @@ const Tensor& Variable::grad() const {
 
 void Variable::zero_grad() {
   LMP_CHECK(requires_grad()) << "Cannot access grad() if requires_grad = false";
-  impl_->grad = tensor::zeros_like(impl_->data);
-  impl_->grad_fn = nullptr;  // variable.cpp:25-29
+  // variable.cpp:25-29 installs a fresh zero tensor; leaving the gradient
+  // unset is observably the same (grad() materialises zeros, the next
+  // accumulation writes 0 + g) and saves a fill per parameter per step.
+  impl_->grad = Tensor();
+  impl_->grad_fn = nullptr;
 }
 
 namespace {
@@ -79,6 +81,19 @@ void Variable::incr_grad(const Tensor& g) {
   LMP_INTERNAL_ASSERT(g.shape() == impl_->grad.shape())
       << "There should be no broadcasting in incr_grad";
   tops::add_inplace(impl_->grad, g);  // variable.cpp:30-35
+}
+
+void Variable::incr_grad_matmul(const Tensor& a, const Tensor& b, bool trans_a,
+                                bool trans_b) {
+  LMP_CHECK(requires_grad()) << "Cannot access grad() if requires_grad = false";
+  if (!impl_->grad.defined()) {
+    // A GEMM accumulates from +0, so its product equals 0 + product exactly.
+    impl_->grad = tops::matmul_t(a, b, trans_a, trans_b);
+    LMP_INTERNAL_ASSERT(impl_->grad.shape() == impl_->data.shape())
+        << "There should be no broadcasting in incr_grad";
+    return;
+  }
+  tops::matmul_acc(impl_->grad, a, b, trans_a, trans_b);
 }
 
 void Variable::set_grad_fn(std::shared_ptr<Function> fn) {
@@ -288,10 +303,8 @@ Variable prod(const Variable& a, size_t axis) {
 Variable matmul(const Variable& a, const Variable& b) {
   return record(tops::matmul(a.data(), b.data()), {a, b}, "MatrixMultiplicationBackward",
                 [](LMP_BW_ARGS) {
-                  if (SELF.requires_grad())
-                    SELF.incr_grad(tops::matmul_t(G, OTHER.data(), false, true));
-                  if (OTHER.requires_grad())
-                    OTHER.incr_grad(tops::matmul_t(SELF.data(), G, true, false));
+                  if (SELF.requires_grad()) SELF.incr_grad_matmul(G, OTHER.data(), false, true);
+                  if (OTHER.requires_grad()) OTHER.incr_grad_matmul(SELF.data(), G, true, false);
                 });
 }
 

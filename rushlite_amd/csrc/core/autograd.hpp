@@ -33,11 +33,13 @@ class GradGuard {
 
 struct VariableImpl {
   Tensor data;
-  // The gradient.  Leaves built with requires_grad=True hold a zero tensor
-  // from construction (variable.hpp:24-28), so its storage is stable across
-  // backward passes.  Op results defer it: the first accumulation writes
-  // 0 + g into a fresh buffer, which equals accumulating into zeros bit for
-  // bit without the separate fill; reading .grad first materialises zeros.
+  // The gradient, materialised on demand.  Lamp3 allocates a zero tensor
+  // when a variable with requires_grad is made (variable.hpp:24-28); here the
+  // first accumulation instead writes 0 + g into a fresh buffer (or the GEMM
+  // product straight into it), equal bit for bit to zeros + g without the
+  // fill pass, and reading .grad before any accumulation materialises the
+  // zeros.  Once it exists the buffer stays put: later accumulations are in
+  // place, so a pointer taken from .grad stays valid across backward passes.
   Tensor grad;
   std::shared_ptr<Function> grad_fn;
   bool requires_grad = false;
@@ -57,6 +59,8 @@ class Variable {
 
   void zero_grad();
   void incr_grad(const Tensor& g);
+  // grad += op(a) @ op(b), fused into the GEMM epilogue.
+  void incr_grad_matmul(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b);
   void set_grad_fn(std::shared_ptr<Function> fn);
   void copy(const Variable& other);
   void fill(Scalar value);

@@ -109,6 +109,16 @@ void copy_cpu(DeviceType to, const void* src, void* dst, size_t n, DataType st,
     convert_host(src, dst, n, st, dt);
     return;
   }
+  // A single value (Python scalars become [1] tensors) goes down as a kernel
+  // argument of a fill launch: stream-ordered, no host synchronisation.  The
+  // host-side conversion to the destination dtype equals the device cast.
+  if (n == 1 && st != DataType::Int64) {
+    double v = 0;
+    convert_host(src, &v, 1, st, DataType::Float64);
+    count_launch();
+    hip_ok(lmp_k_fill(code(dt), dst, 1, v), "lmp_k_fill");
+    return;
+  }
   if (st == dt) {
     hip_ok(lmp_rt_memcpy_h2d(dst, src, n * dtype_size(st)), "memcpy h2d");
     return;
@@ -263,6 +273,30 @@ TensorImpl matmul_t_hip(const TensorImpl& a, const TensorImpl& b, bool ta, bool 
   return gemm_hip(a, b, ta, tb);
 }
 
+void matmul_acc_hip(TensorImpl& c, const TensorImpl& a, const TensorImpl& b, bool ta,
+                    bool tb) {
+  LMP_CHECK(a.shape().size() == 2 && b.shape().size() == 2 && c.shape().size() == 2)
+      << "Both matrices must be 2D.";
+  const size_t m = ta ? a.shape()[1] : a.shape()[0];
+  const size_t k = ta ? a.shape()[0] : a.shape()[1];
+  const size_t kb = tb ? b.shape()[1] : b.shape()[0];
+  const size_t n = tb ? b.shape()[0] : b.shape()[1];
+  LMP_CHECK(k == kb) << "Incompatible matrix dimensions for multiplication.";
+  LMP_CHECK(c.shape()[0] == m && c.shape()[1] == n) << "matmul_acc: output shape mismatch";
+  LMP_CHECK(a.type() == DataType::Float32 && b.type() == DataType::Float32 &&
+            c.type() == DataType::Float32)
+      << "matmul on the HIP device supports Float32";
+  if (!m || !n) return;
+  void* pa = mut(a);
+  void* pb = mut(b);
+  void* pc = c.data();
+  count_launch();
+  hip_ok(lmp_k_gemm_f32(ta, tb, m, n, k, static_cast<const float*>(pa), a.shape()[1],
+                        static_cast<const float*>(pb), b.shape()[1], static_cast<float*>(pc),
+                        n, 1),
+         "lmp_k_gemm_f32");
+}
+
 TensorImpl transpose_hip(const TensorImpl& a) {
   LMP_CHECK(a.shape().size() == 2)
       << "Invalid argument, transpose can only be performed on matrices of dim 2";
@@ -337,6 +371,7 @@ LMP_REGISTER_DISPATCH(abs_backward_stub, kHip, abs_backward_hip)
 LMP_REGISTER_DISPATCH(clamp_backward_stub, kHip, clamp_backward_hip)
 LMP_REGISTER_DISPATCH(matmul_stub, kHip, matmul_hip)
 LMP_REGISTER_DISPATCH(matmul_t_stub, kHip, matmul_t_hip)
+LMP_REGISTER_DISPATCH(matmul_acc_stub, kHip, matmul_acc_hip)
 LMP_REGISTER_DISPATCH(transpose_stub, kHip, transpose_hip)
 
 }  // namespace lmp::tensor::hip

@@ -15,9 +15,10 @@
 // with no source text built.  On a miss the region is turned into HIP source
 // specialised to its shape: the layout is coalesced to the fewest dims, and
 // when it reduces to rows x cols with each leaf contiguous or broadcast along
-// the row, the kernel moves 128-bit vectors (four per lane per step) and
-// stores with nontemporal hints; otherwise it decomposes the flat index with
-// compile-time extents.  Kernels launch on the library stream without a
+// the row, each lane of a one-shot grid produces one float4 (a workgroup owns
+// a contiguous 4 KiB output tile) from 128-bit loads and stores it with a
+// nontemporal hint; otherwise it decomposes the flat index with compile-time
+// extents.  Kernels launch on the library stream without a
 // device synchronisation (the reference synchronises every launch,
 // nvrtc_backend.cpp:135-141).
 #include <cstring>
@@ -34,7 +35,6 @@ namespace {
 constexpr size_t kMaxNodes = 96;
 constexpr size_t kMaxLeaves = 16;
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
 
 struct Region {
   std::vector<TensorImpl*> leaves;
@@ -230,49 +230,37 @@ std::string codegen(const Region& r, const Plan& p, const std::string& name) {
   os << ") {\n";
   const size_t nl = r.leaves.size();
   if (p.vec) {
+    // One-shot: workgroup b owns output float4s [256b, 256b + 256).
     const bool rows = p.groups.size() == 2;
-    os << "  const unsigned nvec = " << p.nvec << "u;\n";
-    os << "  const unsigned stride = gridDim.x * " << kBlock << "u;\n";
-    os << "  for (unsigned v0 = blockIdx.x * " << kBlock
-       << "u + threadIdx.x; v0 < nvec; v0 += stride * " << kUnroll << "u) {\n";
-    os << "    unsigned w[" << kUnroll << "];\n";
-    for (size_t l = 0; l < nl; ++l) {
-      const bool contig = !p.groups.empty() && p.groups[0].stride[l] == 1;
-      os << "    " << (contig ? "lmp_v4" : "float") << " s" << l << "[" << kUnroll << "];\n";
-    }
-    os << "#pragma unroll\n    for (int u = 0; u < " << kUnroll << "; ++u) {\n";
-    os << "      unsigned v = v0 + u * stride;\n      w[u] = v;\n";
-    os << "      if (v >= nvec) v = v0;\n";
+    os << "  const unsigned v = blockIdx.x * " << kBlock << "u + threadIdx.x;\n";
+    os << "  if (v >= " << p.nvec << "u) return;\n";
     if (rows) {
-      os << "      const unsigned r = v / " << p.cols4 << "u;\n";
-      os << "      const unsigned c = (v - r * " << p.cols4 << "u) * 4u;\n";
+      os << "  const unsigned r = v / " << p.cols4 << "u;\n";
+      os << "  const unsigned c = (v - r * " << p.cols4 << "u) * 4u;\n";
     } else {
-      os << "      const unsigned r = 0u;\n      const unsigned c = v * 4u;\n";
+      os << "  const unsigned r = 0u;\n  const unsigned c = v * 4u;\n";
     }
     for (size_t l = 0; l < nl; ++l) {
       const bool contig = !p.groups.empty() && p.groups[0].stride[l] == 1;
       const int64_t rs = rows ? p.groups[1].stride[l] : 0;
-      os << "      s" << l << "[u] = ";
       if (contig)
-        os << "*reinterpret_cast<const lmp_v4*>(in" << l << " + (unsigned long)r * " << rs
-           << "ul + c);\n";
+        os << "  const lmp_v4 s" << l << " = *reinterpret_cast<const lmp_v4*>(in" << l
+           << " + (unsigned long)r * " << rs << "ul + c);\n";
       else
-        os << "in" << l << "[(unsigned long)r * " << rs << "ul];\n";
+        os << "  const float s" << l << " = in" << l << "[(unsigned long)r * " << rs
+           << "ul];\n";
     }
-    os << "    }\n";
-    os << "#pragma unroll\n    for (int u = 0; u < " << kUnroll << "; ++u) {\n";
-    os << "      if (w[u] >= nvec) continue;\n      lmp_v4 o;\n";
+    os << "  lmp_v4 o;\n";
     const char* comp[4] = {"x", "y", "z", "w"};
     for (int c = 0; c < 4; ++c) {
-      os << "      {\n";
-      emit_chain(os, r, "        ", std::string("o.") + comp[c], [&](int l) {
+      os << "  {\n";
+      emit_chain(os, r, "    ", std::string("o.") + comp[c], [&](int l) {
         const bool contig = !p.groups.empty() && p.groups[0].stride[l] == 1;
-        return "s" + std::to_string(l) + "[u]" + (contig ? std::string(".") + comp[c] : "");
+        return "s" + std::to_string(l) + (contig ? std::string(".") + comp[c] : "");
       });
-      os << "      }\n";
+      os << "  }\n";
     }
-    os << "      __builtin_nontemporal_store(o, reinterpret_cast<lmp_v4*>(out) + w[u]);\n";
-    os << "    }\n  }\n}\n";
+    os << "  __builtin_nontemporal_store(o, reinterpret_cast<lmp_v4*>(out) + v);\n}\n";
   } else {
     os << "  const unsigned long n = " << p.n << "ul;\n";
     os << "  for (unsigned long i = (unsigned long)blockIdx.x * " << kBlock
@@ -303,15 +291,6 @@ struct Compiled {
   void* handle = nullptr;
   std::vector<int64_t> sig;
 };
-
-int cu_count() {
-  static int n = [] {
-    lmp_rt_info info{};
-    if (lmp_rt_device_info(&info) != LMP_OK || info.cu_count <= 0) return 256;
-    return info.cu_count;
-  }();
-  return n;
-}
 
 class HipFusionBackend : public lazy::LazyBackend {
  public:
@@ -345,12 +324,11 @@ class HipFusionBackend : public lazy::LazyBackend {
     } else {
       ++backend_stats().jit_cache_hits;
     }
-    // Launch: one thread per float4 (vec) or element, four per lane per
-    // step, capped at 16 workgroups per CU (grid-stride beyond that).
+    // Launch: one lane per float4 (vec, one-shot) or per element (grid-stride
+    // loop, one-shot up to 2^30 workgroups).
     const uint64_t work = p.vec ? p.nvec : p.n;
-    const uint64_t per_block = p.vec ? uint64_t(kBlock) * kUnroll : uint64_t(kBlock);
-    uint64_t grid = (work + per_block - 1) / per_block;
-    grid = std::max<uint64_t>(1, std::min<uint64_t>(grid, uint64_t(cu_count()) * 16));
+    uint64_t grid = (work + kBlock - 1) / kBlock;
+    grid = std::max<uint64_t>(1, std::min<uint64_t>(grid, uint64_t(1) << 30));
     std::vector<void*> ptrs;
     ptrs.reserve(r.leaves.size() + 1);
     ptrs.push_back(out.data());

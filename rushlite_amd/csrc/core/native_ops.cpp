@@ -29,6 +29,7 @@ LMP_DEFINE_DISPATCH(clamp_backward_fn, clamp_backward_stub)
 LMP_DEFINE_DISPATCH(matmul_fn, matmul_stub)
 LMP_DEFINE_DISPATCH(transpose_fn, transpose_stub)
 LMP_DEFINE_DISPATCH(matmul_t_fn, matmul_t_stub)
+LMP_DEFINE_DISPATCH(matmul_acc_fn, matmul_acc_stub)
 
 namespace {
 using Acc = detail::UnsafeTensorAccessor;
@@ -127,6 +128,17 @@ Tensor matmul_t(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b) {
   }
   return wrap(matmul_t_stub()(a.device(), *Acc::getImpl(a), *Acc::getImpl(b),
                               trans_a, trans_b));
+}
+
+void matmul_acc(Tensor& c, const Tensor& a, const Tensor& b, bool trans_a, bool trans_b) {
+  LMP_CHECK(a.device() == b.device() && a.device() == c.device())
+      << "Tensors must be on the same device";
+  if (!matmul_acc_stub().has(c.device())) {
+    add_inplace(c, matmul_t(a, b, trans_a, trans_b));
+    return;
+  }
+  matmul_acc_stub()(c.device(), *Acc::getImpl(c), *Acc::getImpl(a), *Acc::getImpl(b),
+                    trans_a, trans_b);
 }
 
 Tensor transpose(const Tensor& a) {

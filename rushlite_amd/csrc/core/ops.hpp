@@ -52,6 +52,11 @@ using transpose_fn = TensorImpl (*)(const TensorImpl&);
 // (functions/matrix_ops.cpp:15-20).
 using matmul_t_fn = TensorImpl (*)(const TensorImpl&, const TensorImpl&, bool,
                                    bool);
+// C += op(A) * op(B) in place: gradient accumulation fused into the GEMM
+// epilogue instead of a product followed by add_inplace (same rounding: the
+// epilogue adds the finished fp32 product to C once).
+using matmul_acc_fn = void (*)(TensorImpl& c, const TensorImpl&, const TensorImpl&,
+                               bool, bool);
 
 #define LMP_FOR_BINARY_OPS(_) \
   _(add) _(sub) _(mul) _(div) _(pow) _(eq) _(ne) _(ge) _(le) _(gt) _(lt)
@@ -81,6 +86,7 @@ LMP_DECLARE_DISPATCH(clamp_backward_fn, clamp_backward_stub)
 LMP_DECLARE_DISPATCH(matmul_fn, matmul_stub)
 LMP_DECLARE_DISPATCH(transpose_fn, transpose_stub)
 LMP_DECLARE_DISPATCH(matmul_t_fn, matmul_t_stub)
+LMP_DECLARE_DISPATCH(matmul_acc_fn, matmul_acc_stub)
 
 Tensor clamp(const Tensor& a, Scalar lo, Scalar hi);
 Tensor abs_backward(const Tensor& input, const Tensor& grad);
@@ -88,6 +94,8 @@ Tensor clamp_backward(const Tensor& input, const Tensor& grad, Scalar lo, Scalar
 Tensor matmul(const Tensor& a, const Tensor& b);
 // op(a) @ op(b): trans_a uses a^T, trans_b uses b^T (2-D only).
 Tensor matmul_t(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b);
+// c += op(a) @ op(b) in place (shapes must match exactly).
+void matmul_acc(Tensor& c, const Tensor& a, const Tensor& b, bool trans_a, bool trans_b);
 Tensor transpose(const Tensor& a);
 Tensor reshape(const Tensor& a, std::vector<size_t> shape);
 Tensor squeeze(const Tensor& a, size_t dim);

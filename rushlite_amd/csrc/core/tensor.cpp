@@ -3,7 +3,11 @@
 #include "tensor.hpp"
 
 #include <algorithm>
+#include <cstring>
 #include <iostream>
+#include <map>
+#include <mutex>
+#include <tuple>
 
 #include "ops.hpp"
 
@@ -266,8 +270,25 @@ Tensor full_like(const Tensor& t, Scalar value) {
 Tensor ones_like(const Tensor& t) { return full_like(t, 1); }
 Tensor zeros_like(const Tensor& t) { return full_like(t, 0); }
 
+// Scalars in expressions (`x + 1e-3`) are [1] tensors of the operand's dtype
+// and device (native/overloads.hpp:16-28).  They are internal, never handed
+// to the user and never written in place, so each distinct (device, dtype,
+// value) is built once and shared; a training loop then issues no upload per
+// scalar per step.
 Tensor scalar_like(const Tensor& t, Scalar s) {
-  return Tensor(std::vector<Scalar>{s}, {1}, t.device(), t.type());
+  using Key = std::tuple<uint64_t, size_t, int>;
+  static std::mutex mu;
+  static auto* cache = new std::map<Key, Tensor>();  // outlives static teardown
+  uint64_t bits;
+  std::memcpy(&bits, &s, sizeof bits);
+  const Key key{bits, static_cast<size_t>(t.device()), static_cast<int>(t.type())};
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache->find(key);
+  if (it != cache->end()) return it->second;
+  if (cache->size() >= 4096) cache->clear();
+  Tensor fresh(std::vector<Scalar>{s}, {1}, t.device(), t.type());
+  cache->emplace(key, fresh);
+  return fresh;
 }
 
 // ----------------------------------------------------------------- metadata

@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <string>
 
+#include "fastdiv.hpp"
 #include "lmp_hip.h"
 
 namespace lmp_hip {
@@ -57,29 +58,6 @@ inline const char* dtype_name(int dtype) {
     default: return "Unknown";
   }
 }
-
-// Magic-number unsigned 32-bit division (Granlund & Montgomery, "Division by
-// Invariant Integers using Multiplication", PLDI 1994): for d >= 1,
-// n / d == (umulhi(n, m) + n) >> s with s = ceil(log2 d) and
-// m = floor(2^32 * (2^s - d) / d) + 1, exact for all n < 2^32.
-struct FastDiv {
-  uint32_t d = 1, m = 0, s = 0;
-  FastDiv() = default;
-  explicit FastDiv(uint32_t divisor) : d(divisor) {
-    s = 0;
-    while ((uint64_t(1) << s) < divisor) ++s;
-    m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << s) - divisor)) /
-                     divisor + 1);
-  }
-  __host__ __device__ __forceinline__ uint32_t div(uint32_t n) const {
-#if defined(__HIP_DEVICE_COMPILE__)
-    uint32_t hi = __umulhi(n, m);
-#else
-    uint32_t hi = uint32_t((uint64_t(n) * m) >> 32);
-#endif
-    return uint32_t((uint64_t(hi) + n) >> s);
-  }
-};
 
 #define LMP_HIP_TRY(expr)                                                   \
   do {                                                                      \

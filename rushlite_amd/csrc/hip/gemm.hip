@@ -53,6 +53,8 @@ struct Cfg {
 };
 
 using CfgLarge = Cfg<2, 2, 2, 2>;   // 128 x 128
+using CfgMid = Cfg<2, 2, 1, 2>;     // 64 x 128
+using CfgSmall = Cfg<2, 2, 1, 1>;   // 64 x 64
 using CfgSkinny = Cfg<1, 4, 1, 2>;  // 32 x 256
 
 template <class C, bool TA>
@@ -283,19 +285,24 @@ __global__ __launch_bounds__(256) void fold_splits(float* __restrict__ c,
   *p = accumulate ? *p + acc : acc;
 }
 
+// Default split of K: none once there is a tile for every CU; otherwise
+// enough splits to give each CU two workgroups, keeping at least four K tiles
+// per split.
+int default_splits(Runtime* rt, int tiles, int k_tiles) {
+  if (tiles >= rt->cu_count || k_tiles < 8) return 1;
+  const int want = 2 * rt->cu_count;
+  const int splits = std::min((want + tiles - 1) / tiles, std::max(1, k_tiles / 4));
+  return std::max(1, std::min(splits, 64));
+}
+
 template <class C, bool TA, bool TB>
-int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec) {
+int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
   g.tiles_m = (g.m + C::BM - 1) / C::BM;
   g.tiles_n = (g.n + C::BN - 1) / C::BN;
   const int tiles = g.tiles_m * g.tiles_n;
   const int k_tiles = (g.k + kBK - 1) / kBK;
-  // Split K when the tiles alone cannot occupy every CU twice; keep at least
-  // four K tiles per split.
-  int splits = 1;
-  const int want = 2 * rt->cu_count;
-  if (tiles < want && k_tiles >= 8)
-    splits = std::min((want + tiles - 1) / tiles, std::max(1, k_tiles / 4));
-  splits = std::max(1, std::min(splits, 64));
+  if (splits <= 0) splits = default_splits(rt, tiles, k_tiles);
+  splits = std::max(1, std::min(splits, k_tiles));
   g.k_tiles_per_split = (k_tiles + splits - 1) / splits;
   splits = std::max(1, (k_tiles + g.k_tiles_per_split - 1) / g.k_tiles_per_split);
 
@@ -326,9 +333,19 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec) {
   return LMP_OK;
 }
 
+// Tile choice (measured on MI355X, fp32): 128x128 whenever its tiles cover
+// the CUs; with a short K (<= 2048) and too few 128x128 tiles, 64x64 tiles
+// without a split (no partial round trip) win; otherwise 128x128 with split
+// K.  M <= 64 uses 32x256 tiles.
 template <bool TA, bool TB>
 int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec) {
   if (g.m <= 64) return launch_gemm_cfg<CfgSkinny, TA, TB>(rt, g, vec);
+  const int64_t large_tiles = int64_t((g.m + CfgLarge::BM - 1) / CfgLarge::BM) *
+                              ((g.n + CfgLarge::BN - 1) / CfgLarge::BN);
+  const int64_t small_tiles = int64_t((g.m + CfgSmall::BM - 1) / CfgSmall::BM) *
+                              ((g.n + CfgSmall::BN - 1) / CfgSmall::BN);
+  if (large_tiles < rt->cu_count && g.k <= 2048 && small_tiles >= rt->cu_count)
+    return launch_gemm_cfg<CfgSmall, TA, TB>(rt, g, vec, 1);
   return launch_gemm_cfg<CfgLarge, TA, TB>(rt, g, vec);
 }
 

@@ -11,10 +11,13 @@
 //                      partials are folded by a second pass in fixed order.
 //   short rows      -> one wave per row (softmax/loss rows like [512,1000]).
 // Column case (inner > 1, e.g. sum over dim 0, the bias-gradient reduction):
-//   each lane owns four adjacent columns (one float4), a workgroup covers
-//   1024 columns, and the reduced axis is cut into S chunks so the grid has
-//   thousands of workgroups; chunk partials [outer, S, inner] are folded in
-//   chunk order by a second pass.  No atomics: results are deterministic.
+//   each lane owns four adjacent columns (one float4); the four waves of a
+//   workgroup share a 256-column strip and take every fourth row of a chunk
+//   of the reduced axis (8 loads in flight per lane), then combine in LDS in
+//   fixed wave order.  The axis is cut into S chunks so the grid holds about
+//   four workgroups per CU; chunk partials [outer, S, inner] are folded by a
+//   second pass, S float4 loads per lane issued together.  No atomics:
+//   results are deterministic.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -119,39 +122,73 @@ __global__ __launch_bounds__(kBlock) void fold_parts(T* __restrict__ out,
   out[i] = acc;
 }
 
-// Column reduction, fp32, four columns per lane.  grid = (ceil(inner4/256),
-// S, outer); chunk s covers rows [s*chunk, min(len, (s+1)*chunk)).
-// dst layout: [outer, S, inner] (S == 1 writes the final result).
+// Column reduction, fp32.  grid = (ceil(inner4/64), S, outer); lane owns
+// float4 column c4 = blockIdx.x*64 + lane, wave w takes rows r0+w, r0+w+4, ...
+// of chunk s = [s*chunk, min(len, (s+1)*chunk)).  dst layout [outer, S, inner]
+// (S == 1 writes the final result).
+constexpr int kColUnroll = 8;
 template <int OP>
 __global__ __launch_bounds__(kBlock) void col_reduce_f32(
     float* __restrict__ dst, const float* __restrict__ in, uint32_t inner4,
     uint32_t len, uint32_t chunk) {
   using R = Reducer<OP, float>;
-  const uint32_t c4 = blockIdx.x * kBlock + threadIdx.x;
-  if (c4 >= inner4) return;
+  const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint32_t c4 = blockIdx.x * 64 + lane;
   const uint32_t s = blockIdx.y, S = gridDim.y, o = blockIdx.z;
   const uint32_t r0 = s * chunk;
   const uint32_t r1 = min(len, r0 + chunk);
-  const v4f* src = reinterpret_cast<const v4f*>(in) +
-                   (uint64_t(o) * len + r0) * inner4 + c4;
   const v4f id = v4f(R::identity());
-  v4f acc0 = id, acc1 = id, acc2 = id, acc3 = id;
-  uint32_t r = r0;
-  for (; r + 3 < r1; r += 4) {
-    v4f x0 = src[0], x1 = src[uint64_t(inner4)], x2 = src[2 * uint64_t(inner4)],
-        x3 = src[3 * uint64_t(inner4)];
-    acc0 = combine4<OP>(acc0, x0);
-    acc1 = combine4<OP>(acc1, x1);
-    acc2 = combine4<OP>(acc2, x2);
-    acc3 = combine4<OP>(acc3, x3);
-    src += 4 * uint64_t(inner4);
+  v4f acc[kColUnroll];
+#pragma unroll
+  for (int u = 0; u < kColUnroll; ++u) acc[u] = id;
+  if (c4 < inner4) {
+    const v4f* src = reinterpret_cast<const v4f*>(in) + uint64_t(o) * len * inner4 + c4;
+    uint32_t r = r0 + w;
+    for (; r + 4 * (kColUnroll - 1) < r1; r += 4 * kColUnroll) {
+      v4f x[kColUnroll];
+#pragma unroll
+      for (int u = 0; u < kColUnroll; ++u) x[u] = src[uint64_t(r + 4 * u) * inner4];
+#pragma unroll
+      for (int u = 0; u < kColUnroll; ++u) acc[u] = combine4<OP>(acc[u], x[u]);
+    }
+    for (; r < r1; r += 4) acc[0] = combine4<OP>(acc[0], src[uint64_t(r) * inner4]);
   }
-  for (; r < r1; ++r) {
-    acc0 = combine4<OP>(acc0, src[0]);
-    src += inner4;
+  v4f a = acc[0];
+#pragma unroll
+  for (int u = 1; u < kColUnroll; ++u) a = combine4<OP>(a, acc[u]);
+  __shared__ v4f lds[kWaves][64];
+  lds[w][lane] = a;
+  __syncthreads();
+  if (w == 0 && c4 < inner4) {
+    v4f t = lds[0][lane];
+#pragma unroll
+    for (int k = 1; k < kWaves; ++k) t = combine4<OP>(t, lds[k][lane]);
+    reinterpret_cast<v4f*>(dst)[(uint64_t(o) * S + s) * inner4 + c4] = t;
   }
-  const v4f acc = combine4<OP>(combine4<OP>(acc0, acc1), combine4<OP>(acc2, acc3));
-  reinterpret_cast<v4f*>(dst)[(uint64_t(o) * S + s) * inner4 + c4] = acc;
+}
+
+// Fold S chunk partials [outer, S, inner4] -> [outer, inner4], float4 lanes,
+// in chunk order with the loads of eight chunks issued before their combines.
+template <int OP>
+__global__ __launch_bounds__(kBlock) void fold_chunks_f32(
+    float* __restrict__ out, const float* __restrict__ part, uint64_t outer,
+    uint32_t inner4, uint32_t S) {
+  using R = Reducer<OP, float>;
+  const uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= outer * inner4) return;
+  const uint64_t o = i / inner4, c = i - o * inner4;
+  const v4f* src = reinterpret_cast<const v4f*>(part) + o * S * inner4 + c;
+  v4f acc = v4f(R::identity());
+  uint32_t s = 0;
+  for (; s + 8 <= S; s += 8) {
+    v4f x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = src[uint64_t(s + u) * inner4];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = combine4<OP>(acc, x[u]);
+  }
+  for (; s < S; ++s) acc = combine4<OP>(acc, src[uint64_t(s) * inner4]);
+  reinterpret_cast<v4f*>(out)[i] = acc;
 }
 
 // Column reduction for any dtype / alignment: one lane per column.
@@ -242,19 +279,23 @@ template <int OP, typename T>
 int reduce_cols(Runtime* rt, T* out, const T* in, uint64_t outer, uint64_t len,
                 uint64_t inner) {
   const bool vec = std::is_same_v<T, float> && inner % 4 == 0 && aligned16(in) &&
-                   aligned16(out) && inner / 4 <= 0xffffffffull &&
+                   aligned16(out) && inner / 4 <= 0x7fffffffull &&
                    len <= 0xffffffffull;
+  // Lanes per workgroup along the columns: 64 float4 lanes (4 waves share a
+  // strip) on the vector path, 256 scalar lanes otherwise.
   const uint64_t lanes = vec ? inner / 4 : inner;
-  const uint64_t gx = (lanes + kBlock - 1) / kBlock;
+  const uint64_t per_wg = vec ? 64 : kBlock;
+  const uint64_t gx = (lanes + per_wg - 1) / per_wg;
   if (gx > 0x7fffffffull || outer > 65535)
     return fail(LMP_ERR_UNSUPPORTED, "reduce: grid too large");
-  // Chunk the reduced axis until the grid reaches ~8 workgroups per CU,
-  // keeping at least 16 rows per chunk.
-  const uint64_t target = uint64_t(rt->cu_count) * 8;
+  // Chunk the reduced axis until the grid reaches ~4 workgroups per CU
+  // (measured best for [16384,16384]: 176 us at 4/CU vs 196 us at 8/CU),
+  // keeping at least 64 rows per chunk.
+  const uint64_t target = uint64_t(rt->cu_count) * 4;
   uint64_t S = 1;
   const uint64_t base = gx * outer;
   if (base < target) S = std::min<uint64_t>((target + base - 1) / base,
-                                            std::max<uint64_t>(1, len / 16));
+                                            std::max<uint64_t>(1, len / 64));
   S = std::min<uint64_t>(S, 65535);
   const uint64_t chunk = (len + S - 1) / S;
   S = (len + chunk - 1) / chunk;
@@ -268,21 +309,26 @@ int reduce_cols(Runtime* rt, T* out, const T* in, uint64_t outer, uint64_t len,
   const dim3 grid{uint32_t(gx), uint32_t(S), uint32_t(outer)};
   if constexpr (std::is_same_v<T, float>) {
     if (vec) {
-      hipLaunchKernelGGL((col_reduce_f32<OP>), grid, dim3(kBlock), 0,
-                         rt->stream, dst, in, uint32_t(inner / 4),
-                         uint32_t(len), uint32_t(chunk));
+      hipLaunchKernelGGL((col_reduce_f32<OP>), grid, dim3(kBlock), 0, rt->stream,
+                         dst, in, uint32_t(inner / 4), uint32_t(len), uint32_t(chunk));
       LMP_LAUNCH_CHECK("col_reduce_f32");
+      if (S > 1) {
+        const uint64_t n4 = outer * (inner / 4);
+        hipLaunchKernelGGL((fold_chunks_f32<OP>), dim3(blocks_for(n4)), dim3(kBlock), 0,
+                           rt->stream, out, tmp, outer, uint32_t(inner / 4), uint32_t(S));
+        LMP_LAUNCH_CHECK("fold_chunks_f32");
+        scratch_free(tmp);
+      }
+      return LMP_OK;
     }
   }
-  if (!vec) {
-    hipLaunchKernelGGL((col_reduce_scalar<OP, T>), grid, dim3(kBlock), 0,
-                       rt->stream, dst, in, inner, len, chunk);
-    LMP_LAUNCH_CHECK("col_reduce_scalar");
-  }
+  hipLaunchKernelGGL((col_reduce_scalar<OP, T>), grid, dim3(kBlock), 0, rt->stream, dst,
+                     in, inner, len, chunk);
+  LMP_LAUNCH_CHECK("col_reduce_scalar");
   if (S > 1) {
     const uint64_t n = outer * inner;
-    hipLaunchKernelGGL((fold_chunks<OP, T>), dim3(blocks_for(n)), dim3(kBlock),
-                       0, rt->stream, out, tmp, outer, inner, uint32_t(S));
+    hipLaunchKernelGGL((fold_chunks<OP, T>), dim3(blocks_for(n)), dim3(kBlock), 0,
+                       rt->stream, out, tmp, outer, inner, uint32_t(S));
     LMP_LAUNCH_CHECK("fold_chunks");
     scratch_free(tmp);
   }

@@ -430,3 +430,25 @@ def test_config3_linear_forward_backward(rsl):
         gw = w.grad.numpy()
         wrows = rng.choice(k, 32, replace=False)
         assert rel_err(gw[wrows], x64.T[wrows] @ np.ones((m, n))) <= 1e-4
+
+
+@pytest.mark.parametrize("m,k,n", [(96, 80, 72), (4096, 64, 128), (2048, 256, 256)])
+def test_matmul_grad_accumulates_in_gemm_epilogue(rsl, m, k, n):
+    """A weight reached twice accumulates its second product in the GEMM
+    epilogue; that must equal the fp32 sum of the two separate gradients
+    bit for bit (covers the split-K fold with accumulation too)."""
+    rng = np.random.default_rng(m + k + n)
+    xs = [rng.standard_normal((m, k)).astype(np.float32) for _ in range(2)]
+    w_np = (rng.standard_normal((k, n)) * 0.1).astype(np.float32)
+
+    def grad_of(inputs):
+        w = V(rsl, w_np, True)
+        for x_np in inputs:
+            rsl.matmul(V(rsl, x_np, False), w).backward()
+        return w.grad.numpy()
+
+    g1, g2, g12 = grad_of(xs[:1]), grad_of(xs[1:]), grad_of(xs)
+    assert np.array_equal(g12, g1 + g2)
+    want = xs[0].astype(np.float64).T.sum(1, keepdims=True) + xs[1].astype(np.float64).T.sum(
+        1, keepdims=True)
+    assert rel_err(g12, np.broadcast_to(want, (k, n))) <= 1e-4
