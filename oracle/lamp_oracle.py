@@ -383,15 +383,23 @@ def prod(a, axis):
         "mul", n.grad, binary("div", n.data, a.data)))
 
 
-def matmul_v(a: OVar, b: OVar):
-    out = matmul(a.data, b.data)
+def matmul_f64(a, b):
+    """fp32 GEMM accumulated in float64 and rounded once: another summation
+    order the 1e-4 GEMM tolerance admits, used to size how strongly a step
+    amplifies reordering (not a restatement of any reference function)."""
+    return (np.asarray(a, np.float64) @ np.asarray(b, np.float64)).astype(np.float32)
+
+
+def matmul_v(a: OVar, b: OVar, f64: bool = False):
+    mm = matmul_f64 if f64 else matmul
+    out = mm(a.data, b.data)
 
     def bw(node):
         # dA = g @ B^T ; dB = A^T @ g   (functions/matrix_ops.cpp:8-24)
         if a.requires_grad:
-            a.incr_grad(matmul(node.grad, transpose(b.data)))
+            a.incr_grad(mm(node.grad, transpose(b.data)))
         if b.requires_grad:
-            b.incr_grad(matmul(transpose(a.data), node.grad))
+            b.incr_grad(mm(transpose(a.data), node.grad))
 
     return OVar._make(out, [a, b], bw)
 
@@ -417,14 +425,15 @@ def softmax(x: OVar, dim: int) -> OVar:
 # ------------------------------------------------------------------- MLP
 
 
-def mlp_step(weights, biases, x, y):
+def mlp_step(weights, biases, x, y, f64_gemm: bool = False):
     """One forward + backward of the README MLP from the given parameters.
-    Returns (loss, weight grads, bias grads)."""
+    Returns (loss, weight grads, bias grads).  f64_gemm swaps the GEMMs for
+    float64-accumulated ones (see matmul_f64)."""
     W = [OVar(w, True) for w in weights]
     B = [OVar(b, True) for b in biases]
     h = OVar(x)
     for i in range(len(W)):
-        h = (h @ W[i]) + B[i]
+        h = matmul_v(h, W[i], f64_gemm) + B[i]
         if i < len(W) - 1:
             h = relu(h)
     p = softmax(h, -1)

@@ -285,6 +285,175 @@ __global__ __launch_bounds__(256) void fold_splits(float* __restrict__ c,
   *p = accumulate ? *p + acc : acc;
 }
 
+// ------------------------------------------------------------------ direct
+//
+// Register-direct MFMA kernel for M <= 32 (a Linear layer at a small batch:
+// the weight panel streams once from HBM and nothing is reused enough to pay
+// for LDS staging).  Every wave loads its MFMA
+// operands straight from global memory in operand layout, 8 values of k per
+// iteration.  MFMA step s (0..3) pairs k0 + s (lanes 0-31) with k0 + 4 + s
+// (lanes 32-63), so a lane's four A values of one iteration are contiguous in
+// k.  A wave owns a 32 x 128 block of C as four 32x32 MFMA blocks q:
+//   TB == false: a B row is read as float4 along n, lane c holding columns
+//     4c..4c+3; block q takes component q, so block q's column j is
+//     n0 + 4j + q and the epilogue writes whole float4s of a row.
+//   TB == true: block q covers columns n0 + 32q + (0..31); a lane reads the
+//     four k values of one stored B row as one float4.
+// The four waves of a workgroup take consecutive quarters of its K range and
+// add their blocks in a fixed order through LDS; workgroups split K further
+// over blockIdx.y into partials that fold_splits adds in split order.
+// Requirements (checked by the host): the contiguous extent of each operand
+// is a multiple of four with 16-byte aligned rows, and for TB == false C's
+// rows are 16-byte aligned too.
+struct DirectArgs {
+  const float* a;
+  const float* b;
+  float* c;  // final output (one split) or partial buffer base
+  int m, n, k;
+  int lda, ldb, ldc;
+  int n_blocks;    // ceil(n / 128)
+  int k_per_wg;    // K range of one workgroup (a multiple of 32)
+  int accumulate;  // only honoured when writing the final output
+};
+
+constexpr int kDirectN = 128;
+
+template <bool TA, bool TB>
+struct DirectFrag {
+  v4f a;     // A values of steps 0..3
+  v4f b[4];  // TB: b[q][s]; !TB: b[s][q]
+
+  __device__ __forceinline__ void load(const DirectArgs& g, int row, int n0, int k0,
+                                       int ke, int li, int lh) {
+    const int kq = k0 + 4 * lh;  // first k of this lane's half
+    if constexpr (!TA) {
+      a = (row < g.m && kq < ke)
+              ? *reinterpret_cast<const v4f*>(g.a + int64_t(row) * g.lda + kq)
+              : v4f(0.0f);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        a[s] = (row < g.m && kq + s < ke) ? g.a[int64_t(kq + s) * g.lda + row] : 0.0f;
+    }
+    if constexpr (!TB) {
+      const int col = n0 + 4 * li;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        b[s] = (col < g.n && kq + s < ke)
+                   ? *reinterpret_cast<const v4f*>(g.b + int64_t(kq + s) * g.ldb + col)
+                   : v4f(0.0f);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = n0 + 32 * q + li;
+        b[q] = (col < g.n && kq < ke)
+                   ? *reinterpret_cast<const v4f*>(g.b + int64_t(col) * g.ldb + kq)
+                   : v4f(0.0f);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void mma(v16f (&acc)[4]) const {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], TB ? b[q][s] : b[s][q],
+                                                      acc[q], 0, 0, 0);
+  }
+};
+
+// Output row of accumulator register r for a lane in half lh (0 or 1).
+__device__ __forceinline__ int direct_row(int r, int lh) {
+  return (r / 4) * 8 + lh * 4 + (r % 4);
+}
+
+constexpr int kDirectWaves = 4;
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(64 * kDirectWaves) __attribute__((amdgpu_waves_per_eu(TB ? 3 : 4)))
+void gemm_direct(DirectArgs g) {
+  constexpr int KW = kDirectWaves;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & 31, lh = lane >> 5;
+  const int n0 = int(blockIdx.x % g.n_blocks) * kDirectN;
+  const int part = g.k_per_wg / KW;
+  const int kb = int(blockIdx.y) * g.k_per_wg + wave * part;
+  const int ke = min(g.k, kb + part);
+
+  v16f acc[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) acc[q] = v16f(0.0f);
+
+  // Two fragments in flight: the next iteration's loads are issued before
+  // the current iteration's MFMAs.  Loads at or past ke yield zeros, so the
+  // tail needs no branch (0 * 0 adds nothing).
+  DirectFrag<TA, TB> f0, f1;
+  f0.load(g, li, n0, kb, ke, li, lh);
+  for (int k0 = kb; k0 < ke; k0 += 16) {
+    f1.load(g, li, n0, k0 + 8, ke, li, lh);
+    f0.mma(acc);
+    f0.load(g, li, n0, k0 + 16, ke, li, lh);
+    f1.mma(acc);
+  }
+
+  const bool partial = gridDim.y > 1;
+  float* out = partial ? g.c + int64_t(blockIdx.y) * g.m * g.n : g.c;
+  const int64_t ld = partial ? int64_t(g.n) : int64_t(g.ldc);
+  const bool acc_out = !partial && g.accumulate;
+
+  // Blocks are added over the waves through LDS in rounds of BPR blocks
+  // (32 KiB), laid out [wave][block][r][lane] so writes and reads are
+  // conflict-free.  Thread t owns the (r, lane) pairs p = t + 64*KW*u and
+  // sums them in wave order.
+  constexpr int BPR = 8 / KW, U = 16 / KW, NT = 64 * KW;
+  __shared__ __attribute__((aligned(16))) float red[KW * BPR * 16 * 64];
+  v4f v[U];
+#pragma unroll
+  for (int round = 0; round < 4 / BPR; ++round) {
+    if (round) __syncthreads();
+#pragma unroll
+    for (int qq = 0; qq < BPR; ++qq)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        red[((wave * BPR + qq) * 16 + r) * 64 + lane] = acc[round * BPR + qq][r];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int p = int(threadIdx.x) + NT * u;
+      const int r = p >> 6, ln = p & 63;
+#pragma unroll
+      for (int qq = 0; qq < BPR; ++qq) {
+        float t = red[(qq * 16 + r) * 64 + ln];
+#pragma unroll
+        for (int w = 1; w < KW; ++w) t += red[((w * BPR + qq) * 16 + r) * 64 + ln];
+        v[u][round * BPR + qq] = t;
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int p = int(threadIdx.x) + NT * u;
+    const int r = p >> 6, ln = p & 63;
+    const int orow = direct_row(r, ln >> 5);
+    if (orow >= g.m) continue;
+    float* base = out + int64_t(orow) * ld;
+    if constexpr (!TB) {
+      const int col = n0 + 4 * (ln & 31);
+      if (col < g.n) {
+        v4f* o = reinterpret_cast<v4f*>(base + col);
+        *o = acc_out ? *o + v[u] : v[u];
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = n0 + 32 * q + (ln & 31);
+        if (col < g.n) base[col] = acc_out ? base[col] + v[u][q] : v[u][q];
+      }
+    }
+  }
+}
+
 // Default split of K: none once there is a tile for every CU; otherwise
 // enough splits to give each CU two workgroups, keeping at least four K tiles
 // per split.
@@ -333,12 +502,57 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
   return LMP_OK;
 }
 
+// M <= 32 on the register-direct kernel.  Each workgroup takes at least 64
+// values of k per wave; the split count aims at one workgroup per CU (more
+// only adds partial traffic: measured on MI355X); `splits` > 0 overrides it.
+template <bool TA, bool TB>
+int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
+  DirectArgs d{};
+  d.a = g0.a;
+  d.b = g0.b;
+  d.c = g0.c;
+  d.m = g0.m;
+  d.n = g0.n;
+  d.k = g0.k;
+  d.lda = g0.lda;
+  d.ldb = g0.ldb;
+  d.ldc = g0.ldc;
+  d.accumulate = g0.accumulate;
+  d.n_blocks = (g0.n + kDirectN - 1) / kDirectN;
+  constexpr int kGrain = 8 * kDirectWaves;
+  const int max_splits = std::max(1, g0.k / (64 * kDirectWaves));
+  if (splits <= 0) splits = (rt->cu_count + d.n_blocks - 1) / d.n_blocks;
+  splits = std::max(1, std::min(splits, max_splits));
+  d.k_per_wg = ((g0.k + splits - 1) / splits + kGrain - 1) / kGrain * kGrain;
+  splits = (g0.k + d.k_per_wg - 1) / d.k_per_wg;
+  float* part = nullptr;
+  if (splits > 1) {
+    part = static_cast<float*>(
+        scratch_alloc(size_t(splits) * size_t(g0.m) * size_t(g0.n) * sizeof(float)));
+    if (!part) return LMP_ERR_OOM;
+    d.c = part;
+  }
+  const dim3 grid{uint32_t(d.n_blocks), uint32_t(splits), 1u};
+  hipLaunchKernelGGL((gemm_direct<TA, TB>), grid, dim3(64 * kDirectWaves), 0, rt->stream, d);
+  LMP_LAUNCH_CHECK("gemm_direct");
+  if (splits > 1) {
+    const int64_t mn = int64_t(g0.m) * g0.n;
+    hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
+                       rt->stream, g0.c, part, g0.m, g0.n, g0.ldc, splits, g0.accumulate);
+    LMP_LAUNCH_CHECK("fold_splits");
+    scratch_free(part);
+  }
+  return LMP_OK;
+}
+
 // Tile choice (measured on MI355X, fp32): 128x128 whenever its tiles cover
 // the CUs; with a short K (<= 2048) and too few 128x128 tiles, 64x64 tiles
 // without a split (no partial round trip) win; otherwise 128x128 with split
-// K.  M <= 64 uses 32x256 tiles.
+// K.  M <= 64 uses 32x256 tiles, and M <= 32 the register-direct kernel when
+// its alignment requirements hold.
 template <bool TA, bool TB>
-int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec) {
+int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok) {
+  if (direct_ok && g.m <= 32) return launch_direct<TA, TB>(rt, g);
   if (g.m <= 64) return launch_gemm_cfg<CfgSkinny, TA, TB>(rt, g, vec);
   const int64_t large_tiles = int64_t((g.m + CfgLarge::BM - 1) / CfgLarge::BM) *
                               ((g.n + CfgLarge::BN - 1) / CfgLarge::BN);
@@ -415,10 +629,12 @@ extern "C" int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n,
   const size_t b_contig = trans_b ? k : n;
   const bool vec = lda % 4 == 0 && ldb % 4 == 0 && a_contig % 4 == 0 &&
                    b_contig % 4 == 0 && aligned16(a) && aligned16(b);
-  if (!trans_a && !trans_b) return launch_gemm<false, false>(rt, g, vec);
-  if (!trans_a && trans_b) return launch_gemm<false, true>(rt, g, vec);
-  if (trans_a && !trans_b) return launch_gemm<true, false>(rt, g, vec);
-  return launch_gemm<true, true>(rt, g, vec);
+  // The direct kernel's float4 C stores (trans_b == 0) need 16-byte C rows.
+  const bool direct_ok = vec && (trans_b || (ldc % 4 == 0 && aligned16(c)));
+  if (!trans_a && !trans_b) return launch_gemm<false, false>(rt, g, vec, direct_ok);
+  if (!trans_a && trans_b) return launch_gemm<false, true>(rt, g, vec, direct_ok);
+  if (trans_a && !trans_b) return launch_gemm<true, false>(rt, g, vec, direct_ok);
+  return launch_gemm<true, true>(rt, g, vec, direct_ok);
 }
 
 extern "C" int lmp_k_transpose(int dtype, void* out, const void* in, size_t m,

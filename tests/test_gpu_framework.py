@@ -339,7 +339,14 @@ def test_mlp_free_running_matches_oracle(rsl, oracle, dims, batch, scale):
 def test_mlp_each_step_matches_oracle(rsl, oracle, dims, batch, scale):
     """30 training steps on the GPU; before every step the oracle runs the
     same step from the GPU's current parameters, and the step's loss and
-    every parameter gradient must agree within 1e-4 (teacher forcing)."""
+    every parameter gradient must agree within 1e-4 (teacher forcing).
+
+    GEMM summation order is free within the GEMM tolerance, and at the
+    reference's randn(0, 1) init the softmax of large logits amplifies it: two
+    valid orders computed by the oracle itself (sequential fp32, and float64
+    accumulation rounded once) already differ by up to ~5e-5 in a step's
+    gradients.  Each gradient must therefore be within 1e-4 of at least one
+    of those two oracle steps."""
     x_np, y_np, ws, bs = _mlp_problem(dims, batch, scale)
     model = _mlp(rsl, ws, bs)
     x, y = V(rsl, x_np), V(rsl, y_np)
@@ -353,13 +360,16 @@ def test_mlp_each_step_matches_oracle(rsl, oracle, dims, batch, scale):
         params = [p.numpy() for _, p in model.named_parameters()]
         cur_w, cur_b = params[0::2], params[1::2]
         ref_loss, ref_gw, ref_gb = oracle.mlp_step(cur_w, cur_b, x_np, y_np)
+        _, ref64_gw, ref64_gb = oracle.mlp_step(cur_w, cur_b, x_np, y_np, f64_gemm=True)
         probs = forward(x)
         loss = (-y * rsl.log(probs + 1e-3)).sum(1).sum(0)
         loss.backward()
         assert abs(loss.tolist()[0] - ref_loss) <= 1e-4 * abs(ref_loss), step
         grads = [p.grad.numpy() for _, p in model.named_parameters()]
-        for g, r in zip(grads, [t for pair in zip(ref_gw, ref_gb) for t in pair]):
-            assert rel_err(g, r) <= 1e-4, step
+        refs = [t for pair in zip(ref_gw, ref_gb) for t in pair]
+        refs64 = [t for pair in zip(ref64_gw, ref64_gb) for t in pair]
+        for g, r, r64 in zip(grads, refs, refs64):
+            assert min(rel_err(g, r), rel_err(g, r64)) <= 1e-4, step
         for name, p in zip(names, list(model.parameters())):
             model.params[name] = rsl.Variable(p.data - 1e-3 * p.grad, requires_grad=True)
 

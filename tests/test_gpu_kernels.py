@@ -156,9 +156,13 @@ def test_reduce_ones_column_is_exact(hip):
     ones.free()
 
 
+# M <= 32 with 16-byte rows takes the register-direct kernel: (32, 132, 1028)
+# and (20, 132, 1028) split K with a ragged last split and a partial column
+# block, (4, 260, 2048) splits K eight ways, (1, 8, 8) is a single row.
 GEMM_SHAPES = [(64, 64, 64), (128, 256, 96), (33, 17, 70), (32, 512, 1024),
                (256, 1000, 128), (32, 64, 256), (32, 10, 64), (200, 3, 5),
-               (1, 7, 3), (512, 512, 2048), (130, 260, 33)]
+               (1, 7, 3), (512, 512, 2048), (130, 260, 33), (32, 132, 1028),
+               (20, 132, 1028), (4, 260, 2048), (1, 8, 8)]
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES, ids=str)

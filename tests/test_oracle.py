@@ -346,3 +346,31 @@ def test_mlp_trajectory_vs_torch(oracle):
     for mine, ref in zip(fw + fb, tw + tb):
         ref = ref.numpy()
         assert np.max(np.abs(mine - ref)) / np.max(np.abs(ref)) < 1e-4
+
+
+def test_mlp_step_gemm_orders_vs_torch(oracle):
+    """Both GEMM orders of the oracle's MLP step (sequential fp32, float64
+    accumulation) match a torch float64 step of the same graph within 1e-5
+    (the remaining error is the fp32 elementwise rounding both share); a
+    wrong product (a transposed operand, a dropped term) would miss both."""
+    rng = np.random.default_rng(5)
+    x = rng.random((32, 256), dtype=np.float32)
+    y = rng.random((32, 10), dtype=np.float32)
+    ws = [(rng.standard_normal((256, 64)) * 0.1).astype(np.float32),
+          (rng.standard_normal((64, 10)) * 0.1).astype(np.float32)]
+    bs = [(rng.standard_normal(64) * 0.1).astype(np.float32),
+          (rng.standard_normal(10) * 0.1).astype(np.float32)]
+    tw = [torch.tensor(w, dtype=torch.float64, requires_grad=True) for w in ws]
+    tb = [torch.tensor(b, dtype=torch.float64, requires_grad=True) for b in bs]
+    tx, ty = torch.tensor(x, dtype=torch.float64), torch.tensor(y, dtype=torch.float64)
+    h = torch.clamp(tx @ tw[0] + tb[0], min=0.0)
+    p = _torch_softmax_lamp(h @ tw[1] + tb[1], -1)
+    tl = (-ty * torch.log(p + 1e-3)).sum(1, keepdim=True).sum(0, keepdim=True)
+    tl.backward()
+    want = [t.grad.numpy() for t in (tw[0], tb[0], tw[1], tb[1])]
+    for f64 in (False, True):
+        loss, gw, gb = oracle.mlp_step(ws, bs, x, y, f64_gemm=f64)
+        assert abs(loss - float(tl)) <= 1e-5 * abs(float(tl))
+        got = [gw[0], gb[0], gw[1], gb[1]]
+        for g, w in zip(got, want):
+            assert np.max(np.abs(g - w)) / np.max(np.abs(w)) < 1e-5
