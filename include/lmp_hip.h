@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define LMP_HIP_ABI_VERSION 1
+#define LMP_HIP_ABI_VERSION 2
 #define LMP_MAX_DIMS 16 /* align_utils.hpp:7 */
 
 typedef enum {
@@ -234,8 +234,14 @@ int lmp_jit_compile(uint64_t key, const char* source, const char* kernel_name,
  * synchronisation (the reference synchronises every launch,
  * nvrtc_backend.cpp:135-141). */
 int lmp_jit_launch(void* handle, uint32_t grid, uint32_t block, void** args);
-/* Number of modules compiled by this process (cache misses). */
+/* Number of modules compiled by this process with hipRTC. */
 int lmp_jit_compiled_count(uint64_t* count);
+/* Number of modules this process loaded from the on-disk code-object cache
+ * instead of compiling ($LMP_HIP_JIT_CACHE, default
+ * ~/.cache/rushlite_amd/hiprtc; an empty value disables it).  No counterpart
+ * in the reference, which compiles every graph again in each process
+ * (nvrtc_backend.cpp:54-128). */
+int lmp_jit_disk_loaded_count(uint64_t* count);
 
 #ifdef __cplusplus
 }

@@ -95,6 +95,7 @@ SIGNATURES = {
                              C.POINTER(_vp)]),
     "lmp_jit_launch": (_i, [_vp, C.c_uint32, C.c_uint32, C.POINTER(_vp)]),
     "lmp_jit_compiled_count": (_i, [C.POINTER(C.c_uint64)]),
+    "lmp_jit_disk_loaded_count": (_i, [C.POINTER(C.c_uint64)]),
 }
 
 _lib = None

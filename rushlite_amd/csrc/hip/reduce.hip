@@ -9,7 +9,9 @@
 //                      a row is split over several workgroups only when
 //                      there are too few rows to fill 256 CUs, and the
 //                      partials are folded by a second pass in fixed order.
-//   short rows      -> one wave per row (softmax/loss rows like [512,1000]).
+//   short rows      -> one wave per row (softmax/loss rows like [512,1000]),
+//                      float4 loads when rows are 16-byte multiples, four
+//                      loads in flight per lane.
 // Column case (inner > 1, e.g. sum over dim 0, the bias-gradient reduction):
 //   each lane owns four adjacent columns (one float4); the four waves of a
 //   workgroup share a 256-column strip and take every fourth row of a chunk
@@ -92,7 +94,9 @@ __global__ __launch_bounds__(kBlock) void row_reduce_f32(
   }
 }
 
-// One wave per row, any dtype, any length.
+// One wave per row, any dtype, any length.  Four loads per lane are issued
+// before they are combined (four accumulators), so a short row costs one
+// memory latency rather than one per 64 elements.
 template <int OP, typename T>
 __global__ __launch_bounds__(kBlock) void row_reduce_wave(
     T* __restrict__ out, const T* __restrict__ in, uint64_t rows,
@@ -102,10 +106,47 @@ __global__ __launch_bounds__(kBlock) void row_reduce_wave(
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
   const T* src = in + row * len;
-  T acc = R::identity();
-  for (uint64_t j = lane; j < len; j += 64) acc = R::combine(acc, src[j]);
+  T a0 = R::identity(), a1 = a0, a2 = a0, a3 = a0;
+  uint64_t j = lane;
+  for (; j + 192 < len; j += 256) {
+    const T x0 = src[j], x1 = src[j + 64], x2 = src[j + 128], x3 = src[j + 192];
+    a0 = R::combine(a0, x0);
+    a1 = R::combine(a1, x1);
+    a2 = R::combine(a2, x2);
+    a3 = R::combine(a3, x3);
+  }
+  for (; j < len; j += 64) a0 = R::combine(a0, src[j]);
+  T acc = R::combine(R::combine(a0, a1), R::combine(a2, a3));
   acc = wave_reduce<OP, T>(acc);
   if (lane == 0) out[row] = acc;
+}
+
+// One wave per fp32 row with 16-byte rows (len % 4 == 0): float4 loads, four
+// in flight per lane.
+template <int OP>
+__global__ __launch_bounds__(kBlock) void row_reduce_wave_f32(
+    float* __restrict__ out, const float* __restrict__ in, uint64_t rows,
+    uint32_t len4) {
+  using R = Reducer<OP, float>;
+  const uint64_t row = uint64_t(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint32_t lane = threadIdx.x & 63;
+  const v4f* src = reinterpret_cast<const v4f*>(in) + row * len4;
+  const v4f id = v4f(R::identity());
+  v4f a0 = id, a1 = id, a2 = id, a3 = id;
+  uint32_t j = lane;
+  for (; j + 192 < len4; j += 256) {
+    const v4f x0 = src[j], x1 = src[j + 64], x2 = src[j + 128], x3 = src[j + 192];
+    a0 = combine4<OP>(a0, x0);
+    a1 = combine4<OP>(a1, x1);
+    a2 = combine4<OP>(a2, x2);
+    a3 = combine4<OP>(a3, x3);
+  }
+  for (; j < len4; j += 64) a0 = combine4<OP>(a0, src[j]);
+  const v4f a = combine4<OP>(combine4<OP>(a0, a1), combine4<OP>(a2, a3));
+  float v = R::combine(R::combine(a.x, a.y), R::combine(a.z, a.w));
+  v = wave_reduce<OP, float>(v);
+  if (lane == 0) out[row] = v;
 }
 
 // Fold `parts` consecutive partials per output in order.
@@ -269,6 +310,14 @@ int reduce_rows(Runtime* rt, T* out, const T* in, uint64_t rows, uint64_t len) {
   }
   const uint64_t blocks = (rows + kWaves - 1) / kWaves;
   if (blocks > 0x7fffffffull) return fail(LMP_ERR_UNSUPPORTED, "reduce: too many rows");
+  if constexpr (std::is_same_v<T, float>) {
+    if (len % 4 == 0 && aligned16(in) && len / 4 <= 0xffffffffull) {
+      hipLaunchKernelGGL((row_reduce_wave_f32<OP>), dim3(uint32_t(blocks)), dim3(kBlock), 0,
+                         rt->stream, out, in, rows, uint32_t(len / 4));
+      LMP_LAUNCH_CHECK("row_reduce_wave_f32");
+      return LMP_OK;
+    }
+  }
   hipLaunchKernelGGL((row_reduce_wave<OP, T>), dim3(uint32_t(blocks)),
                      dim3(kBlock), 0, rt->stream, out, in, rows, len);
   LMP_LAUNCH_CHECK("row_reduce_wave");

@@ -6,7 +6,10 @@ chain, fused == eager == oracle bit for bit where the ops are exact), the
 README MLP trajectory against the oracle, and config-size properties.
 """
 import json
+import os
+import subprocess
 import sys
+import textwrap
 from pathlib import Path
 
 import numpy as np
@@ -462,3 +465,49 @@ def test_matmul_grad_accumulates_in_gemm_epilogue(rsl, m, k, n):
     want = xs[0].astype(np.float64).T.sum(1, keepdims=True) + xs[1].astype(np.float64).T.sum(
         1, keepdims=True)
     assert rel_err(g12, np.broadcast_to(want, (k, n))) <= 1e-4
+
+
+_JIT_CHILD = textwrap.dedent("""
+    import ctypes as C, json, sys
+    import numpy as np
+    sys.path.insert(0, sys.argv[1])
+    import rushlite_amd as rsl
+    from rushlite_amd import abi
+    a = rsl.Variable(np.arange(24, dtype=np.float32).reshape(4, 6))
+    b = rsl.Variable(np.full((4, 1), 0.25, np.float32))
+    with rsl.capture_on():
+        c = rsl.exp(a * 0.125) * b - a
+    vals = c.numpy()
+    n, d = C.c_uint64(), C.c_uint64()
+    abi.check(abi.lib().lmp_jit_compiled_count(C.byref(n)))
+    abi.check(abi.lib().lmp_jit_disk_loaded_count(C.byref(d)))
+    print(json.dumps({"compiled": n.value, "disk": d.value,
+                      "bits": vals.view(np.uint32).ravel().tolist()}))
+""")
+
+
+def _jit_child(cache_dir):
+    root = str(Path(__file__).resolve().parents[1])
+    env = dict(os.environ, LMP_HIP_JIT_CACHE=str(cache_dir))
+    print(f"jit disk cache child, cache={cache_dir}", flush=True)
+    out = subprocess.run([sys.executable, "-c", _JIT_CHILD, root], env=env,
+                         capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr[-2000:]
+    return json.loads(out.stdout.strip().splitlines()[-1])
+
+
+def test_jit_disk_cache_reused_by_a_new_process(tmp_path):
+    """A second process loads the fused kernel the first one compiled; a
+    truncated cache file is a miss that recompiles, never a wrong kernel."""
+    first = _jit_child(tmp_path)
+    assert first["compiled"] >= 1 and first["disk"] == 0
+    files = sorted(tmp_path.glob("*.hsaco"))
+    assert len(files) == first["compiled"]
+    second = _jit_child(tmp_path)
+    assert second["compiled"] == 0 and second["disk"] == first["compiled"]
+    assert second["bits"] == first["bits"]
+    for f in files:
+        f.write_bytes(f.read_bytes()[: f.stat().st_size // 2])
+    third = _jit_child(tmp_path)
+    assert third["compiled"] == first["compiled"] and third["disk"] == 0
+    assert third["bits"] == first["bits"]
