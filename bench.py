@@ -34,6 +34,7 @@ import numpy as np  # noqa: E402
 METRIC = "fused-kernel HBM GB/s (% of peak); fp32 matmul TFLOP/s; MLP train steps/s"
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+FP64_MFMA_PEAK_TFLOPS = 78.6
 N8K = 8192
 N16K = 16384
 BYTES_C1 = 4 * (2 * N8K * N8K + N8K)          # 536,903,680
@@ -175,6 +176,20 @@ def extras(rsl, abi, a, b, steps, warmup):
                 "frac_of_fp32_peak": round(flop / ms / 1e9 / FP32_MFMA_PEAK_TFLOPS, 3)}
         del X, W, dY, Y, dX, dW
     out["c3_gemm"] = gemm
+
+    # float64 GEMM (the reference's float64 suites run matmul on the device)
+    n = 4096
+    A64, B64, C64 = (abi.DeviceBuffer((n, n), np.float64) for _ in range(3))
+    for buf in (A64, B64):
+        abi.check(L.lmp_k_fill(abi.FLOAT64, buf.ptr, n * n, 0.01))
+
+    def run64():
+        abi.check(L.lmp_k_gemm(abi.FLOAT64, 0, 0, n, n, n, A64.ptr, n, B64.ptr, n, C64.ptr, n, 0))
+    ms = time_steps(abi, run64, 5, 1) / 5
+    flop = 2.0 * n ** 3
+    out["gemm_f64_4096"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(flop / ms / 1e9, 1),
+                            "frac_of_fp64_peak": round(flop / ms / 1e9 / FP64_MFMA_PEAK_TFLOPS, 3)}
+    del A64, B64, C64
 
     # --- config 4 and config 0: MLP training loops
     out["c4_wide_mlp"] = mlp_bench(rsl, abi, (4096, 4096, 4096, 1000), 512, 50, onehot=True)

@@ -214,6 +214,18 @@ int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
                    const float* a, size_t lda, const float* b, size_t ldb,
                    float* c, size_t ldc, int accumulate);
 
+/* The same product for any dtype, operands and C all of `dtype`
+ * (LMP_FLOAT32 is lmp_k_gemm_f32).  float64 accumulates on the f64 matrix
+ * cores; bool / int16 / int32 / int64 follow cpu/matrix.cpp:8-18 exactly:
+ * the sum starts at 0 in the output type, so integers wrap modulo 2^bits and
+ * bool is an OR of ANDs.  Replaces the remaining cudaMatMul instantiations
+ * (matrix.cu:208-216) behind matmul_cuda (kernels.cu:83-110), whose callers
+ * cast mixed operands to the promoted type first (cpu/matrix.cpp:8-18 casts
+ * each operand to the output type). */
+int lmp_k_gemm(int dtype, int trans_a, int trans_b, size_t m, size_t n, size_t k,
+               const void* a, size_t lda, const void* b, size_t ldb, void* c,
+               size_t ldc, int accumulate);
+
 /* out[n,m] = in[m,n].  Replaces transpose_cuda / cudaTransposeKernel
  * (kernels.cu:66-81, matrix.cu:165-206). */
 int lmp_k_transpose(int dtype, void* out, const void* in, size_t m, size_t n);

@@ -89,6 +89,7 @@ SIGNATURES = {
     "lmp_k_reduce": (_i, [_i, _i, _vp, _vp, _sz, _sz, _sz]),
     "lmp_k_gemm_f32": (_i, [_i, _i, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp,
                             _sz, _i]),
+    "lmp_k_gemm": (_i, [_i, _i, _i, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _i]),
     "lmp_k_transpose": (_i, [_i, _vp, _vp, _sz, _sz]),
     "lmp_jit_lookup": (_i, [C.c_uint64, C.POINTER(_vp)]),
     "lmp_jit_compile": (_i, [C.c_uint64, C.c_char_p, C.c_char_p,
@@ -254,11 +255,17 @@ def gemm(a: DeviceBuffer, b: DeviceBuffer, trans_a=False, trans_b=False,
         kb, n = b.shape
     if kb != k:
         raise ValueError("gemm: inner dimensions differ")
+    if a.dtype != b.dtype:
+        raise ValueError("gemm: operands must share a dtype")
     if out is None:
-        out = DeviceBuffer((m, n), np.float32)
-    check(lib().lmp_k_gemm_f32(int(trans_a), int(trans_b), m, n, k, a.ptr,
-                               a.shape[1], b.ptr, b.shape[1], out.ptr, n,
-                               int(accumulate)))
+        out = DeviceBuffer((m, n), a.dtype)
+    if a.dtype == np.float32:
+        check(lib().lmp_k_gemm_f32(int(trans_a), int(trans_b), m, n, k, a.ptr,
+                                   a.shape[1], b.ptr, b.shape[1], out.ptr, n,
+                                   int(accumulate)))
+    else:
+        check(lib().lmp_k_gemm(a.code, int(trans_a), int(trans_b), m, n, k, a.ptr,
+                               a.shape[1], b.ptr, b.shape[1], out.ptr, n, int(accumulate)))
     return out
 
 

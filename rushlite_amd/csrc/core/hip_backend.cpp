@@ -241,7 +241,11 @@ TensorImpl reduce_hip(const TensorImpl& a, size_t axis) {
 
 // ------------------------------------------------------------------- matrix
 
-TensorImpl gemm_hip(const TensorImpl& a, const TensorImpl& b, bool ta, bool tb) {
+struct GemmShape {
+  size_t m, n, k;
+};
+
+GemmShape gemm_shape(const TensorImpl& a, const TensorImpl& b, bool ta, bool tb) {
   LMP_CHECK(a.shape().size() == 2 && b.shape().size() == 2)
       << "Both matrices must be 2D.";
   const size_t m = ta ? a.shape()[1] : a.shape()[0];
@@ -249,20 +253,30 @@ TensorImpl gemm_hip(const TensorImpl& a, const TensorImpl& b, bool ta, bool tb) 
   const size_t kb = tb ? b.shape()[1] : b.shape()[0];
   const size_t n = tb ? b.shape()[0] : b.shape()[1];
   LMP_CHECK(k == kb) << "Incompatible matrix dimensions for multiplication.";
+  return {m, n, k};
+}
+
+// C (+)= op(A) op(B) in dtype `dt`; A and B are cast to `dt` first, as the
+// reference's matmul casts each operand to the output type
+// (cpu/matrix.cpp:14-15).
+void gemm_into(void* c, DataType dt, const TensorImpl& a, const TensorImpl& b, bool ta,
+               bool tb, const GemmShape& s, bool accumulate) {
+  if (!s.m || !s.n) return;
+  void *pa = nullptr, *pb = nullptr;
+  Storage ka = as_dtype(a, dt, &pa);
+  Storage kb = as_dtype(b, dt, &pb);
+  count_launch();
+  hip_ok(lmp_k_gemm(code(dt), ta, tb, s.m, s.n, s.k, pa, a.shape()[1], pb, b.shape()[1], c,
+                    s.n, accumulate ? 1 : 0),
+         "lmp_k_gemm");
+}
+
+TensorImpl gemm_hip(const TensorImpl& a, const TensorImpl& b, bool ta, bool tb) {
+  const GemmShape s = gemm_shape(a, b, ta, tb);
   const DataType dt = type_upcast(a.type(), b.type());
-  LMP_CHECK(dt == DataType::Float32)
-      << "matmul on the HIP device supports Float32 (got " << dt << ")";
-  Storage out(m * n * sizeof(float), DeviceType::HIP);
-  if (m && n) {
-    void* pa = mut(a);
-    void* pb = mut(b);
-    count_launch();
-    hip_ok(lmp_k_gemm_f32(ta, tb, m, n, k, static_cast<const float*>(pa),
-                          a.shape()[1], static_cast<const float*>(pb), b.shape()[1],
-                          static_cast<float*>(out.data()), n, 0),
-           "lmp_k_gemm_f32");
-  }
-  return TensorImpl(out, {m, n}, dt);
+  Storage out(s.m * s.n * dtype_size(dt), DeviceType::HIP);
+  gemm_into(out.data(), dt, a, b, ta, tb, s, false);
+  return TensorImpl(out, {s.m, s.n}, dt);
 }
 
 TensorImpl matmul_hip(const TensorImpl& a, const TensorImpl& b) {
@@ -273,28 +287,17 @@ TensorImpl matmul_t_hip(const TensorImpl& a, const TensorImpl& b, bool ta, bool 
   return gemm_hip(a, b, ta, tb);
 }
 
+// c += op(a) op(b) for a gradient c, accumulated by the GEMM.  The product's
+// promoted dtype must be c's, as add_inplace requires identical dtypes
+// (native/memory_ops.cpp:28-35).
 void matmul_acc_hip(TensorImpl& c, const TensorImpl& a, const TensorImpl& b, bool ta,
                     bool tb) {
-  LMP_CHECK(a.shape().size() == 2 && b.shape().size() == 2 && c.shape().size() == 2)
-      << "Both matrices must be 2D.";
-  const size_t m = ta ? a.shape()[1] : a.shape()[0];
-  const size_t k = ta ? a.shape()[0] : a.shape()[1];
-  const size_t kb = tb ? b.shape()[1] : b.shape()[0];
-  const size_t n = tb ? b.shape()[0] : b.shape()[1];
-  LMP_CHECK(k == kb) << "Incompatible matrix dimensions for multiplication.";
-  LMP_CHECK(c.shape()[0] == m && c.shape()[1] == n) << "matmul_acc: output shape mismatch";
-  LMP_CHECK(a.type() == DataType::Float32 && b.type() == DataType::Float32 &&
-            c.type() == DataType::Float32)
-      << "matmul on the HIP device supports Float32";
-  if (!m || !n) return;
-  void* pa = mut(a);
-  void* pb = mut(b);
-  void* pc = c.data();
-  count_launch();
-  hip_ok(lmp_k_gemm_f32(ta, tb, m, n, k, static_cast<const float*>(pa), a.shape()[1],
-                        static_cast<const float*>(pb), b.shape()[1], static_cast<float*>(pc),
-                        n, 1),
-         "lmp_k_gemm_f32");
+  const GemmShape s = gemm_shape(a, b, ta, tb);
+  LMP_CHECK(c.shape().size() == 2 && c.shape()[0] == s.m && c.shape()[1] == s.n)
+      << "add_inplace requires tensors with identical shapes";
+  const DataType dt = type_upcast(a.type(), b.type());
+  LMP_CHECK(dt == c.type()) << "add_inplace requires tensors with identical dtypes";
+  gemm_into(c.data(), dt, a, b, ta, tb, s, true);
 }
 
 TensorImpl transpose_hip(const TensorImpl& a) {

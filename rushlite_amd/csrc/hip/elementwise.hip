@@ -346,7 +346,7 @@ __global__ __launch_bounds__(kBlock) void add_inplace_scalar(
   const uint64_t stride = uint64_t(gridDim.x) * kBlock;
   for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n;
        i += stride)
-    dst[i] = dst[i] + src[i];
+    dst[i] = binary_apply<LMP_BIN_ADD, T>(dst[i], src[i], T(0), T(0));
 }
 
 __global__ __launch_bounds__(kBlock) void add_inplace_f32_vec(
@@ -393,10 +393,6 @@ int lmp_k_binary(int op, int dtype, void* out, const void* a, const void* b,
   const Coalesced c = coalesce(*desc);
   return with_dtype(dtype, [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
-    if constexpr (std::is_same_v<T, bool>) {
-      if (op == LMP_BIN_POW || op == LMP_BIN_DIV)
-        return fail(LMP_ERR_UNSUPPORTED, "pow/div on Bool tensors");
-    }
     return dispatch_bin<T>(op, static_cast<T*>(out), static_cast<const T*>(a),
                            static_cast<const T*>(b), c, p0, p1);
   });
@@ -408,12 +404,8 @@ int lmp_k_unary(int op, int dtype, void* out, const void* in, size_t n,
   if (!out || !in) return fail(LMP_ERR_INVALID, "lmp_k_unary: null buffer");
   return with_dtype(dtype, [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
-    if constexpr (std::is_same_v<T, bool>) {
-      return fail(LMP_ERR_UNSUPPORTED, "unary ops on Bool tensors");
-    } else {
-      return dispatch_unary<T>(op, static_cast<T*>(out), static_cast<const T*>(in),
-                               n, p0, p1);
-    }
+    return dispatch_unary<T>(op, static_cast<T*>(out), static_cast<const T*>(in), n, p0,
+                             p1);
   });
 }
 

@@ -1,0 +1,293 @@
+// GEMM for the non-fp32 dtypes: float64 on the matrix cores
+// (v_mfma_f64_16x16x4f64) and bool / int16 / int32 / int64 on the vector ALUs.
+//
+// Lamp3 instantiates its matmul for every dtype (matrix.cu:208-216,
+// cpu/matrix.cpp:44-52) with the semantics of cpu/matrix.cpp:8-18: the sum
+// starts at 0 in the output type and adds static_cast<Out>(a) *
+// static_cast<Out>(b).  For the integer types that is arithmetic modulo 2^bits
+// (int16 products are formed in int and truncated when stored back), which
+// the kernels reproduce with unsigned accumulators of the output's width so no
+// signed overflow occurs; for bool every product is a && b and the sum is an
+// OR.  Operands arrive already cast to the output type.
+//
+// float64 tiling.  A workgroup of 4 waves owns a 64 x 64 tile of C; each wave
+// owns 2 x 2 blocks of 16 x 16 accumulated by v_mfma_f64_16x16x4f64 (lane l
+// supplies A[l % 16][l / 16] and B[l / 16][l % 16]; accumulator register r
+// holds row 4r + l / 16, column l % 16).  K advances 16 at a time through two
+// LDS buffers with register prefetch of the next tile, one barrier per step.
+// The integer kernel uses the same 64 x 64 tiles staged through LDS, each
+// thread owning a 4 x 4 block of C.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace lmp_hip {
+
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTile = 64;
+constexpr int kBK = 16;
+
+struct TypedArgs {
+  const void* a;
+  const void* b;
+  void* c;
+  int m, n, k;
+  int lda, ldb, ldc;
+  int accumulate;
+};
+
+// Thread f's element of a [kTile x kBK] A tile (row-major in k when !TA) or a
+// [kBK x kTile] B tile, loaded so consecutive threads read consecutive
+// addresses of the stored matrix.  Returns the tile coordinates (r, c) as
+// (m or n index, k index) and the value, zero outside the matrix.
+template <typename T, bool TRANS_CONTIG_K>
+__device__ __forceinline__ T load_elem(const T* __restrict__ p, int ld, int f, int base,
+                                       int k0, int extent, int K, int* idx, int* kk) {
+  // TRANS_CONTIG_K: the stored matrix is contiguous along k ([extent][K]).
+  int r, c;
+  if constexpr (TRANS_CONTIG_K) {
+    r = f / kBK;
+    c = f % kBK;
+  } else {
+    c = f / kTile;
+    r = f % kTile;
+  }
+  *idx = r;
+  *kk = c;
+  const int gr = base + r, gk = k0 + c;
+  if (gr >= extent || gk >= K) return T(0);
+  return TRANS_CONTIG_K ? p[int64_t(gr) * ld + gk] : p[int64_t(gk) * ld + gr];
+}
+
+// A is op(A)[m][k]: stored [m][k] (contiguous in k) unless TA.
+// B is op(B)[k][n]: stored [k][n] (contiguous in n) unless TB.
+template <typename T, bool TA, bool TB, int PER>
+struct TileLoader {
+  T av[PER], bv[PER];
+  int ai[PER], ak[PER], bi[PER], bk[PER];
+
+  __device__ __forceinline__ void load(const TypedArgs& g, int m0, int n0, int k0) {
+    const T* A = static_cast<const T*>(g.a);
+    const T* B = static_cast<const T*>(g.b);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int f = threadIdx.x + j * kThreads;
+      av[j] = load_elem<T, !TA>(A, g.lda, f, m0, k0, g.m, g.k, &ai[j], &ak[j]);
+      bv[j] = load_elem<T, TB>(B, g.ldb, f, n0, k0, g.n, g.k, &bi[j], &bk[j]);
+    }
+  }
+  // LDS layout: As[k][m], Bs[k][n] (pitch kTile + 1).
+  __device__ __forceinline__ void store(T* As, T* Bs) const {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      As[ak[j] * (kTile + 1) + ai[j]] = av[j];
+      Bs[bk[j] * (kTile + 1) + bi[j]] = bv[j];
+    }
+  }
+};
+
+constexpr int kPer = kTile * kBK / kThreads;  // 4 elements of A and of B per thread
+constexpr int kLds = kBK * (kTile + 1);
+
+// ------------------------------------------------------------------ float64
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(kThreads) void gemm_f64_mfma(TypedArgs g) {
+  __shared__ double smem[2][2][kLds];  // [buffer][A|B]
+  const int tiles_n = (g.n + kTile - 1) / kTile;
+  const int m0 = int(blockIdx.x / tiles_n) * kTile, n0 = int(blockIdx.x % tiles_n) * kTile;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 15, lk = lane >> 4;
+
+  v4d acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v4d{0.0, 0.0, 0.0, 0.0};
+
+  TileLoader<double, TA, TB, kPer> ld;
+  const int k_tiles = (g.k + kBK - 1) / kBK;
+  ld.load(g, m0, n0, 0);
+  ld.store(smem[0][0], smem[0][1]);
+  __syncthreads();
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < k_tiles;
+    if (more) ld.load(g, m0, n0, (kt + 1) * kBK);
+    const double* As = smem[cur][0];
+    const double* Bs = smem[cur][1];
+#pragma unroll
+    for (int s = 0; s < kBK / 4; ++s) {
+      const int kk = 4 * s + lk;
+      double af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = As[kk * (kTile + 1) + wm * 32 + i * 16 + li];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = Bs[kk * (kTile + 1) + wn * 32 + j * 16 + li];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) ld.store(smem[cur ^ 1][0], smem[cur ^ 1][1]);
+    __syncthreads();
+  }
+
+  double* C = static_cast<double*>(g.c);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + wn * 32 + j * 16 + li;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 32 + i * 16 + 4 * r + lk;
+        if (row < g.m && col < g.n) {
+          double* p = C + int64_t(row) * g.ldc + col;
+          *p = g.accumulate ? *p + acc[i][j][r] : acc[i][j][r];
+        }
+      }
+    }
+}
+
+// ------------------------------------------------------------ bool / ints
+
+// Accumulator of each output type: wrap-around unsigned arithmetic of the
+// output's width (int16 accumulates in 32 bits and is truncated on store,
+// which is the same residue), or OR of ANDs for bool.
+template <typename T> struct IntAcc { using U = std::make_unsigned_t<T>; };
+template <> struct IntAcc<int16_t> { using U = uint32_t; };
+template <> struct IntAcc<bool> { using U = bool; };
+
+template <typename T>
+__device__ __forceinline__ typename IntAcc<T>::U mac(typename IntAcc<T>::U acc, T a, T b) {
+  using U = typename IntAcc<T>::U;
+  if constexpr (std::is_same_v<T, bool>) {
+    return acc || (a && b);
+  } else {
+    return U(acc + U(U(a) * U(b)));
+  }
+}
+
+template <typename T, bool TA, bool TB>
+__global__ __launch_bounds__(kThreads) void gemm_int(TypedArgs g) {
+  using U = typename IntAcc<T>::U;
+  __shared__ T As[kLds], Bs[kLds];
+  const int tiles_n = (g.n + kTile - 1) / kTile;
+  const int m0 = int(blockIdx.x / tiles_n) * kTile, n0 = int(blockIdx.x % tiles_n) * kTile;
+  const int tr = threadIdx.x / 16, tc = threadIdx.x % 16;  // rows tr + 16i, cols tc + 16j
+  U acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = U(0);
+
+  TileLoader<T, TA, TB, kPer> ld;
+  for (int k0 = 0; k0 < g.k; k0 += kBK) {
+    ld.load(g, m0, n0, k0);
+    ld.store(As, Bs);
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kBK; ++kk) {
+      T a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[kk * (kTile + 1) + tr + 16 * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[kk * (kTile + 1) + tc + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mac<T>(acc[i][j], a[i], b[j]);
+    }
+    __syncthreads();
+  }
+
+  T* C = static_cast<T*>(g.c);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = m0 + tr + 16 * i, col = n0 + tc + 16 * j;
+      if (row >= g.m || col >= g.n) continue;
+      T* p = C + int64_t(row) * g.ldc + col;
+      if constexpr (std::is_same_v<T, bool>) {
+        *p = g.accumulate ? (*p || acc[i][j]) : acc[i][j];
+      } else {
+        *p = g.accumulate ? T(U(U(*p) + acc[i][j])) : T(acc[i][j]);
+      }
+    }
+}
+
+template <typename T, bool TA, bool TB>
+void launch_typed(Runtime* rt, const TypedArgs& g) {
+  const int64_t tiles = int64_t((g.m + kTile - 1) / kTile) * ((g.n + kTile - 1) / kTile);
+  if constexpr (std::is_same_v<T, double>)
+    hipLaunchKernelGGL((gemm_f64_mfma<TA, TB>), dim3(uint32_t(tiles)), dim3(kThreads), 0,
+                       rt->stream, g);
+  else
+    hipLaunchKernelGGL((gemm_int<T, TA, TB>), dim3(uint32_t(tiles)), dim3(kThreads), 0,
+                       rt->stream, g);
+}
+
+template <typename T>
+int dispatch_typed(Runtime* rt, bool ta, bool tb, const TypedArgs& g) {
+  if (!ta && !tb) launch_typed<T, false, false>(rt, g);
+  else if (!ta && tb) launch_typed<T, false, true>(rt, g);
+  else if (ta && !tb) launch_typed<T, true, false>(rt, g);
+  else launch_typed<T, true, true>(rt, g);
+  LMP_LAUNCH_CHECK("gemm (typed)");
+  return LMP_OK;
+}
+
+}  // namespace
+}  // namespace lmp_hip
+
+using namespace lmp_hip;
+
+extern "C" int lmp_k_gemm(int dtype, int trans_a, int trans_b, size_t m, size_t n, size_t k,
+                          const void* a, size_t lda, const void* b, size_t ldb, void* c,
+                          size_t ldc, int accumulate) {
+  if (dtype == LMP_FLOAT32)
+    return lmp_k_gemm_f32(trans_a, trans_b, m, n, k, static_cast<const float*>(a), lda,
+                          static_cast<const float*>(b), ldb, static_cast<float*>(c), ldc,
+                          accumulate);
+  if (dtype != LMP_FLOAT64 && dtype != LMP_INT64 && dtype != LMP_INT32 &&
+      dtype != LMP_INT16 && dtype != LMP_BOOL)
+    return fail(LMP_ERR_INVALID, "gemm: unknown dtype");
+  if (m == 0 || n == 0) return LMP_OK;
+  if (!c) return fail(LMP_ERR_INVALID, "gemm: null output");
+  if (k == 0) {
+    if (accumulate) return LMP_OK;
+    if (ldc != n) return fail(LMP_ERR_UNSUPPORTED, "gemm: k == 0 with ldc != n");
+    return lmp_k_fill(dtype, c, m * n, 0.0);
+  }
+  if (!a || !b) return fail(LMP_ERR_INVALID, "gemm: null input");
+  const size_t lim = 0x7fffffff;
+  if (m > lim || n > lim || k > lim || lda > lim || ldb > lim || ldc > lim)
+    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension above 2^31");
+  if ((trans_a ? lda < m : lda < k) || (trans_b ? ldb < k : ldb < n) || ldc < n)
+    return fail(LMP_ERR_INVALID, "gemm: leading dimension too small");
+  const uint64_t tiles = uint64_t((m + kTile - 1) / kTile) * ((n + kTile - 1) / kTile);
+  if (tiles > 0x7fffffffull) return fail(LMP_ERR_UNSUPPORTED, "gemm: grid too large");
+  LMP_RUNTIME_OR_FAIL(rt);
+  TypedArgs g{a, b, c, int(m), int(n), int(k), int(lda), int(ldb), int(ldc),
+              accumulate ? 1 : 0};
+  const bool ta = trans_a != 0, tb = trans_b != 0;
+  switch (dtype) {
+    case LMP_FLOAT64: return dispatch_typed<double>(rt, ta, tb, g);
+    case LMP_INT64: return dispatch_typed<int64_t>(rt, ta, tb, g);
+    case LMP_INT32: return dispatch_typed<int32_t>(rt, ta, tb, g);
+    case LMP_INT16: return dispatch_typed<int16_t>(rt, ta, tb, g);
+    default: return dispatch_typed<bool>(rt, ta, tb, g);
+  }
+}

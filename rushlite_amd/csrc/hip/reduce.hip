@@ -384,14 +384,37 @@ int reduce_cols(Runtime* rt, T* out, const T* in, uint64_t outer, uint64_t len,
   return LMP_OK;
 }
 
+// An empty reduced axis leaves every output at the functor's identity
+// (cpu/reduct.cpp:15-19 folds nothing into it).
+template <int OP, typename T>
+__global__ __launch_bounds__(kBlock) void fill_identity(T* __restrict__ out, uint64_t n) {
+  const uint64_t stride = uint64_t(gridDim.x) * kBlock;
+  for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+    out[i] = Reducer<OP, T>::identity();
+}
+
+template <int OP, typename T>
+int reduce_any(Runtime* rt, T* out, const T* in, uint64_t outer, uint64_t len,
+               uint64_t inner) {
+  if (len == 0) {
+    const uint64_t n = outer * inner;
+    hipLaunchKernelGGL((fill_identity<OP, T>),
+                       dim3(uint32_t(std::min<uint64_t>((n + kBlock - 1) / kBlock, 65536))),
+                       dim3(kBlock), 0, rt->stream, out, n);
+    LMP_LAUNCH_CHECK("fill_identity");
+    return LMP_OK;
+  }
+  return inner == 1 ? reduce_rows<OP, T>(rt, out, in, outer, len)
+                    : reduce_cols<OP, T>(rt, out, in, outer, len, inner);
+}
+
 template <typename T>
 int dispatch_reduce(int op, Runtime* rt, T* out, const T* in, uint64_t outer,
                     uint64_t len, uint64_t inner) {
   switch (op) {
-#define LMP_CASE(OPV)                                                      \
-  case OPV:                                                                \
-    return inner == 1 ? reduce_rows<OPV, T>(rt, out, in, outer, len)       \
-                      : reduce_cols<OPV, T>(rt, out, in, outer, len, inner);
+#define LMP_CASE(OPV) \
+  case OPV:           \
+    return reduce_any<OPV, T>(rt, out, in, outer, len, inner);
     LMP_CASE(LMP_RED_SUM)
     LMP_CASE(LMP_RED_MAX)
     LMP_CASE(LMP_RED_MIN)
@@ -410,15 +433,7 @@ using namespace lmp_hip;
 extern "C" int lmp_k_reduce(int op, int dtype, void* out, const void* in,
                             size_t outer, size_t len, size_t inner) {
   if (outer == 0 || inner == 0) return LMP_OK;
-  if (!out || !in) return fail(LMP_ERR_INVALID, "lmp_k_reduce: null buffer");
-  if (len == 0) {
-    // Empty reduced axis: every output is the identity.
-    double id = 0.0;
-    if (op == LMP_RED_PROD) id = 1.0;
-    else if (op == LMP_RED_MAX || op == LMP_RED_MIN)
-      return fail(LMP_ERR_INVALID, "max/min over an empty axis");
-    return lmp_k_fill(dtype, out, outer * inner, id);
-  }
+  if (!out || (!in && len)) return fail(LMP_ERR_INVALID, "lmp_k_reduce: null buffer");
   LMP_RUNTIME_OR_FAIL(rt);
   switch (dtype) {
     case LMP_FLOAT32:
@@ -436,6 +451,9 @@ extern "C" int lmp_k_reduce(int op, int dtype, void* out, const void* in,
     case LMP_INT16:
       return dispatch_reduce<int16_t>(op, rt, static_cast<int16_t*>(out),
                                       static_cast<const int16_t*>(in), outer, len, inner);
+    case LMP_BOOL:
+      return dispatch_reduce<bool>(op, rt, static_cast<bool*>(out),
+                                   static_cast<const bool*>(in), outer, len, inner);
     default:
       return fail(LMP_ERR_UNSUPPORTED,
                   std::string("lmp_k_reduce: dtype ") + dtype_name(dtype));

@@ -28,7 +28,7 @@ def declared_functions():
 
 def test_header_declares_the_abi():
     names = declared_functions()
-    assert len(names) == 31
+    assert len(names) == 32
     for group in ("lmp_rt_malloc", "lmp_k_binary", "lmp_k_reduce", "lmp_k_gemm_f32",
                   "lmp_jit_compile"):
         assert group in names

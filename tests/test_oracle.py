@@ -374,3 +374,119 @@ def test_mlp_step_gemm_orders_vs_torch(oracle):
         got = [gw[0], gb[0], gw[1], gb[1]]
         for g, w in zip(got, want):
             assert np.max(np.abs(g - w)) / np.max(np.abs(w)) < 1e-5
+
+
+# ------------------------------------------------ typed (non-fp32) oracle
+
+from oracle import lamp_typed as T  # noqa: E402
+
+_INT_BITS = {np.int16: 16, np.int32: 32, np.int64: 64}
+
+
+def _signed(v: int, bits: int) -> int:
+    v &= (1 << bits) - 1
+    return v - (1 << bits) if v >> (bits - 1) else v
+
+
+def _cdiv(x: int, y: int) -> int:
+    q = abs(x) // abs(y)
+    return q if (x < 0) == (y < 0) else -q
+
+
+@pytest.mark.parametrize("dt", [np.int16, np.int32, np.int64])
+def test_typed_int_arithmetic_vs_python_ints(dt):
+    """Wrap-around add/sub/mul and truncating division against Python's exact
+    integers reduced modulo 2^bits (the two's-complement results the
+    reference's C++ kernels produce), extremes included."""
+    bits = _INT_BITS[dt]
+    info = np.iinfo(dt)
+    rng = np.random.default_rng(bits)
+    a = np.concatenate([rng.integers(info.min, info.max, 400, dtype=dt, endpoint=True),
+                        np.array([info.min, info.max, -1, 0, 1, 7, -7], dt)])
+    b = np.concatenate([rng.integers(info.min, info.max, 400, dtype=dt, endpoint=True),
+                        np.array([1, -1, 2, 3, -2, 2, -2], dt)])
+    for op, f in (("add", lambda x, y: x + y), ("sub", lambda x, y: x - y),
+                  ("mul", lambda x, y: x * y)):
+        got = T.binary(op, a, b)
+        assert got.dtype == dt
+        want = [_signed(f(int(x), int(y)), bits) for x, y in zip(a, b)]
+        assert got.tolist() == want, op
+    ok = (b != 0) & ~((a == info.min) & (b == -1))
+    got = T.binary("div", a[ok], b[ok])
+    assert got.tolist() == [_cdiv(int(x), int(y)) for x, y in zip(a[ok], b[ok])]
+    assert T.binary("div", np.array([-7, 7, -7], dt), np.array([2, -2, -2], dt)).tolist() == [-3, -3, 3]
+
+
+def test_typed_bool_arithmetic_is_cpp_bool():
+    """bool + bool etc. promote to int and convert back (nonzero -> true)."""
+    t = np.array([False, False, True, True])
+    u = np.array([False, True, False, True])
+    assert T.binary("add", t, u).tolist() == [bool(int(x) + int(y)) for x, y in zip(t, u)]
+    assert T.binary("sub", t, u).tolist() == [bool(int(x) - int(y)) for x, y in zip(t, u)]
+    assert T.binary("mul", t, u).tolist() == [bool(int(x) * int(y)) for x, y in zip(t, u)]
+    assert T.binary("eq", t, u).tolist() == [x == y for x, y in zip(t, u)]
+    assert T.unary("neg", t).tolist() == t.tolist()
+    assert T.reduce("sum", np.array([[0, 1], [0, 0]], bool), 0).tolist() == [[False, True]]
+    assert T.reduce("prod", np.array([[1, 1], [0, 1]], bool), 0).tolist() == [[False, True]]
+
+
+def test_typed_promotion_and_casts():
+    """Promotion is the larger DataType code; float -> int truncates."""
+    names = [np.bool_, np.int16, np.int32, np.int64, np.float32, np.float64]
+    for i, x in enumerate(names):
+        for j, y in enumerate(names):
+            got = T.binary("add", np.zeros(2, x), np.zeros(2, y)).dtype
+            assert got == np.dtype(names[max(i, j)])
+    assert T.cast(np.array([2.7, -2.7, 0.5]), np.int32).tolist() == [2, -2, 0]
+    # int32 + float32: the int is rounded to float32 before the add
+    got = T.binary("add", np.array([16777217], np.int32), np.array([0.0], np.float32))
+    assert got.dtype == np.float32 and got.tolist() == [16777216.0]
+
+
+def test_typed_int_transcendentals_truncate():
+    x = np.array([0, 1, 2, 3, 10], np.int32)
+    assert T.unary("exp", x).tolist() == [1, 2, 7, 20, 22026]
+    assert T.unary("sqrt", np.array([10, 16, 99], np.int64)).tolist() == [3, 4, 9]
+    assert T.unary("log", np.array([1, 2, 100], np.int16)).tolist() == [0, 0, 4]
+    assert T.unary("neg", np.array([-32768, 5], np.int16)).tolist() == [-32768, -5]
+    assert T.unary("clamp", np.array([-5, 3, 9], np.int32), 0.0, 4.7).tolist() == [0, 3, 4]
+    assert T.binary("pow", np.array([2, 3, -2], np.int32), np.array([10, 3, 3], np.int32)).tolist() == [1024, 27, -8]
+
+
+def test_typed_reductions():
+    x = np.array([[30000, 1], [30000, 2]], np.int16)
+    assert T.reduce("sum", x, 0).tolist() == [[_signed(60000, 16), 3]]
+    assert T.reduce("prod", np.array([[65536], [65536]], np.int64), 0).tolist() == [[2 ** 32]]
+    assert T.reduce("max", np.array([[np.nan], [1.0]]), 0).tolist() == [[1.0]]
+    assert T.reduce("max", np.array([[1.0], [np.nan]]), 0).tolist() == [[1.0]]
+    assert T.reduce("min", np.zeros((0, 2), np.int32), 0).tolist() == [[2 ** 31 - 1] * 2]
+    assert T.reduce("max", np.zeros((0, 1)), 0).tolist() == [[-np.finfo(np.float64).max]]
+    v = np.random.default_rng(3).standard_normal((50, 3))
+    np.testing.assert_allclose(T.reduce("sum", v, 0)[0], [sum(c) for c in v.T], rtol=1e-14)
+
+
+@pytest.mark.parametrize("dt", [np.int16, np.int32, np.int64, np.bool_])
+def test_typed_matmul_vs_brute_force(dt):
+    rng = np.random.default_rng(7)
+    if dt is np.bool_:
+        a, b = rng.random((5, 7)) < 0.3, rng.random((7, 4)) < 0.3
+        want = [[any(a[i, k] and b[k, j] for k in range(7)) for j in range(4)] for i in range(5)]
+    else:
+        info, bits = np.iinfo(dt), _INT_BITS[dt]
+        a = rng.integers(info.min, info.max, (5, 7), dtype=dt, endpoint=True)
+        b = rng.integers(info.min, info.max, (7, 4), dtype=dt, endpoint=True)
+        want = [[_signed(sum(int(a[i, k]) * int(b[k, j]) for k in range(7)), bits)
+                 for j in range(4)] for i in range(5)]
+    got = T.matmul(a, b)
+    assert got.dtype == np.dtype(dt) and got.tolist() == want
+
+
+def test_typed_float64_ops_are_ieee():
+    """numpy float64 arithmetic is the IEEE double arithmetic of the C++
+    kernels: pin against Python floats (also binary64)."""
+    xs = [0.1, -3.5, 1e300, 2.0 ** -1074, 7.0]
+    ys = [0.2, 1e-300, 3.0, -0.0, 7.0]
+    a, b = np.array(xs), np.array(ys)
+    assert T.binary("add", a, b).tolist() == [x + y for x, y in zip(xs, ys)]
+    assert T.binary("mul", a, b).tolist() == [x * y for x, y in zip(xs, ys)]
+    assert T.binary("div", a[:4], b[:4] + 1).tolist() == [x / (y + 1) for x, y in zip(xs[:4], ys[:4])]
