@@ -2,7 +2,8 @@
 // nvrtc_backend.cpp:145-192, fused_graph.cpp:6-35, codegen.cpp:21-61).
 //
 // realize(root) grows one region backwards from the root through deferred
-// fp32 elementwise nodes; every other input (already realised tensors, and
+// elementwise nodes of one float type (float32, or float64 on the indexed
+// path); every other input (already realised tensors, and
 // non-fusible or too-distant pending nodes, which are realised first) becomes
 // a leaf, deduplicated by identity so `a*a` loads `a` once.  Unlike the
 // reference, operands of different shapes fuse: every leaf is indexed from
@@ -43,12 +44,16 @@ struct Region {
   std::unordered_map<TensorImpl*, int> node_of;
 };
 
+// Regions are homogeneous float32 or float64: a node fuses when it and all
+// of its inputs have one of those types and the same one.
 bool fusible_node(const TensorImpl* t) {
-  if (!t->is_deferred() || t->type() != DataType::Float32) return false;
+  if (!t->is_deferred()) return false;
+  const DataType dt = t->type();
+  if (dt != DataType::Float32 && dt != DataType::Float64) return false;
   const auto& fn = t->lazy_op();
   if (!fn->is_fusible()) return false;
   for (const auto& in : fn->inputs)
-    if (in->type() != DataType::Float32) return false;
+    if (in->type() != dt) return false;
   return true;
 }
 
@@ -111,13 +116,14 @@ struct Plan {
   int64_t cols4 = 0;   // vec: float4s per row
 };
 
-Plan make_plan(const Region& r, const std::vector<size_t>& shape) {
+Plan make_plan(const Region& r, const std::vector<size_t>& shape, bool f64) {
   Plan p;
   p.n = shape_numel(shape);
   std::vector<std::vector<stride_t>> strides;
   for (TensorImpl* leaf : r.leaves) strides.push_back(padded_strides(leaf->shape(), shape.size()));
   p.groups = coalesce(shape, strides);
-  if (p.groups.size() > 2 || p.n / 4 >= (1ull << 31)) return p;
+  // The float4 plan is float32 only; float64 regions use the indexed loop.
+  if (f64 || p.groups.size() > 2 || p.n / 4 >= (1ull << 31)) return p;
   const int64_t cols = p.groups.empty() ? 1 : p.groups[0].extent;
   if (cols % 4 != 0) return p;
   for (size_t l = 0; l < r.leaves.size(); ++l) {
@@ -148,7 +154,13 @@ uint64_t fnv1a(const std::vector<int64_t>& words) {
   return h;
 }
 
-int64_t float_bits(Scalar v) {
+// A clamp bound as the kernel will see it: float bits, or double bits.
+int64_t bound_bits(Scalar v, bool f64) {
+  if (f64) {
+    int64_t b;
+    std::memcpy(&b, &v, sizeof b);
+    return b;
+  }
   const float f = static_cast<float>(v);
   uint32_t b;
   std::memcpy(&b, &f, sizeof b);
@@ -156,9 +168,10 @@ int64_t float_bits(Scalar v) {
 }
 
 std::vector<int64_t> signature(const Region& r, const std::vector<size_t>& shape,
-                               const Plan& p) {
+                               const Plan& p, bool f64) {
   std::vector<int64_t> s;
   s.push_back(0x4c4d5046);  // tag
+  s.push_back(f64 ? 8 : 4);
   s.push_back(static_cast<int64_t>(shape.size()));
   for (size_t d : shape) s.push_back(static_cast<int64_t>(d));
   s.push_back(static_cast<int64_t>(r.leaves.size()));
@@ -172,8 +185,8 @@ std::vector<int64_t> signature(const Region& r, const std::vector<size_t>& shape
     const auto& fn = n->lazy_op();
     s.push_back(static_cast<int64_t>(fn->kind()) * 256 + fn->code());
     if (fn->kind() == lazy::OpKind::Unary && fn->code() == LMP_UN_CLAMP) {
-      s.push_back(float_bits(fn->param0()));
-      s.push_back(float_bits(fn->param1()));
+      s.push_back(bound_bits(fn->param0(), f64));
+      s.push_back(bound_bits(fn->param1(), f64));
     }
     for (const auto& in : fn->inputs) {
       auto it = r.leaf_of.find(in.get());
@@ -198,7 +211,7 @@ std::string substitute(std::string tmpl, const std::vector<std::string>& args) {
 // Emit the SSA chain for one lane value; `leaf(l)` spells leaf l's value.
 template <typename LeafName>
 void emit_chain(std::ostringstream& os, const Region& r, const std::string& indent,
-                const std::string& dst, LeafName leaf) {
+                const std::string& dst, const char* type, LeafName leaf) {
   for (size_t m = 0; m < r.nodes.size(); ++m) {
     const auto& fn = r.nodes[m]->lazy_op();
     std::vector<std::string> args;
@@ -207,7 +220,7 @@ void emit_chain(std::ostringstream& os, const Region& r, const std::string& inde
       args.push_back(it != r.leaf_of.end() ? leaf(it->second)
                                            : "t" + std::to_string(r.node_of.at(in.get())));
     }
-    os << indent << "const float t" << m << " = " << substitute(fn->codegen_expr(), args)
+    os << indent << "const " << type << " t" << m << " = " << substitute(fn->codegen_expr(), args)
        << ";\n";
   }
   os << indent << dst << " = t" << (r.nodes.size() - 1) << ";\n";
@@ -218,15 +231,19 @@ typedef float lmp_v4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float lmp_clamp(float x, float lo, float hi) {
   return x < lo ? lo : (x > hi ? hi : x);
 }
+__device__ __forceinline__ double lmp_clamp(double x, double lo, double hi) {
+  return x < lo ? lo : (x > hi ? hi : x);
+}
 )";
 
-std::string codegen(const Region& r, const Plan& p, const std::string& name) {
+std::string codegen(const Region& r, const Plan& p, const std::string& name, bool f64) {
+  const char* T = f64 ? "double" : "float";
   std::ostringstream os;
   os << kPrelude;
   os << "extern \"C\" __global__ __launch_bounds__(" << kBlock << ") void " << name
-     << "(float* __restrict__ out";
+     << "(" << T << "* __restrict__ out";
   for (size_t l = 0; l < r.leaves.size(); ++l)
-    os << ", const float* __restrict__ in" << l;
+    os << ", const " << T << "* __restrict__ in" << l;
   os << ") {\n";
   const size_t nl = r.leaves.size();
   if (p.vec) {
@@ -254,7 +271,7 @@ std::string codegen(const Region& r, const Plan& p, const std::string& name) {
     const char* comp[4] = {"x", "y", "z", "w"};
     for (int c = 0; c < 4; ++c) {
       os << "  {\n";
-      emit_chain(os, r, "    ", std::string("o.") + comp[c], [&](int l) {
+      emit_chain(os, r, "    ", std::string("o.") + comp[c], T, [&](int l) {
         const bool contig = !p.groups.empty() && p.groups[0].stride[l] == 1;
         return "s" + std::to_string(l) + (contig ? std::string(".") + comp[c] : "");
       });
@@ -276,8 +293,8 @@ std::string codegen(const Region& r, const Plan& p, const std::string& name) {
           os << "      o" << l << " += c * " << p.groups[g].stride[l] << "ul;\n";
       os << "    }\n";
     }
-    os << "    float res;\n    {\n";
-    emit_chain(os, r, "      ", "res", [&](int l) {
+    os << "    " << T << " res;\n    {\n";
+    emit_chain(os, r, "      ", "res", T, [&](int l) {
       return "in" + std::to_string(l) + "[o" + std::to_string(l) + "]";
     });
     os << "    }\n    out[i] = res;\n  }\n}\n";
@@ -303,20 +320,21 @@ class HipFusionBackend : public lazy::LazyBackend {
     }
     Region r;
     grow(root, r, true);
+    const bool f64 = root->type() == DataType::Float64;
     const std::vector<size_t> shape = root->shape();
     const size_t n = shape_numel(shape);
-    Storage out(n * sizeof(float), DeviceType::HIP);
+    Storage out(n * dtype_size(root->type()), DeviceType::HIP);
     if (n == 0) {
       root->set_realized(out);
       return;
     }
-    const Plan p = make_plan(r, shape);
-    std::vector<int64_t> sig = signature(r, shape, p);
+    const Plan p = make_plan(r, shape, f64);
+    std::vector<int64_t> sig = signature(r, shape, p, f64);
     const uint64_t key = fnv1a(sig);
     void* handle = lookup(key, sig);
     if (!handle) {
       const std::string name = "lmp_fused";
-      const std::string src = codegen(r, p, name);
+      const std::string src = codegen(r, p, name, f64);
       hip_ok(lmp_jit_compile(key, src.c_str(), name.c_str(), &handle), "lmp_jit_compile");
       std::lock_guard<std::mutex> lock(mu_);
       cache_[key] = Compiled{handle, std::move(sig)};
@@ -367,7 +385,8 @@ std::string fused_source_for(TensorImpl* root) {
   LMP_CHECK(root->is_deferred()) << "tensor has no pending graph";
   Region r;
   grow(root, r, true);
-  return codegen(r, make_plan(r, root->shape()), "lmp_fused");
+  const bool f64 = root->type() == DataType::Float64;
+  return codegen(r, make_plan(r, root->shape(), f64), "lmp_fused", f64);
 }
 
 }  // namespace lmp::tensor::hip

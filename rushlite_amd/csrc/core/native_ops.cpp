@@ -189,15 +189,28 @@ std::array<LazyBackend*, static_cast<size_t>(DeviceType::Count)>& registry() {
   return r;
 }
 
-// A Scalar bound converted to float on the host, as the eager launch does,
-// and spelled by its bit pattern so inf (from DBL_MAX) and -0.0 survive.
-std::string float_literal(Scalar v) {
-  const float f = static_cast<float>(v);
-  uint32_t bits;
-  std::memcpy(&bits, &f, sizeof bits);
+// A Scalar bound converted to the tensor's float type on the host, as the
+// eager launch does, and spelled by its bit pattern so inf (from DBL_MAX) and
+// -0.0 survive.
+std::string float_literal(Scalar v, bool f64) {
   std::ostringstream os;
-  os << "__uint_as_float(0x" << std::hex << bits << "u)";
+  if (f64) {
+    uint64_t bits;
+    std::memcpy(&bits, &v, sizeof bits);
+    os << "__longlong_as_double(0x" << std::hex << bits << "ll)";
+  } else {
+    const float f = static_cast<float>(v);
+    uint32_t bits;
+    std::memcpy(&bits, &f, sizeof bits);
+    os << "__uint_as_float(0x" << std::hex << bits << "u)";
+  }
   return os.str();
+}
+
+// Fused regions are float32 or float64 throughout; the spellings below call
+// the same device math functions the eager kernels call for that type.
+bool is_f64(const std::vector<std::shared_ptr<TensorImpl>>& ins) {
+  return ins[0]->type() == DataType::Float64;
 }
 
 struct BinaryFn : LazyFunction {
@@ -235,18 +248,23 @@ struct BinaryFn : LazyFunction {
     out.set_realized(r.storage());
   }
   std::string codegen_expr() const override {
+    const bool d = is_f64(inputs);
+    const std::string one = d ? "1.0" : "1.0f", zero = d ? "0.0" : "0.0f";
+    const auto cmp = [&](const char* op_text) {
+      return std::string("({0} ") + op_text + " {1} ? " + one + " : " + zero + ")";
+    };
     switch (op) {
       case LMP_BIN_ADD: return "({0} + {1})";
       case LMP_BIN_SUB: return "({0} - {1})";
       case LMP_BIN_MUL: return "({0} * {1})";
       case LMP_BIN_DIV: return "({0} / {1})";
-      case LMP_BIN_POW: return "powf({0}, {1})";
-      case LMP_BIN_EQ: return "({0} == {1} ? 1.0f : 0.0f)";
-      case LMP_BIN_NE: return "({0} != {1} ? 1.0f : 0.0f)";
-      case LMP_BIN_GE: return "({0} >= {1} ? 1.0f : 0.0f)";
-      case LMP_BIN_LE: return "({0} <= {1} ? 1.0f : 0.0f)";
-      case LMP_BIN_GT: return "({0} > {1} ? 1.0f : 0.0f)";
-      default: return "({0} < {1} ? 1.0f : 0.0f)";
+      case LMP_BIN_POW: return d ? "pow({0}, {1})" : "powf({0}, {1})";
+      case LMP_BIN_EQ: return cmp("==");
+      case LMP_BIN_NE: return cmp("!=");
+      case LMP_BIN_GE: return cmp(">=");
+      case LMP_BIN_LE: return cmp("<=");
+      case LMP_BIN_GT: return cmp(">");
+      default: return cmp("<");
     }
   }
 };
@@ -287,17 +305,21 @@ struct UnaryFn : LazyFunction {
   // GPU functor), which maps -0.0 to +0.0; the reference's fused spelling
   // `x < 0 ? -x : x` would keep -0.0 and disagree with its own eager path.
   std::string codegen_expr() const override {
+    const bool d = is_f64(inputs);
+    const auto fn = [&](const char* name) {
+      return std::string(name) + (d ? "" : "f") + "({0})";
+    };
     switch (op) {
       case LMP_UN_NEG: return "(-{0})";
-      case LMP_UN_EXP: return "expf({0})";
-      case LMP_UN_LOG: return "logf({0})";
-      case LMP_UN_SQRT: return "sqrtf({0})";
-      case LMP_UN_ABS: return "fabsf({0})";
-      case LMP_UN_SIN: return "sinf({0})";
-      case LMP_UN_COS: return "cosf({0})";
-      case LMP_UN_TAN: return "tanf({0})";
+      case LMP_UN_EXP: return fn("exp");
+      case LMP_UN_LOG: return fn("log");
+      case LMP_UN_SQRT: return fn("sqrt");
+      case LMP_UN_ABS: return fn("fabs");
+      case LMP_UN_SIN: return fn("sin");
+      case LMP_UN_COS: return fn("cos");
+      case LMP_UN_TAN: return fn("tan");
       default:
-        return "lmp_clamp({0}, " + float_literal(lo) + ", " + float_literal(hi) + ")";
+        return "lmp_clamp({0}, " + float_literal(lo, d) + ", " + float_literal(hi, d) + ")";
     }
   }
 };

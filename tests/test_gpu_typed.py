@@ -261,3 +261,49 @@ def test_known_answer_ops_per_reference_dtype(rsl, dt):
         check(rsl.pow(V(A), V([[10, 20]]) / 10), [1, 4, 3, 16, 5, 36])    # :717-727
     check(rsl.sum(V(A), 0), [9, 12])                               # :196-212
     check(rsl.sum(V(A), 1), [3, 7, 11])                            # :213-224
+
+
+def test_float64_capture_fuses_one_kernel_equal_to_eager(rsl):
+    """A captured float64 chain with [M,1] broadcasts becomes one hipRTC
+    kernel, bit-identical to the eager float64 kernels, and within 1e-14 of the
+    typed oracle under the normalised metric (exp is the only step that may
+    differ, by an ulp, and the subtraction can cancel, so ulps of the result
+    are not the measure)."""
+    rng = np.random.default_rng(21)
+    a_np, b_np = rng.standard_normal((257, 64)), rng.standard_normal((257, 1))
+    f64 = rsl.dtype.float64
+    a, b = rsl.Variable(a_np, dtype=f64), rsl.Variable(b_np, dtype=f64)
+    big = 1.7976931348623157e308
+
+    def chain():
+        return rsl.exp(a) * b - rsl.clamp(a, 0.0, big) / (b + 1.0)
+
+    s0 = rsl._stats()
+    with rsl.capture_on():
+        c = chain()
+        assert rsl._is_deferred(c)
+        src = rsl._fused_source(c)
+    got = c.numpy()
+    s1 = rsl._stats()
+    assert s1["fused_launches"] - s0["fused_launches"] == 1
+    assert "double" in src and "expf" not in src
+    eager = chain().numpy()
+    assert got.dtype == np.float64
+    assert np.array_equal(got.view(np.int64), eager.view(np.int64))
+    want = T.binary("sub", T.binary("mul", T.unary("exp", a_np), b_np),
+                    T.binary("div", T.unary("clamp", a_np, 0.0, big),
+                             T.binary("add", b_np, np.array([1.0]))))
+    assert rel_err(got, want) <= 1e-14
+
+
+def test_mixed_dtype_chain_under_capture_stays_correct(rsl):
+    """Nodes whose operands have different dtypes are not fused; capture must
+    still give the eager result (cast-then-operate)."""
+    i = rsl.Variable(np.arange(12, dtype=np.int32).reshape(3, 4), dtype=rsl.dtype.int32)
+    f = rsl.Variable(np.full((3, 1), 0.5, np.float32))
+    with rsl.capture_on():
+        c = (i * 3) + f
+    eager = ((i * 3) + f).numpy()
+    got = c.numpy()
+    assert got.dtype == np.float32 and np.array_equal(got, eager)
+    assert got.tolist() == (np.arange(12).reshape(3, 4) * 3 + 0.5).tolist()
