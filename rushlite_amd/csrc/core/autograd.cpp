@@ -130,9 +130,21 @@ void Variable::backward() {
     stack.pop_back();
   }
   std::reverse(topo.begin(), topo.end());
-  impl_->grad = tensor::ones_like(impl_->data);
+  {
+    // The gradient formulas are elementwise chains over tensors the pass
+    // already holds, so they run captured: each formula, with the first
+    // accumulation into a gradient (0 + g), becomes one fused kernel on a
+    // device with a lazy backend.  Values are those of the eager formulas
+    // (fused kernels equal eager ones bit for bit).
+    tensor::lazy::CaptureGuard capture(true);
+    impl_->grad = tensor::ones_like(impl_->data);
+    for (Variable& node : topo)
+      if (node.impl_->grad_fn) node.impl_->grad_fn->apply({node});
+  }
+  // No pending gradient outlives backward(): later in-place updates of the
+  // tensors a pending gradient reads must not change it.
   for (Variable& node : topo)
-    if (node.impl_->grad_fn) node.impl_->grad_fn->apply({node});
+    if (node.impl_->grad.defined()) node.impl_->grad.realize();
 }
 
 // ------------------------------------------------------------ op recording

@@ -42,6 +42,7 @@ struct Region {
   std::vector<TensorImpl*> nodes;  // topological, root last
   std::unordered_map<TensorImpl*, int> leaf_of;
   std::unordered_map<TensorImpl*, int> node_of;
+  std::unordered_map<TensorImpl*, long> owners;  // shared_ptr owners of each input
 };
 
 // Regions are homogeneous float32 or float64: a node fuses when it and all
@@ -64,16 +65,43 @@ void add_leaf(TensorImpl* t, Region& r) {
   r.leaves.push_back(t);
 }
 
-void grow(TensorImpl* t, Region& r, bool is_root) {
+void grow(TensorImpl* t, Region& r, bool is_root,
+          const std::unordered_set<TensorImpl*>& forced) {
   if (r.node_of.count(t) || r.leaf_of.count(t)) return;
-  if (!is_root && (!fusible_node(t) || r.nodes.size() >= kMaxNodes ||
+  if (!is_root && (!fusible_node(t) || forced.count(t) || r.nodes.size() >= kMaxNodes ||
                    r.leaves.size() >= kMaxLeaves)) {
     add_leaf(t, r);
     return;
   }
-  for (const auto& in : t->lazy_op()->inputs) grow(in.get(), r, false);
+  for (const auto& in : t->lazy_op()->inputs) {
+    r.owners[in.get()] = in.use_count();
+    grow(in.get(), r, false, forced);
+  }
   r.node_of[t] = static_cast<int>(r.nodes.size());
   r.nodes.push_back(t);
+}
+
+// Grow the region for `root`, then turn every interior node that something
+// outside the region still owns (a variable, a saved input, another pending
+// node) into a leaf, which realises it once as its own region; inlining it
+// would compute it again whenever that other owner is realised.  Repeats
+// until the region is closed.
+Region build_region(TensorImpl* root) {
+  std::unordered_set<TensorImpl*> forced;
+  for (;;) {
+    Region r;
+    grow(root, r, true, forced);
+    std::unordered_map<TensorImpl*, long> refs;
+    for (TensorImpl* n : r.nodes)
+      for (const auto& in : n->lazy_op()->inputs)
+        if (r.node_of.count(in.get())) ++refs[in.get()];
+    bool changed = false;
+    for (TensorImpl* n : r.nodes) {
+      if (n == root) continue;
+      if (r.owners.at(n) > refs[n]) changed |= forced.insert(n).second;
+    }
+    if (!changed) return r;
+  }
 }
 
 // ------------------------------------------------------------ layout
@@ -318,8 +346,7 @@ class HipFusionBackend : public lazy::LazyBackend {
       root->lazy_op()->run_eager(*root);
       return;
     }
-    Region r;
-    grow(root, r, true);
+    const Region r = build_region(root);
     const bool f64 = root->type() == DataType::Float64;
     const std::vector<size_t> shape = root->shape();
     const size_t n = shape_numel(shape);
@@ -383,8 +410,7 @@ const bool kRegistered = [] {
 // Source of the kernel a region would compile to; for tests and inspection.
 std::string fused_source_for(TensorImpl* root) {
   LMP_CHECK(root->is_deferred()) << "tensor has no pending graph";
-  Region r;
-  grow(root, r, true);
+  const Region r = build_region(root);
   const bool f64 = root->type() == DataType::Float64;
   return codegen(r, make_plan(r, root->shape(), f64), "lmp_fused", f64);
 }
