@@ -50,6 +50,8 @@ def parse():
     p.add_argument("--no-extra", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--only", nargs="+", choices=["c1", "c2", "c3", "f64", "mlp"],
+                   help="run only these extra sections (for per-config profiles)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also launch a known-size copy kernel (x + 0 over 64 Mi "
                         "floats: 256 MiB read, 256 MiB written) to calibrate "
@@ -110,90 +112,96 @@ def headline(rsl, abi, steps, warmup):
     return a, b, per_step_ms, launches
 
 
-def extras(rsl, abi, a, b, steps, warmup):
+def extras(rsl, abi, a, b, steps, warmup, only=None):
     out = {}
+    want = lambda tag: only is None or tag in only  # noqa: E731
+    L = abi.lib()
     dbl_max = sys.float_info.max
 
-    # --- config 1b: 6-op chain, fused, and the reference-style unfused path
-    def chain():
-        with rsl.capture_on():
-            c = rsl.exp(a) * b - rsl.clamp(a, 0, dbl_max) / (b + 1)
-        c.realize()
-    ms = time_steps(abi, chain, steps, warmup) / steps
-    out["c1b_chain6_fused"] = {"us": round(ms * 1e3, 2),
-                               "GB/s": round(BYTES_C1 / ms / 1e6, 1)}
+    if want("c1"):
+        # --- config 1b: 6-op chain, fused, and the reference-style unfused path
+        def chain():
+            with rsl.capture_on():
+                c = rsl.exp(a) * b - rsl.clamp(a, 0, dbl_max) / (b + 1)
+            c.realize()
+        ms = time_steps(abi, chain, steps, warmup) / steps
+        out["c1b_chain6_fused"] = {"us": round(ms * 1e3, 2),
+                                   "GB/s": round(BYTES_C1 / ms / 1e6, 1)}
 
-    def unfused():
-        (a * a + b).realize()
-    ms = time_steps(abi, unfused, steps // 4 + 1, 2) / (steps // 4 + 1)
-    out["c1a_eager_unfused_2_launches"] = {"us": round(ms * 1e3, 2),
-                                           "GB/s_algorithmic": round(BYTES_C1 / ms / 1e6, 1)}
-    del a, b
+        def unfused():
+            (a * a + b).realize()
+        ms = time_steps(abi, unfused, steps // 4 + 1, 2) / (steps // 4 + 1)
+        out["c1a_eager_unfused_2_launches"] = {"us": round(ms * 1e3, 2),
+                                               "GB/s_algorithmic": round(BYTES_C1 / ms / 1e6, 1)}
 
-    # --- config 2: dim reductions and the broadcast-add backward
-    A_np = np.random.default_rng(3).standard_normal((N16K, N16K), dtype=np.float32)
-    A = rsl.Variable(A_np, requires_grad=True)
-    del A_np
-    reps = max(5, steps // 10)
-    for name, fn in (("sum_dim0", lambda: rsl.sum(A, 0).realize()),
-                     ("sum_dim1", lambda: rsl.sum(A, 1).realize()),
-                     ("max_dim1", lambda: rsl.max(A, 1).realize())):
-        with rsl.no_grad():
-            ms = time_steps(abi, fn, reps, 2) / reps
-        out["c2_" + name] = {"us": round(ms * 1e3, 2), "GB/s": round(BYTES_C2 / ms / 1e6, 1)}
-    B = rsl.Variable(np.zeros((1, N16K), np.float32), requires_grad=True)
+    if want("c2"):
+        # --- config 2: dim reductions and the broadcast-add backward
+        A_np = np.random.default_rng(3).standard_normal((N16K, N16K), dtype=np.float32)
+        A = rsl.Variable(A_np, requires_grad=True)
+        del A_np
+        reps = max(5, steps // 10)
+        for name, fn in (("sum_dim0", lambda: rsl.sum(A, 0).realize()),
+                         ("sum_dim1", lambda: rsl.sum(A, 1).realize()),
+                         ("max_dim1", lambda: rsl.max(A, 1).realize())):
+            with rsl.no_grad():
+                ms = time_steps(abi, fn, reps, 2) / reps
+            out["c2_" + name] = {"us": round(ms * 1e3, 2), "GB/s": round(BYTES_C2 / ms / 1e6, 1)}
+        B = rsl.Variable(np.zeros((1, N16K), np.float32), requires_grad=True)
 
-    def bwd():
-        (A + B).backward()
-    ms = time_steps(abi, bwd, max(3, reps // 2), 1) / max(3, reps // 2)
-    out["c2_broadcast_add_backward"] = {
-        "ms": round(ms, 3),
-        "note": "whole backward: ones seed 1 GiB + A.grad += g 3 GiB + dim-0 sum 1 GiB"}
-    del A, B
+        def bwd():
+            (A + B).backward()
+        ms = time_steps(abi, bwd, max(3, reps // 2), 1) / max(3, reps // 2)
+        out["c2_broadcast_add_backward"] = {
+            "ms": round(ms, 3),
+            "note": "whole backward: ones seed 1 GiB + A.grad += g 3 GiB + dim-0 sum 1 GiB"}
+        del A, B
 
-    # --- config 3: fp32 GEMMs through the C ABI (the same kernels Linear uses)
-    gemm = {}
-    L = abi.lib()
-    for (m, n, k) in ((4096, 4096, 4096), (8192, 8192, 8192), (32, 4096, 8192)):
-        X, W, dY = abi.DeviceBuffer((m, k)), abi.DeviceBuffer((k, n)), abi.DeviceBuffer((m, n))
-        Y, dX, dW = abi.DeviceBuffer((m, n)), abi.DeviceBuffer((m, k)), abi.DeviceBuffer((k, n))
-        for buf, cnt in ((X, m * k), (W, k * n), (dY, m * n)):
-            abi.check(L.lmp_k_fill(abi.FLOAT32, buf.ptr, cnt, 0.01))
-        # Linear: Y = X W ; dX = dY W^T ; dW = X^T dY   (each 2*m*n*k flop)
-        cases = (("fwd", 0, 0, m, n, k, X, k, W, n, Y),
-                 ("dX", 0, 1, m, k, n, dY, n, W, n, dX),
-                 ("dW", 1, 0, k, n, m, X, k, dY, n, dW))
-        for label, ta, tb, mm, nn, kk, A_, lda, B_, ldb, C_ in cases:
-            r = 3 if m >= 8192 else 10
+    if want("c3"):
+        # --- config 3: fp32 GEMMs through the C ABI (the same kernels Linear uses)
+        gemm = {}
+        L = abi.lib()
+        for (m, n, k) in ((4096, 4096, 4096), (8192, 8192, 8192), (32, 4096, 8192)):
+            X, W, dY = abi.DeviceBuffer((m, k)), abi.DeviceBuffer((k, n)), abi.DeviceBuffer((m, n))
+            Y, dX, dW = abi.DeviceBuffer((m, n)), abi.DeviceBuffer((m, k)), abi.DeviceBuffer((k, n))
+            for buf, cnt in ((X, m * k), (W, k * n), (dY, m * n)):
+                abi.check(L.lmp_k_fill(abi.FLOAT32, buf.ptr, cnt, 0.01))
+            # Linear: Y = X W ; dX = dY W^T ; dW = X^T dY   (each 2*m*n*k flop)
+            cases = (("fwd", 0, 0, m, n, k, X, k, W, n, Y),
+                     ("dX", 0, 1, m, k, n, dY, n, W, n, dX),
+                     ("dW", 1, 0, k, n, m, X, k, dY, n, dW))
+            for label, ta, tb, mm, nn, kk, A_, lda, B_, ldb, C_ in cases:
+                r = 3 if m >= 8192 else 10
 
-            def run(ta=ta, tb=tb, mm=mm, nn=nn, kk=kk, A_=A_, lda=lda, B_=B_, ldb=ldb, C_=C_):
-                abi.check(L.lmp_k_gemm_f32(ta, tb, mm, nn, kk, A_.ptr, lda, B_.ptr, ldb,
-                                           C_.ptr, nn, 0))
-            ms = time_steps(abi, run, r, 2) / r
-            flop = 2.0 * mm * nn * kk
-            gemm[f"{m}x{n}x{k}_{label}"] = {
-                "us": round(ms * 1e3, 1), "TFLOP/s": round(flop / ms / 1e9, 1),
-                "frac_of_fp32_peak": round(flop / ms / 1e9 / FP32_MFMA_PEAK_TFLOPS, 3)}
-        del X, W, dY, Y, dX, dW
-    out["c3_gemm"] = gemm
+                def run(ta=ta, tb=tb, mm=mm, nn=nn, kk=kk, A_=A_, lda=lda, B_=B_, ldb=ldb, C_=C_):
+                    abi.check(L.lmp_k_gemm_f32(ta, tb, mm, nn, kk, A_.ptr, lda, B_.ptr, ldb,
+                                               C_.ptr, nn, 0))
+                ms = time_steps(abi, run, r, 2) / r
+                flop = 2.0 * mm * nn * kk
+                gemm[f"{m}x{n}x{k}_{label}"] = {
+                    "us": round(ms * 1e3, 1), "TFLOP/s": round(flop / ms / 1e9, 1),
+                    "frac_of_fp32_peak": round(flop / ms / 1e9 / FP32_MFMA_PEAK_TFLOPS, 3)}
+            del X, W, dY, Y, dX, dW
+        out["c3_gemm"] = gemm
 
-    # float64 GEMM (the reference's float64 suites run matmul on the device)
-    n = 4096
-    A64, B64, C64 = (abi.DeviceBuffer((n, n), np.float64) for _ in range(3))
-    for buf in (A64, B64):
-        abi.check(L.lmp_k_fill(abi.FLOAT64, buf.ptr, n * n, 0.01))
+    if want("f64"):
+        # float64 GEMM (the reference's float64 suites run matmul on the device)
+        n = 4096
+        A64, B64, C64 = (abi.DeviceBuffer((n, n), np.float64) for _ in range(3))
+        for buf in (A64, B64):
+            abi.check(L.lmp_k_fill(abi.FLOAT64, buf.ptr, n * n, 0.01))
 
-    def run64():
-        abi.check(L.lmp_k_gemm(abi.FLOAT64, 0, 0, n, n, n, A64.ptr, n, B64.ptr, n, C64.ptr, n, 0))
-    ms = time_steps(abi, run64, 5, 1) / 5
-    flop = 2.0 * n ** 3
-    out["gemm_f64_4096"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(flop / ms / 1e9, 1),
-                            "frac_of_fp64_peak": round(flop / ms / 1e9 / FP64_MFMA_PEAK_TFLOPS, 3)}
-    del A64, B64, C64
+        def run64():
+            abi.check(L.lmp_k_gemm(abi.FLOAT64, 0, 0, n, n, n, A64.ptr, n, B64.ptr, n, C64.ptr, n, 0))
+        ms = time_steps(abi, run64, 5, 1) / 5
+        flop = 2.0 * n ** 3
+        out["gemm_f64_4096"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(flop / ms / 1e9, 1),
+                                "frac_of_fp64_peak": round(flop / ms / 1e9 / FP64_MFMA_PEAK_TFLOPS, 3)}
+        del A64, B64, C64
 
-    # --- config 4 and config 0: MLP training loops
-    out["c4_wide_mlp"] = mlp_bench(rsl, abi, (4096, 4096, 4096, 1000), 512, 50, onehot=True)
-    out["c0_readme_mlp"] = mlp_bench(rsl, abi, (256, 64, 10), 32, 100, onehot=False)
+    if want("mlp"):
+        # --- config 4 and config 0: MLP training loops
+        out["c4_wide_mlp"] = mlp_bench(rsl, abi, (4096, 4096, 4096, 1000), 512, 50, onehot=True)
+        out["c0_readme_mlp"] = mlp_bench(rsl, abi, (256, 64, 10), 32, 100, onehot=False)
     return out
 
 
@@ -331,7 +339,7 @@ def main():
         line["copy_probe"] = {"kernel": "bin2d_f32 (x + 0)", "read_bytes": 4 * N8K * N8K,
                               "write_bytes": 4 * N8K * N8K, "launches": args.steps}
     if not args.no_extra:
-        line["extra"] = extras(rsl, abi, a, b, args.steps, args.warmup)
+        line["extra"] = extras(rsl, abi, a, b, args.steps, args.warmup, args.only)
     del a, b
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
