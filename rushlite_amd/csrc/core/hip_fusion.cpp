@@ -58,11 +58,20 @@ bool fusible_node(const TensorImpl* t) {
   return true;
 }
 
+// Leaves are only recorded while a region grows; they are realised once the
+// region is closed (realise_leaves).  Realising during growth could realise a
+// node already placed in the region and free the nodes beneath it.
 void add_leaf(TensorImpl* t, Region& r) {
   if (r.leaf_of.count(t)) return;
-  t->data();  // realise (may run the leaf's own fused region)
   r.leaf_of[t] = static_cast<int>(r.leaves.size());
   r.leaves.push_back(t);
+}
+
+// Realise the inputs of a closed region (each may run its own region).  A
+// closed region's interior nodes have no owner outside it, so no leaf's graph
+// can reach them.
+void realise_leaves(const Region& r) {
+  for (TensorImpl* leaf : r.leaves) leaf->data();
 }
 
 void grow(TensorImpl* t, Region& r, bool is_root,
@@ -81,11 +90,95 @@ void grow(TensorImpl* t, Region& r, bool is_root,
   r.nodes.push_back(t);
 }
 
+bool is_reduce(const TensorImpl* t) {
+  return t->is_deferred() && t->lazy_op()->kind() == lazy::OpKind::Reduce;
+}
+
+// ------------------------------------------------------------ row regions
+//
+// A region holding reduce nodes runs as a row kernel: one wave per row of the
+// reduced shape S = [..., N], each lane holding its share of the row in
+// registers.  Every node is either full (shape S) or a row value (shape S
+// with last dim 1); a reduce node turns a full value into a row value with
+// exactly the order of the eager wave-per-row kernel (row_reduce_wave_f32 for
+// float32 rows with N % 4 == 0, row_reduce_wave otherwise: four interleaved
+// accumulators, their pairwise combination, then a wave butterfly), so a
+// fused softmax equals the eager one bit for bit.  Rows of 2048 or more, which
+// the eager path reduces with a workgroup per row, are not fused.
+constexpr int64_t kRowMax = 2048;
+
+struct RowPlan {
+  bool ok = false;
+  std::vector<size_t> S;
+  int64_t R = 0, N = 0;
+  bool vec_order = false;  // float32 and N % 4 == 0: elements come in float4s
+  bool vec_load = false;   // every full leaf can be read with aligned float4s
+  std::vector<bool> full;               // per leaf: varies along the row
+  std::vector<int64_t> row_stride;      // per leaf, in elements
+};
+
+RowPlan row_plan(const Region& r) {
+  RowPlan p;
+  const TensorImpl* first = nullptr;
+  for (TensorImpl* n : r.nodes)
+    if (is_reduce(n)) {
+      first = n;
+      break;
+    }
+  if (!first) return p;
+  p.S = first->lazy_op()->inputs[0]->shape();
+  const size_t nd = p.S.size();
+  if (nd == 0) return p;
+  p.N = static_cast<int64_t>(p.S.back());
+  if (p.N < 2 || p.N >= kRowMax) return p;
+  p.R = static_cast<int64_t>(shape_numel(p.S)) / p.N;
+  if (p.R > (int64_t(1) << 31)) return p;  // one wave per row, one-shot grid
+  std::vector<size_t> S1 = p.S;
+  S1.back() = 1;
+  for (TensorImpl* n : r.nodes) {
+    if (n->shape() != p.S && n->shape() != S1) return p;
+    if (is_reduce(n)) {
+      const auto& fn = n->lazy_op();
+      if (fn->inputs[0]->shape() != p.S || n->shape() != S1 ||
+          static_cast<size_t>(fn->param0()) != nd - 1)
+        return p;
+    }
+  }
+  const bool f32 = r.nodes.back()->type() == DataType::Float32;
+  p.vec_order = f32 && p.N % 4 == 0;
+  p.vec_load = p.vec_order;
+  for (TensorImpl* leaf : r.leaves) {
+    const std::vector<stride_t> st = padded_strides(leaf->shape(), nd);
+    const int64_t last = st[nd - 1];
+    if (last != 0 && last != 1) return p;
+    // The leading dims must address rows linearly: offset = row * stride.
+    int64_t rs = 0, span = 1;
+    bool found = false;
+    for (size_t i = nd - 1; i-- > 0;) {
+      if (p.S[i] == 1) continue;
+      if (!found) {
+        rs = st[i];
+        found = true;
+      } else if (st[i] != rs * span) {
+        return p;
+      }
+      span *= static_cast<int64_t>(p.S[i]);
+    }
+    p.full.push_back(last == 1);
+    p.row_stride.push_back(rs);
+    if (last == 1 && (rs % 4 != 0 || (reinterpret_cast<uintptr_t>(leaf->raw()) & 15u) != 0))
+      p.vec_load = false;
+  }
+  p.ok = true;
+  return p;
+}
+
 // Grow the region for `root`, then turn every interior node that something
 // outside the region still owns (a variable, a saved input, another pending
 // node) into a leaf, which realises it once as its own region; inlining it
-// would compute it again whenever that other owner is realised.  Repeats
-// until the region is closed.
+// would compute it again whenever that other owner is realised.  Interior
+// reduce nodes that cannot share a row kernel with the rest are made leaves
+// too.  Repeats until the region is closed.
 Region build_region(TensorImpl* root) {
   std::unordered_set<TensorImpl*> forced;
   for (;;) {
@@ -99,6 +192,13 @@ Region build_region(TensorImpl* root) {
     for (TensorImpl* n : r.nodes) {
       if (n == root) continue;
       if (r.owners.at(n) > refs[n]) changed |= forced.insert(n).second;
+    }
+    if (!changed) {
+      bool has_reduce = false;
+      for (TensorImpl* n : r.nodes) has_reduce |= is_reduce(n);
+      if (has_reduce && !row_plan(r).ok)
+        for (TensorImpl* n : r.nodes)
+          if (n != root && is_reduce(n)) changed |= forced.insert(n).second;
     }
     if (!changed) return r;
   }
@@ -196,10 +296,12 @@ int64_t bound_bits(Scalar v, bool f64) {
 }
 
 std::vector<int64_t> signature(const Region& r, const std::vector<size_t>& shape,
-                               const Plan& p, bool f64) {
+                               const Plan& p, bool f64, const RowPlan& rp) {
   std::vector<int64_t> s;
   s.push_back(0x4c4d5046);  // tag
   s.push_back(f64 ? 8 : 4);
+  s.push_back(rp.ok ? (rp.vec_load ? 3 : 2) : 0);
+  for (size_t d : rp.S) s.push_back(static_cast<int64_t>(d));
   s.push_back(static_cast<int64_t>(shape.size()));
   for (size_t d : shape) s.push_back(static_cast<int64_t>(d));
   s.push_back(static_cast<int64_t>(r.leaves.size()));
@@ -216,6 +318,7 @@ std::vector<int64_t> signature(const Region& r, const std::vector<size_t>& shape
       s.push_back(bound_bits(fn->param0(), f64));
       s.push_back(bound_bits(fn->param1(), f64));
     }
+    if (fn->kind() == lazy::OpKind::Reduce) s.push_back(static_cast<int64_t>(fn->param0()));
     for (const auto& in : fn->inputs) {
       auto it = r.leaf_of.find(in.get());
       s.push_back(it != r.leaf_of.end() ? it->second : -1 - r.node_of.at(in.get()));
@@ -330,6 +433,158 @@ std::string codegen(const Region& r, const Plan& p, const std::string& name, boo
   return os.str();
 }
 
+// Row kernel for a region with reduce nodes (see RowPlan).
+std::string codegen_rows(const Region& r, const RowPlan& rp, const std::string& name,
+                         bool f64) {
+  const char* T = f64 ? "double" : "float";
+  const bool vo = rp.vec_order;
+  const int64_t NN = vo ? rp.N / 4 : rp.N;      // units a lane steps over
+  const int64_t TT = (NN + 63) / 64;            // units per lane
+  const int64_t E = vo ? TT * 4 : TT;           // elements per lane
+  const auto elem_col = [&](int64_t e) {        // column of element e, as code
+    std::ostringstream c;
+    if (vo) c << "4u * (lane + " << 64 * (e / 4) << "u) + " << e % 4 << "u";
+    else c << "lane + " << 64 * e << "u";
+    return c.str();
+  };
+  const auto ok_of = [&](int64_t e) { return "ok" + std::to_string(vo ? e / 4 : e); };
+  std::vector<bool> node_full(r.nodes.size());
+  for (size_t m = 0; m < r.nodes.size(); ++m)
+    node_full[m] = !is_reduce(r.nodes[m]) && r.nodes[m]->shape() == rp.S;
+
+  std::ostringstream os;
+  os << kPrelude;
+  os << "extern \"C\" __global__ __launch_bounds__(" << kBlock << ") void " << name << "("
+     << T << "* __restrict__ out";
+  for (size_t l = 0; l < r.leaves.size(); ++l) os << ", const " << T << "* __restrict__ in" << l;
+  os << ") {\n";
+  os << "  const unsigned lane = threadIdx.x & 63u;\n";
+  os << "  const unsigned long row = (unsigned long)blockIdx.x * " << kBlock / 64
+     << "ul + (threadIdx.x >> 6);\n";
+  os << "  if (row >= " << rp.R << "ul) return;\n";
+  for (int64_t t = 0; t < TT; ++t)
+    os << "  const bool ok" << t << " = lane + " << 64 * t << "u < " << NN << "u;\n";
+  // Leaves.
+  for (size_t l = 0; l < r.leaves.size(); ++l) {
+    const std::string base = "in" + std::to_string(l) + " + row * " +
+                             std::to_string(rp.row_stride[l]) + "ul";
+    if (!rp.full[l]) {
+      os << "  const " << T << " l" << l << " = *(" << base << ");\n";
+      continue;
+    }
+    if (rp.vec_load) {
+      for (int64_t t = 0; t < TT; ++t) {
+        os << "  const lmp_v4 q" << l << "_" << t << " = ok" << t
+           << " ? *reinterpret_cast<const lmp_v4*>(" << base << " + 4u * (lane + " << 64 * t
+           << "u)) : lmp_v4{0.0f, 0.0f, 0.0f, 0.0f};\n";
+        const char* comp[4] = {"x", "y", "z", "w"};
+        for (int c = 0; c < 4; ++c)
+          os << "  const " << T << " l" << l << "_" << 4 * t + c << " = q" << l << "_" << t
+             << "." << comp[c] << ";\n";
+      }
+    } else {
+      for (int64_t e = 0; e < E; ++e)
+        os << "  const " << T << " l" << l << "_" << e << " = " << ok_of(e) << " ? (" << base
+           << ")[" << elem_col(e) << "] : " << T << "(0);\n";
+    }
+  }
+  const auto arg = [&](const std::shared_ptr<TensorImpl>& in, int64_t e) {
+    auto lt = r.leaf_of.find(in.get());
+    if (lt != r.leaf_of.end())
+      return "l" + std::to_string(lt->second) +
+             (rp.full[lt->second] && e >= 0 ? "_" + std::to_string(e) : "");
+    const int k = r.node_of.at(in.get());
+    return "v" + std::to_string(k) + (node_full[k] && e >= 0 ? "_" + std::to_string(e) : "");
+  };
+  for (size_t m = 0; m < r.nodes.size(); ++m) {
+    const auto& fn = r.nodes[m]->lazy_op();
+    if (!is_reduce(r.nodes[m])) {
+      const int64_t count = node_full[m] ? E : 1;
+      for (int64_t e = 0; e < count; ++e) {
+        std::vector<std::string> args;
+        for (const auto& in : fn->inputs) args.push_back(arg(in, node_full[m] ? e : -1));
+        os << "  const " << T << " v" << m << (node_full[m] ? "_" + std::to_string(e) : "")
+           << " = " << substitute(fn->codegen_expr(), args) << ";\n";
+      }
+      continue;
+    }
+    // Reduction in the eager kernels' order.
+    const int op = fn->code();
+    std::string id;
+    if (op == LMP_RED_SUM) id = f64 ? "0.0" : "0.0f";
+    else if (op == LMP_RED_PROD) id = f64 ? "1.0" : "1.0f";
+    else if (op == LMP_RED_MAX) id = f64 ? "__longlong_as_double(0xffefffffffffffffll)"
+                                         : "__uint_as_float(0xff7fffffu)";
+    else id = f64 ? "__longlong_as_double(0x7fefffffffffffffll)" : "__uint_as_float(0x7f7fffffu)";
+    const auto comb = [&](const std::string& acc, const std::string& x) {
+      switch (op) {
+        case LMP_RED_SUM: return "(" + acc + " + " + x + ")";
+        case LMP_RED_PROD: return "(" + acc + " * " + x + ")";
+        case LMP_RED_MAX: return "(" + acc + " < " + x + " ? " + x + " : " + acc + ")";
+        default: return "(" + x + " < " + acc + " ? " + x + " : " + acc + ")";
+      }
+    };
+    const std::string P = "r" + std::to_string(m) + "_";
+    const int W = vo ? 4 : 1;  // components per accumulator
+    const auto acc = [&](int i, int c) { return P + "a" + std::to_string(i) + "_" + std::to_string(c); };
+    const auto src = [&](int64_t t, int c) { return arg(fn->inputs[0], vo ? 4 * t + c : t); };
+    os << "  " << T << " v" << m << ";\n  {\n";
+    for (int i = 0; i < 4; ++i)
+      for (int c = 0; c < W; ++c) os << "    " << T << " " << acc(i, c) << " = " << id << ";\n";
+    os << "    unsigned " << P << "gd = 0u;\n";
+    for (int64_t g = 0; 4 * g + 3 < TT; ++g) {
+      os << "    if (lane + " << 64 * (4 * g + 3) << "u < " << NN << "u) {\n";
+      for (int i = 0; i < 4; ++i)
+        for (int c = 0; c < W; ++c)
+          os << "      " << acc(i, c) << " = " << comb(acc(i, c), src(4 * g + i, c)) << ";\n";
+      os << "      " << P << "gd = " << g + 1 << "u;\n    }\n";
+    }
+    for (int64_t t = 0; t < TT; ++t) {
+      os << "    if (" << t << "u >= 4u * " << P << "gd && ok" << t << ") {\n";
+      for (int c = 0; c < W; ++c)
+        os << "      " << acc(0, c) << " = " << comb(acc(0, c), src(t, c)) << ";\n";
+      os << "    }\n";
+    }
+    std::vector<std::string> b;
+    for (int c = 0; c < W; ++c)
+      b.push_back(comb(comb(acc(0, c), acc(1, c)), comb(acc(2, c), acc(3, c))));
+    os << "    " << T << " " << P << "v = ";
+    if (vo) {
+      os << T << "(0);\n";
+      for (int c = 0; c < 4; ++c)
+        os << "    const " << T << " " << P << "b" << c << " = " << b[c] << ";\n";
+      os << "    " << P << "v = " << comb(comb(P + "b0", P + "b1"), comb(P + "b2", P + "b3"))
+         << ";\n";
+    } else {
+      os << b[0] << ";\n";
+    }
+    for (int off = 32; off >= 1; off >>= 1)
+      os << "    { const " << T << " o = __shfl_xor(" << P << "v, " << off << ", 64); " << P
+         << "v = " << comb(P + "v", "o") << "; }\n";
+    os << "    v" << m << " = " << P << "v;\n  }\n";
+  }
+  os << "  // stores\n";
+  const size_t root = r.nodes.size() - 1;
+  if (node_full[root]) {
+    const std::string obase = "out + row * " + std::to_string(rp.N) + "ul";
+    if (vo) {
+      for (int64_t t = 0; t < TT; ++t)
+        os << "  if (ok" << t << ") *reinterpret_cast<lmp_v4*>(" << obase << " + 4u * (lane + "
+           << 64 * t << "u)) = lmp_v4{v" << root << "_" << 4 * t << ", v" << root << "_"
+           << 4 * t + 1 << ", v" << root << "_" << 4 * t + 2 << ", v" << root << "_"
+           << 4 * t + 3 << "};\n";
+    } else {
+      for (int64_t e = 0; e < E; ++e)
+        os << "  if (ok" << e << ") (" << obase << ")[" << elem_col(e) << "] = v" << root << "_"
+           << e << ";\n";
+    }
+  } else {
+    os << "  if (lane == 0u) out[row] = v" << root << ";\n";
+  }
+  os << "}\n";
+  return os.str();
+}
+
 // --------------------------------------------------------------- backend
 
 struct Compiled {
@@ -347,7 +602,15 @@ class HipFusionBackend : public lazy::LazyBackend {
       return;
     }
     const Region r = build_region(root);
+    realise_leaves(r);
     const bool f64 = root->type() == DataType::Float64;
+    const RowPlan rp = row_plan(r);
+    if (is_reduce(root) && !rp.ok) {
+      // A reduction no row kernel can take (long rows, other layouts): eager.
+      for (const auto& in : root->lazy_op()->inputs) in->data();
+      root->lazy_op()->run_eager(*root);
+      return;
+    }
     const std::vector<size_t> shape = root->shape();
     const size_t n = shape_numel(shape);
     Storage out(n * dtype_size(root->type()), DeviceType::HIP);
@@ -356,12 +619,12 @@ class HipFusionBackend : public lazy::LazyBackend {
       return;
     }
     const Plan p = make_plan(r, shape, f64);
-    std::vector<int64_t> sig = signature(r, shape, p, f64);
+    std::vector<int64_t> sig = signature(r, shape, p, f64, rp);
     const uint64_t key = fnv1a(sig);
     void* handle = lookup(key, sig);
     if (!handle) {
       const std::string name = "lmp_fused";
-      const std::string src = codegen(r, p, name, f64);
+      const std::string src = rp.ok ? codegen_rows(r, rp, name, f64) : codegen(r, p, name, f64);
       hip_ok(lmp_jit_compile(key, src.c_str(), name.c_str(), &handle), "lmp_jit_compile");
       std::lock_guard<std::mutex> lock(mu_);
       cache_[key] = Compiled{handle, std::move(sig)};
@@ -371,7 +634,7 @@ class HipFusionBackend : public lazy::LazyBackend {
     }
     // Launch: one lane per float4 (vec, one-shot) or per element (grid-stride
     // loop, one-shot up to 2^30 workgroups).
-    const uint64_t work = p.vec ? p.nvec : p.n;
+    const uint64_t work = rp.ok ? uint64_t(rp.R) * 64 : p.vec ? p.nvec : p.n;
     uint64_t grid = (work + kBlock - 1) / kBlock;
     grid = std::max<uint64_t>(1, std::min<uint64_t>(grid, uint64_t(1) << 30));
     std::vector<void*> ptrs;
@@ -411,7 +674,10 @@ const bool kRegistered = [] {
 std::string fused_source_for(TensorImpl* root) {
   LMP_CHECK(root->is_deferred()) << "tensor has no pending graph";
   const Region r = build_region(root);
+  realise_leaves(r);
   const bool f64 = root->type() == DataType::Float64;
+  const RowPlan rp = row_plan(r);
+  if (rp.ok) return codegen_rows(r, rp, "lmp_fused", f64);
   return codegen(r, make_plan(r, root->shape(), f64), "lmp_fused", f64);
 }
 

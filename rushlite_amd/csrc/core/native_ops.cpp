@@ -108,11 +108,28 @@ Tensor clamp_backward(const Tensor& input, const Tensor& grad, Scalar lo, Scalar
                                     *Acc::getImpl(grad), lo, hi));
 }
 
-#define LMP_DEF_REDUCT(name)                                               \
-  Tensor name(const Tensor& a, size_t axis) {                              \
-    return wrap(name##_stub()(a.device(), *Acc::getImpl(a), axis));        \
+namespace {
+// Under capture, a float32/float64 reduction over the last axis is recorded
+// so the fusion backend can build it into a row kernel.
+bool capture_reduction(const Tensor& a, size_t axis) {
+  if (!lazy::should_capture(a.device())) return false;
+  const DataType t = a.type();
+  return (t == DataType::Float32 || t == DataType::Float64) && a.shape().size() >= 1 &&
+         axis + 1 == a.shape().size() && a.numel() > 0;
+}
+}  // namespace
+
+#define LMP_DEF_REDUCT(name, CODE)                                              \
+  Tensor name(const Tensor& a, size_t axis) {                                   \
+    const auto& ai = Acc::getImpl(a);                                           \
+    if (capture_reduction(a, axis))                                             \
+      return Acc::fromImpl(lazy::record(lazy::make_reduce(CODE, ai, axis)));    \
+    return wrap(name##_stub()(a.device(), *ai, axis));                          \
   }
-LMP_FOR_REDUCT_OPS(LMP_DEF_REDUCT)
+LMP_DEF_REDUCT(sum, LMP_RED_SUM)
+LMP_DEF_REDUCT(max, LMP_RED_MAX)
+LMP_DEF_REDUCT(min, LMP_RED_MIN)
+LMP_DEF_REDUCT(prod, LMP_RED_PROD)
 #undef LMP_DEF_REDUCT
 
 Tensor matmul(const Tensor& a, const Tensor& b) {
@@ -324,6 +341,38 @@ struct UnaryFn : LazyFunction {
   }
 };
 
+// Keep-dims reduction over the last axis (see OpKind::Reduce).  The fusion
+// backend emits its code itself, replaying the eager row kernel's order.
+struct ReduceFn : LazyFunction {
+  int op;
+  size_t axis;
+  ReduceFn(int code, std::vector<std::shared_ptr<TensorImpl>> ins, size_t ax)
+      : LazyFunction(std::move(ins)), op(code), axis(ax) {}
+  std::shared_ptr<TensorImpl> infer_output() const override {
+    OpMeta m = infer_reduct(*inputs[0], axis);
+    return std::make_shared<TensorImpl>(Storage(0, inputs[0]->device()), m.shape,
+                                        m.dtype);
+  }
+  bool is_fusible() const override { return true; }
+  OpKind kind() const override { return OpKind::Reduce; }
+  int code() const override { return op; }
+  Scalar param0() const override { return static_cast<Scalar>(axis); }
+  void run_eager(TensorImpl& out) override {
+    using namespace ops;
+    const DeviceType d = inputs[0]->device();
+    TensorImpl r = [&]() -> TensorImpl {
+      switch (op) {
+        case LMP_RED_SUM: return sum_stub()(d, *inputs[0], axis);
+        case LMP_RED_MAX: return max_stub()(d, *inputs[0], axis);
+        case LMP_RED_MIN: return min_stub()(d, *inputs[0], axis);
+        default: return prod_stub()(d, *inputs[0], axis);
+      }
+    }();
+    out.set_realized(r.storage());
+  }
+  std::string codegen_expr() const override { return ""; }
+};
+
 }  // namespace
 
 bool is_capture_enabled() { return t_capture; }
@@ -363,6 +412,13 @@ std::shared_ptr<LazyFunction> make_unary(int code, std::shared_ptr<TensorImpl> a
                                          Scalar p0, Scalar p1) {
   return std::make_shared<UnaryFn>(code, std::vector<std::shared_ptr<TensorImpl>>{std::move(a)},
                                    p0, p1);
+}
+
+std::shared_ptr<LazyFunction> make_reduce(int code, std::shared_ptr<TensorImpl> a,
+                                          size_t axis) {
+  infer_reduct(*a, axis);  // shape and axis checks, as the eager path does
+  return std::make_shared<ReduceFn>(code, std::vector<std::shared_ptr<TensorImpl>>{std::move(a)},
+                                    axis);
 }
 
 }  // namespace lazy

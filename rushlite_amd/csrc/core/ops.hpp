@@ -2,9 +2,11 @@
 //
 // Each elementwise frontend checks the capture mode, then either records a
 // LazyFunction node (deferred tensor) or calls its device stub
-// (native/expand_ops.cpp:28-39, native/unary_ops.cpp:23-33).  Reductions,
-// matmul, transpose, views and memory ops are never captured; reading their
-// inputs realises any pending graph (tensor_impl.cpp:33-36).
+// (native/expand_ops.cpp:28-39, native/unary_ops.cpp:23-33).  Floating-point
+// reductions over the last axis are captured too (the reference never
+// captures reductions), so a softmax row becomes one kernel.  Other
+// reductions, matmul, transpose, views and memory ops are never captured;
+// reading their inputs realises any pending graph (tensor_impl.cpp:33-36).
 #pragma once
 
 #include <memory>
@@ -146,9 +148,11 @@ class CaptureGuard {
   bool prev_;
 };
 
-// Elementwise op codes shared by the lazy nodes, the structural graph hash
-// and the code generator; values equal lmp_binary_op / lmp_unary_op.
-enum class OpKind : uint8_t { Binary, Unary };
+// Op kinds shared by the lazy nodes, the structural graph hash and the code
+// generator; codes equal lmp_binary_op / lmp_unary_op / lmp_reduce_op.
+// Reduce nodes are keep-dims reductions over the last axis, recorded under
+// capture so a region can end in (or pass through) a row reduction.
+enum class OpKind : uint8_t { Binary, Unary, Reduce };
 
 // A deferred elementwise node (lazy_function.hpp:11-22).  codegen_expr()
 // returns the node's expression with {0}/{1} for its operands, in the HIP
@@ -183,6 +187,9 @@ std::shared_ptr<LazyFunction> make_binary(int code,
                                           std::shared_ptr<TensorImpl> b);
 std::shared_ptr<LazyFunction> make_unary(int code, std::shared_ptr<TensorImpl> a,
                                          Scalar p0 = 0, Scalar p1 = 0);
+// param0() of a reduce node is its axis.
+std::shared_ptr<LazyFunction> make_reduce(int code, std::shared_ptr<TensorImpl> a,
+                                          size_t axis);
 
 }  // namespace lazy
 

@@ -511,3 +511,69 @@ def test_jit_disk_cache_reused_by_a_new_process(tmp_path):
     third = _jit_child(tmp_path)
     assert third["compiled"] == first["compiled"] and third["disk"] == 0
     assert third["bits"] == first["bits"]
+
+
+# ------------------------------------------------- row (reduction) fusion
+
+def _softmax(rsl, x):
+    m = rsl.max(x, 1)
+    e = rsl.exp(x - m)
+    return e / rsl.sum(e, 1)
+
+
+@pytest.mark.parametrize("shape,dt", [((512, 1000), "float32"), ((32, 10), "float32"),
+                                      ((7, 333), "float32"), ((64, 100), "float64"),
+                                      ((3, 2048), "float32")], ids=str)
+def test_softmax_row_fusion_matches_eager(rsl, shape, dt):
+    """Under capture a softmax row (max, sub, exp, sum, div) is one kernel
+    whose reductions replay the eager kernels' order: bit-identical to the
+    eager softmax.  Rows of 2048 or more are reduced by the eager kernels."""
+    rng = np.random.default_rng(shape[1])
+    x_np = (rng.standard_normal(shape) * 4).astype(dt)
+    x = rsl.Variable(x_np, dtype=getattr(rsl.dtype, dt))
+    eager = _softmax(rsl, x).numpy()
+    s0 = rsl._stats()
+    with rsl.no_grad(), rsl.capture_on():
+        p = _softmax(rsl, x)
+    got = p.numpy()
+    s1 = rsl._stats()
+    if shape[1] < 2048:
+        assert s1["fused_launches"] - s0["fused_launches"] == 1
+        assert s1["eager_launches"] == s0["eager_launches"]
+    assert got.dtype == eager.dtype
+    assert np.array_equal(got.view(np.uint8), eager.view(np.uint8))
+    x64 = x_np.astype(np.float64)
+    e64 = np.exp(x64 - x64.max(1, keepdims=True))
+    assert rel_err(got, e64 / e64.sum(1, keepdims=True)) <= (1e-6 if dt == "float32" else 1e-14)
+
+
+@pytest.mark.parametrize("op", ["sum", "max", "min", "prod"])
+@pytest.mark.parametrize("shape", [(300, 257), (512, 1000), (5, 3, 12), (9, 4)], ids=str)
+def test_captured_reductions_equal_eager(rsl, op, shape):
+    """A reduction over the last axis of a captured elementwise chain (with a
+    row-broadcast [N] operand) fuses into one row kernel equal to eager."""
+    rng = np.random.default_rng(len(shape) * 100 + shape[-1])
+    a_np = rng.standard_normal(shape, dtype=np.float32)
+    w_np = (1.0 + 0.01 * rng.standard_normal(shape[-1:])).astype(np.float32)
+    a, w = V(rsl, a_np), V(rsl, w_np)
+    fn = getattr(rsl, op)
+    eager = fn(a * w + 0.5, len(shape) - 1).numpy()
+    s0 = rsl._stats()
+    with rsl.no_grad(), rsl.capture_on():
+        r = fn(a * w + 0.5, len(shape) - 1)
+    got = r.numpy()
+    assert rsl._stats()["fused_launches"] - s0["fused_launches"] == 1
+    assert np.array_equal(got.view(np.uint32), eager.view(np.uint32))
+
+
+def test_loss_row_chain_fuses(rsl):
+    """The README loss's row part, sum(-y * log(p + 1e-3), 1), is one kernel."""
+    rng = np.random.default_rng(8)
+    p, y = V(rsl, rng.random((32, 10), dtype=np.float32)), V(rsl, rng.random((32, 10), dtype=np.float32))
+    eager = rsl.sum(-y * rsl.log(p + 1e-3), 1).numpy()
+    s0 = rsl._stats()
+    with rsl.no_grad(), rsl.capture_on():
+        r = rsl.sum(-y * rsl.log(p + 1e-3), 1)
+    got = r.numpy()
+    assert rsl._stats()["fused_launches"] - s0["fused_launches"] == 1
+    assert np.array_equal(got.view(np.uint32), eager.view(np.uint32))
