@@ -318,37 +318,48 @@ struct DirectArgs {
 
 constexpr int kDirectN = 128;
 
+// Read by lanes whose operand element lies outside the matrix: zeros, never
+// written.
+__device__ __attribute__((aligned(16))) float g_direct_zeros[4];
+
 template <bool TA, bool TB>
 struct DirectFrag {
   v4f a;     // A values of steps 0..3
   v4f b[4];  // TB: b[q][s]; !TB: b[s][q]
 
+  // Loads are unconditional: a lane whose element lies outside the matrix (or
+  // past ke) reads zeros from g_direct_zeros instead.  Guarded loads would
+  // each sit behind a branch, and a select after the load would wait for it
+  // at once; either way nothing would stay in flight while the MFMAs run.
   __device__ __forceinline__ void load(const DirectArgs& g, int row, int n0, int k0,
                                        int ke, int li, int lh) {
     const int kq = k0 + 4 * lh;  // first k of this lane's half
     if constexpr (!TA) {
-      a = (row < g.m && kq < ke)
-              ? *reinterpret_cast<const v4f*>(g.a + int64_t(row) * g.lda + kq)
-              : v4f(0.0f);
+      const bool ok = row < g.m && kq < ke;
+      a = *reinterpret_cast<const v4f*>(ok ? g.a + int64_t(row) * g.lda + kq
+                                           : g_direct_zeros);
     } else {
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        a[s] = (row < g.m && kq + s < ke) ? g.a[int64_t(kq + s) * g.lda + row] : 0.0f;
+      for (int s = 0; s < 4; ++s) {
+        const bool ok = row < g.m && kq + s < ke;
+        a[s] = *(ok ? g.a + int64_t(kq + s) * g.lda + row : g_direct_zeros);
+      }
     }
     if constexpr (!TB) {
       const int col = n0 + 4 * li;
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        b[s] = (col < g.n && kq + s < ke)
-                   ? *reinterpret_cast<const v4f*>(g.b + int64_t(kq + s) * g.ldb + col)
-                   : v4f(0.0f);
+      for (int s = 0; s < 4; ++s) {
+        const bool ok = col < g.n && kq + s < ke;
+        b[s] = *reinterpret_cast<const v4f*>(ok ? g.b + int64_t(kq + s) * g.ldb + col
+                                                : g_direct_zeros);
+      }
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int col = n0 + 32 * q + li;
-        b[q] = (col < g.n && kq < ke)
-                   ? *reinterpret_cast<const v4f*>(g.b + int64_t(col) * g.ldb + kq)
-                   : v4f(0.0f);
+        const bool ok = col < g.n && kq < ke;
+        b[q] = *reinterpret_cast<const v4f*>(ok ? g.b + int64_t(col) * g.ldb + kq
+                                                : g_direct_zeros);
       }
     }
   }
@@ -370,11 +381,15 @@ __device__ __forceinline__ int direct_row(int r, int lh) {
 
 constexpr int kDirectWaves = 4;
 
-template <bool TA, bool TB>
-__global__ __launch_bounds__(64 * kDirectWaves) __attribute__((amdgpu_waves_per_eu(TB ? 3 : 4)))
+template <bool TA, bool TB, int STAGES>
+__global__ __launch_bounds__(64 * kDirectWaves)
+__attribute__((amdgpu_waves_per_eu(STAGES > 2 ? 2 : TB ? 3 : 4)))
 void gemm_direct(DirectArgs g) {
   constexpr int KW = kDirectWaves;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The wave index (and with it the K range) is uniform across the wave;
+  // saying so keeps the K loop a scalar loop.
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int li = lane & 31, lh = lane >> 5;
   const int n0 = int(blockIdx.x % g.n_blocks) * kDirectN;
   const int part = g.k_per_wg / KW;
@@ -385,16 +400,23 @@ void gemm_direct(DirectArgs g) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) acc[q] = v16f(0.0f);
 
-  // Two fragments in flight: the next iteration's loads are issued before
-  // the current iteration's MFMAs.  Loads at or past ke yield zeros, so the
+  // STAGES fragments in flight: each iteration's loads are issued STAGES - 1
+  // iterations ahead of its MFMAs.  Loads at or past ke yield zeros, so the
   // tail needs no branch (0 * 0 adds nothing).
-  DirectFrag<TA, TB> f0, f1;
-  f0.load(g, li, n0, kb, ke, li, lh);
-  for (int k0 = kb; k0 < ke; k0 += 16) {
-    f1.load(g, li, n0, k0 + 8, ke, li, lh);
-    f0.mma(acc);
-    f0.load(g, li, n0, k0 + 16, ke, li, lh);
-    f1.mma(acc);
+  DirectFrag<TA, TB> f[STAGES];
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s) f[s].load(g, li, n0, kb + 8 * s, ke, li, lh);
+  for (int k0 = kb; k0 < ke; k0 += 8 * STAGES) {
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) {
+      f[s].mma(acc);
+      // Keep each refill right after the MFMAs that free its registers; the
+      // scheduler would otherwise sink every load to the end of the trip,
+      // leaving nothing in flight while the MFMAs run.
+      __builtin_amdgcn_sched_barrier(0);
+      f[s].load(g, li, n0, k0 + 8 * (s + STAGES), ke, li, lh);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
   const bool partial = gridDim.y > 1;
@@ -505,7 +527,7 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
 // M <= 32 on the register-direct kernel.  Each workgroup takes at least 64
 // values of k per wave; the split count aims at one workgroup per CU (more
 // only adds partial traffic: measured on MI355X); `splits` > 0 overrides it.
-template <bool TA, bool TB>
+template <bool TA, bool TB, int STAGES = 2>
 int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
   DirectArgs d{};
   d.a = g0.a;
@@ -533,7 +555,8 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
     d.c = part;
   }
   const dim3 grid{uint32_t(d.n_blocks), uint32_t(splits), 1u};
-  hipLaunchKernelGGL((gemm_direct<TA, TB>), grid, dim3(64 * kDirectWaves), 0, rt->stream, d);
+  hipLaunchKernelGGL((gemm_direct<TA, TB, STAGES>), grid, dim3(64 * kDirectWaves), 0, rt->stream,
+                     d);
   LMP_LAUNCH_CHECK("gemm_direct");
   if (splits > 1) {
     const int64_t mn = int64_t(g0.m) * g0.n;
