@@ -1,0 +1,259 @@
+"""Random float64 graphs on the device against torch float64 autograd.
+
+The reference checks its device backend with float64 differential suites:
+random chains of ops evaluated by rushlite and by torch, forward value and
+every input gradient compared, with and without capture
+(tests/graphs/test_graphs.py:38-45, tests/graphs/runner.py:44-74,
+tests/stress/pytorch_stress_test.py:57-110).  This suite does the same for the
+MI355X backend with its own generator, in float64 and float32: each seed draws
+a program of 10-14 ops
+over broadcastable leaves -- binary ops, bounded unary ops, keep-dims
+reductions over either axis, matmul and transpose -- builds it in both
+libraries, and compares under Lamp3's normalised metric
+(tests/stress/testutils.py:47-50) at 1e-9.  Where Lamp3's gradient rules differ
+from torch's, the torch side uses Lamp3's: max/min send the gradient to every
+tied position (functions/reduct_ops.cpp:14; torch picks one), and clamp's
+backward uses strict bounds (cpu/kernels.hpp:143-152; torch's is inclusive).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+from _helpers import rel_err  # noqa: E402
+
+torch = pytest.importorskip("torch")
+
+SHAPES = [(16, 16), (16, 1), (1, 16), (16,)]
+TOL = 1e-9
+
+
+class _LampMax(torch.autograd.Function):
+    """max/min over `dim` (keep-dims) with Lamp3's tie rule: every position
+    equal to the result receives the gradient."""
+
+    @staticmethod
+    def forward(ctx, x, dim, is_max):
+        out = x.amax(dim, keepdim=True) if is_max else x.amin(dim, keepdim=True)
+        ctx.save_for_backward(x, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        x, out = ctx.saved_tensors
+        return g * (x == out).to(g.dtype), None, None
+
+
+class _LampClamp(torch.autograd.Function):
+    """clamp with Lamp3's strict-bounds backward (ClampBackwardFunctor,
+    cpu/kernels.hpp:143-152): a value sitting exactly on a bound gets no
+    gradient (torch passes it through)."""
+
+    @staticmethod
+    def forward(ctx, x, lo, hi):
+        ctx.save_for_backward(x)
+        ctx.lo, ctx.hi = lo, hi
+        return torch.clamp(x, lo, hi)
+
+    @staticmethod
+    def backward(ctx, g):
+        (x,) = ctx.saved_tensors
+        return g * ((x > ctx.lo) & (x < ctx.hi)).to(g.dtype), None, None
+
+
+class TorchOps:
+    add = staticmethod(lambda a, b: a + b)
+    sub = staticmethod(lambda a, b: a - b)
+    mul = staticmethod(lambda a, b: a * b)
+    div = staticmethod(lambda a, b: a / b)
+    pow = staticmethod(lambda a, b: a ** b)
+    neg = staticmethod(lambda a: -a)
+    exp = staticmethod(torch.exp)
+    log = staticmethod(torch.log)
+    sqrt = staticmethod(torch.sqrt)
+    sin = staticmethod(torch.sin)
+    cos = staticmethod(torch.cos)
+    tan = staticmethod(torch.tan)
+    abs = staticmethod(torch.abs)
+    clamp = staticmethod(lambda a, lo, hi: _LampClamp.apply(a, lo, hi))
+    sum = staticmethod(lambda a, d: a.sum(d, keepdim=True))
+    max = staticmethod(lambda a, d: _LampMax.apply(a, d, True))
+    min = staticmethod(lambda a, d: _LampMax.apply(a, d, False))
+    matmul = staticmethod(lambda a, b: a @ b)
+    transpose = staticmethod(lambda a: a.t())
+
+    @staticmethod
+    def const(like, v):
+        return torch.tensor([v], dtype=torch.float64)
+
+
+def lamp_ops(rsl, kind):
+    class LampOps:
+        add = staticmethod(lambda a, b: a + b)
+        sub = staticmethod(lambda a, b: a - b)
+        mul = staticmethod(lambda a, b: a * b)
+        div = staticmethod(lambda a, b: a / b)
+        pow = staticmethod(lambda a, b: rsl.pow(a, b))
+        neg = staticmethod(lambda a: -a)
+        exp = staticmethod(rsl.exp)
+        log = staticmethod(rsl.log)
+        sqrt = staticmethod(rsl.sqrt)
+        sin = staticmethod(rsl.sin)
+        cos = staticmethod(rsl.cos)
+        tan = staticmethod(rsl.tan)
+        abs = staticmethod(rsl.abs)
+        clamp = staticmethod(lambda a, lo, hi: rsl.clamp(a, lo, hi))
+        sum = staticmethod(lambda a, d: rsl.sum(a, d))
+        max = staticmethod(lambda a, d: rsl.max(a, d))
+        min = staticmethod(lambda a, d: rsl.min(a, d))
+        matmul = staticmethod(rsl.matmul)
+        transpose = staticmethod(rsl.transpose)
+
+        @staticmethod
+        def const(like, v):
+            return rsl.Variable(np.array([v]), dtype=kind)
+    return LampOps
+
+
+def broadcast(a, b):
+    a, b = list(a), list(b)
+    n = max(len(a), len(b))
+    a, b = [1] * (n - len(a)) + a, [1] * (n - len(b)) + b
+    out = []
+    for x, y in zip(a, b):
+        if x != 1 and y != 1 and x != y:
+            return None
+        out.append(max(x, y))
+    return tuple(out)
+
+
+def make_program(seed):
+    """A list of steps over a value pool; each step names an op and the pool
+    indices it reads, with every operation kept in a numerically tame range
+    (denominators >= 1, positive log/sqrt/pow arguments, bounded tan)."""
+    rng = np.random.default_rng(seed)
+    leaves = [SHAPES[i] for i in rng.integers(0, len(SHAPES), 4)]
+    leaves[0] = (16, 16)
+    shapes = list(leaves)
+    steps = []
+    for _ in range(int(rng.integers(10, 15))):
+        kind = rng.choice(["bin", "bin", "bin", "unary", "unary", "reduce", "matmul", "transpose"])
+        recent = list(range(max(0, len(shapes) - 5), len(shapes)))
+        if kind == "bin":
+            i = int(rng.choice(recent))
+            js = [j for j in range(len(shapes)) if broadcast(shapes[i], shapes[j])]
+            j = int(rng.choice(js))
+            op = str(rng.choice(["add", "sub", "mul", "div", "pow"]))
+            steps.append(("bin", op, i, j))
+            shapes.append(broadcast(shapes[i], shapes[j]))
+        elif kind == "unary":
+            i = int(rng.choice(recent))
+            op = str(rng.choice(["neg", "exp", "log", "sqrt", "sin", "cos", "tan", "abs", "clamp"]))
+            steps.append(("unary", op, i))
+            shapes.append(shapes[i])
+        elif kind == "reduce":
+            cand = [i for i in recent if len(shapes[i]) == 2]
+            if not cand:
+                continue
+            i = int(rng.choice(cand))
+            axis = int(rng.integers(0, 2))
+            op = str(rng.choice(["sum", "max", "min"]))
+            steps.append(("reduce", op, i, axis))
+            s = list(shapes[i])
+            s[axis] = 1
+            shapes.append(tuple(s))
+        elif kind == "matmul":
+            cand = [i for i in range(len(shapes)) if shapes[i] == (16, 16)]
+            rhs = [j for j in range(len(shapes)) if len(shapes[j]) == 2 and shapes[j][0] == 16]
+            i, j = int(rng.choice(cand)), int(rng.choice(rhs))
+            steps.append(("matmul", "matmul", i, j))
+            shapes.append((16, shapes[j][1]))
+        else:
+            cand = [i for i in recent if len(shapes[i]) == 2]
+            if not cand:
+                continue
+            i = int(rng.choice(cand))
+            steps.append(("transpose", "transpose", i))
+            shapes.append((shapes[i][1], shapes[i][0]))
+    return leaves, steps, shapes
+
+
+def run(ops, leaves, steps, shapes):
+    pool = list(leaves)
+    one = ops.const(pool[0], 1.0)
+    half = ops.const(pool[0], 0.5)
+    for st in steps:
+        kind, op = st[0], st[1]
+        if kind == "bin":
+            a, b = pool[st[2]], pool[st[3]]
+            if op == "div":
+                r = ops.div(a, ops.add(ops.mul(b, b), one))          # denominator >= 1
+            elif op == "pow":
+                r = ops.pow(ops.add(ops.mul(a, a), half), ops.clamp(b, -1.5, 1.5))
+            else:
+                r = getattr(ops, op)(a, b)
+        elif kind == "unary":
+            a = pool[st[2]]
+            if op in ("log", "sqrt"):
+                r = getattr(ops, op)(ops.add(ops.mul(a, a), one))
+            elif op == "exp":
+                r = ops.exp(ops.clamp(a, -3.0, 3.0))
+            elif op == "tan":
+                r = ops.tan(ops.mul(ops.sin(a), half))
+            elif op == "clamp":
+                r = ops.clamp(a, -0.75, 0.75)
+            else:
+                r = getattr(ops, op)(a)
+        elif kind == "reduce":
+            r = getattr(ops, op)(pool[st[2]], st[3])
+        elif kind == "matmul":
+            r = ops.matmul(pool[st[2]], pool[st[3]])
+        else:
+            r = ops.transpose(pool[st[2]])
+        pool.append(r)
+    out = pool[-1]
+    if len(shapes[-1]) == 1:
+        return ops.sum(out, 0)
+    return ops.sum(ops.sum(out, 0), 1)
+
+
+@pytest.fixture(scope="module")
+def rsl(hip):
+    import rushlite_amd
+    return rushlite_amd
+
+
+def check_graph(rsl, seed, capture, dtype, tol):
+    leaves, steps, shapes = make_program(seed)
+    rng = np.random.default_rng(1000 + seed)
+    arrs = [rng.uniform(-1.0, 1.0, s).astype(dtype) for s in leaves]
+    tv = [torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in arrs]
+    t_out = run(TorchOps, tv, steps, shapes)
+    t_out.backward()
+    kind = rsl.dtype.float64 if dtype == np.float64 else rsl.dtype.float32
+    lv = [rsl.Variable(a, requires_grad=True, dtype=kind) for a in arrs]
+    ops = lamp_ops(rsl, kind)
+    with rsl.capture_on(capture):
+        l_out = run(ops, lv, steps, shapes)
+    l_out.backward()
+    want = t_out.detach().numpy().reshape(-1)
+    got = l_out.numpy().reshape(-1)
+    assert rel_err(got, want) <= tol, (seed, steps)
+    for i, (t, l) in enumerate(zip(tv, lv)):
+        g_want = t.grad.numpy() if t.grad is not None else np.zeros(leaves[i])
+        assert rel_err(l.grad.numpy().reshape(g_want.shape), g_want) <= tol, (seed, i, steps)
+
+
+@pytest.mark.parametrize("capture", [False, True], ids=["eager", "captured"])
+@pytest.mark.parametrize("seed", range(24))
+def test_random_graph_float64_matches_torch(rsl, seed, capture):
+    check_graph(rsl, seed, capture, np.float64, TOL)
+
+
+@pytest.mark.parametrize("capture", [False, True], ids=["eager", "captured"])
+@pytest.mark.parametrize("seed", range(24))
+def test_random_graph_float32_matches_torch(rsl, seed, capture):
+    """The float32 path (fused regions, row kernels, MFMA GEMMs) on the same
+    programs, against torch float64 at the reference stress suites' 1e-4
+    (tests/stress/pytorch_stress_test.py:92-110)."""
+    check_graph(rsl, seed, capture, np.float32, 1e-4)
