@@ -201,10 +201,11 @@ def extras(rsl, abi, a, b, steps, warmup, evict, only=None):
         gemm = {}
         L = abi.lib()
         for (m, n, k) in ((4096, 4096, 4096), (8192, 8192, 8192), (32, 4096, 8192)):
-            X, W, dY = abi.DeviceBuffer((m, k)), abi.DeviceBuffer((k, n)), abi.DeviceBuffer((m, n))
+            # entries normal(0, 0.02) from fixed seeds (x 2, weights 10, dY 3)
+            X, W, dY = (abi.DeviceBuffer.from_numpy(
+                np.random.default_rng(seed).standard_normal(shape, dtype=np.float32) * 0.02)
+                for seed, shape in ((2, (m, k)), (10, (k, n)), (3, (m, n))))
             Y, dX, dW = abi.DeviceBuffer((m, n)), abi.DeviceBuffer((m, k)), abi.DeviceBuffer((k, n))
-            for buf, cnt in ((X, m * k), (W, k * n), (dY, m * n)):
-                abi.check(L.lmp_k_fill(abi.FLOAT32, buf.ptr, cnt, 0.01))
             # Linear: Y = X W ; dX = dY W^T ; dW = X^T dY   (each 2*m*n*k flop)
             cases = (("fwd", 0, 0, m, n, k, X, k, W, n, Y),
                      ("dX", 0, 1, m, k, n, dY, n, W, n, dX),
@@ -215,7 +216,8 @@ def extras(rsl, abi, a, b, steps, warmup, evict, only=None):
                 def run(ta=ta, tb=tb, mm=mm, nn=nn, kk=kk, A_=A_, lda=lda, B_=B_, ldb=ldb, C_=C_):
                     abi.check(L.lmp_k_gemm_f32(ta, tb, mm, nn, kk, A_.ptr, lda, B_.ptr, ldb,
                                                C_.ptr, nn, 0))
-                ms = time_steps(abi, run, r, 2) / r
+                # about 25 ms of warm-up so the clocks have settled
+                ms = time_steps(abi, run, r, 3 if m >= 8192 else 20) / r
                 flop = 2.0 * mm * nn * kk
                 gemm[f"{m}x{n}x{k}_{label}"] = {
                     "us": round(ms * 1e3, 1), "TFLOP/s": round(flop / ms / 1e9, 1),
@@ -226,9 +228,9 @@ def extras(rsl, abi, a, b, steps, warmup, evict, only=None):
     if want("f64"):
         # float64 GEMM (the reference's float64 suites run matmul on the device)
         n = 4096
-        A64, B64, C64 = (abi.DeviceBuffer((n, n), np.float64) for _ in range(3))
-        for buf in (A64, B64):
-            abi.check(L.lmp_k_fill(abi.FLOAT64, buf.ptr, n * n, 0.01))
+        A64, B64 = (abi.DeviceBuffer.from_numpy(
+            np.random.default_rng(seed).standard_normal((n, n)) * 0.02) for seed in (2, 10))
+        C64 = abi.DeviceBuffer((n, n), np.float64)
 
         def run64():
             abi.check(L.lmp_k_gemm(abi.FLOAT64, 0, 0, n, n, n, A64.ptr, n, B64.ptr, n, C64.ptr, n, 0))

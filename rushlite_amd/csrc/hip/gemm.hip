@@ -8,9 +8,11 @@
 // Tiling.  A workgroup of 4 waves owns a BM x BN tile of C; the waves form a
 // WGM x WGN grid and each wave owns TM x TN blocks of 32x32, accumulated by
 // one MFMA chain per block.  K advances BK = 32 at a time through two LDS
-// buffers: the next tile's global loads are issued into registers before the
-// MFMAs on the current tile and written to the other LDS buffer afterwards,
-// so one barrier per K step suffices.
+// buffers with one barrier per K step.  gemm_f32_mfma stages the next tile's
+// global loads in registers and writes them to the other LDS buffer after the
+// current tile's MFMAs; gemm_f32_lds_direct (128 x 128 tiles, operands that
+// allow 128-bit loads) loads straight into LDS and pipelines its fragment
+// reads inside the tile.
 //
 // MFMA operand layout.  For 32x32x2 a lane l supplies A[i][kk] and B[kk][j]
 // with i = j = l % 32 and kk = l / 32.  Within a BK tile, MFMA step s pairs
@@ -30,6 +32,7 @@
 
 #include <algorithm>
 #include <string>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -476,6 +479,230 @@ void gemm_direct(DirectArgs g) {
   }
 }
 
+// ------------------------------------------------------------- LDS-direct
+//
+// The 128 x 128 tile kernel for operands that allow 128-bit loads.  Panels go
+// from global memory straight into LDS with global_load_lds_dwordx4 (no VGPR
+// staging and no ds_write), two stages deep: the loads of K tile t+1 are issued
+// before the MFMAs of tile t, and one barrier per tile (after every wave's
+// loads have landed and its reads of the old stage are done) hands the stages
+// over.  Within a tile the four 4-step sub-steps are software-pipelined: the
+// LDS fragments of sub-step u+1 are read while the MFMAs of sub-step u run.
+// Tile walk, MFMA step order and epilogue are those of gemm_f32_mfma, so both
+// kernels produce identical bits.
+//
+// One DMA instruction fills a contiguous 1 KiB of LDS (lane i -> bytes 16i..),
+// so the LDS layout is chosen by which global float4 each lane fetches:
+//   K-major panel (32 k values contiguous in global: A untransposed, B
+//     transposed), 128 rows x 8 chunks of 4 floats: 16-byte slot p holds row
+//     p / 8, chunk (p % 8) ^ kswz(row).  A lane's fragment read (one row, one
+//     chunk) then spreads 16 consecutive rows over all 64 banks.
+//   N-major panel (128 m or n values contiguous: A transposed, B
+//     untransposed), 32 k-rows x 32 chunks: slot p holds k-row p / 32, chunk
+//     (p % 32) ^ 8 * (k-row / 16).  Lanes 32-63 read k-rows 16 apart from
+//     lanes 0-31; the swizzle moves them to the other half of the banks.
+// Lanes whose element lies outside the matrix fetch the zero page.
+constexpr int kPanel = 128 * kBK;  // floats per operand panel
+
+__device__ __forceinline__ int kswz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+// One 16-byte global load per lane into LDS.  Kept out of the templates: a
+// target builtin inside a kernel template keeps the host pass from emitting
+// that kernel's launch stub.
+__device__ __forceinline__ void lds_dma16(const float* src, float* lds) {
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+}
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(kThreads, 2) void gemm_f32_lds_direct(GemmArgs g) {
+  using C = CfgLarge;
+  constexpr int BM = C::BM, BN = C::BN;
+  constexpr int HK = kBK / 2;
+  constexpr int SU = 4;           // MFMA steps per sub-step
+  constexpr int NU = HK / SU;     // sub-steps per K tile
+  constexpr int STAGE = 2 * kPanel;
+  static_assert(BM == 128 && BN == 128 && NU % 2 == 0, "layout assumes 128 x 128 tiles");
+  __shared__ __attribute__((aligned(1024))) float smem[2 * STAGE];
+
+  const int ntiles = g.tiles_m * g.tiles_n;
+  int bid = blockIdx.x;
+  if (ntiles % 8 == 0) bid = (bid % 8) * (ntiles / 8) + bid / 8;
+  constexpr int kGroup = 8;
+  const int per_group = kGroup * g.tiles_n;
+  const int group = bid / per_group;
+  const int first_m = group * kGroup;
+  const int gsize = min(g.tiles_m - first_m, kGroup);
+  const int in_group = bid - group * per_group;
+  const int tile_m = first_m + in_group % gsize;
+  const int tile_n = in_group / gsize;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+
+  const int split = blockIdx.z;
+  const int k_tiles = (g.k + kBK - 1) / kBK;
+  const int kt0 = split * g.k_tiles_per_split;
+  const int kt1 = min(k_tiles, kt0 + g.k_tiles_per_split);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
+  const int li = lane & 31, lh = lane >> 5;
+
+  // The zero page's address, materialised once outside the loop.
+  uint64_t zero_bits = reinterpret_cast<uint64_t>(g_direct_zeros);
+  asm volatile("" : "+s"(zero_bits));
+  const float* zero = reinterpret_cast<const float*>(zero_bits);
+
+  // Each wave issues four DMA instructions per operand and K tile.  Per
+  // instruction q: the lane's fixed coordinate along m (or n), its k offset
+  // inside the tile, and its element offset without the tile's k0.
+  int a_mn[4], a_k[4], b_mn[4], b_k[4];
+  int64_t a_off[4], b_off[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int p = (wave * 4 + q) * 64 + lane;
+    if constexpr (!TA) {
+      const int r = p >> 3, c = (p & 7) ^ kswz(p >> 3);
+      a_mn[q] = m0 + r;
+      a_k[q] = 4 * c;
+      a_off[q] = int64_t(m0 + r) * g.lda + 4 * c;
+    } else {
+      const int kr = p >> 5, c = (p & 31) ^ ((kr >> 4) << 3);
+      a_mn[q] = m0 + 4 * c;
+      a_k[q] = kr;
+      a_off[q] = int64_t(kr) * g.lda + m0 + 4 * c;
+    }
+    if constexpr (TB) {
+      const int r = p >> 3, c = (p & 7) ^ kswz(p >> 3);
+      b_mn[q] = n0 + r;
+      b_k[q] = 4 * c;
+      b_off[q] = int64_t(n0 + r) * g.ldb + 4 * c;
+    } else {
+      const int kr = p >> 5, c = (p & 31) ^ ((kr >> 4) << 3);
+      b_mn[q] = n0 + 4 * c;
+      b_k[q] = kr;
+      b_off[q] = int64_t(kr) * g.ldb + n0 + 4 * c;
+    }
+  }
+  auto issue = [&](int kt, int stage) {
+    const int k0 = kt * kBK;
+    float* sa = smem + stage * STAGE;
+    float* sb = sa + kPanel;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool ok = a_mn[q] < g.m && k0 + a_k[q] < g.k;
+      const float* src = ok ? g.a + a_off[q] + (TA ? int64_t(k0) * g.lda : k0) : zero;
+      lds_dma16(src, sa + (wave * 4 + q) * 256);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool ok = b_mn[q] < g.n && k0 + b_k[q] < g.k;
+      const float* src = ok ? g.b + b_off[q] + (TB ? k0 : int64_t(k0) * g.ldb) : zero;
+      lds_dma16(src, sb + (wave * 4 + q) * 256);
+    }
+  };
+  // MFMA operands of sub-step u (steps SU*u .. SU*u+3 of the tile): step s
+  // reads k = s + HK*lh, as in gemm_f32_mfma.
+  auto read_frag = [&](int stage, int u, float (&fa)[C::TM][SU], float (&fb)[C::TN][SU]) {
+    const float* sa = smem + stage * STAGE;
+    const float* sb = sa + kPanel;
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+      const int row = (wm * C::TM + i) * 32 + li;
+      if constexpr (!TA) {
+        const int slot = row * 8 + ((lh * 4 + u) ^ kswz(row));
+        const v4f t = *reinterpret_cast<const v4f*>(sa + slot * 4);
+        fa[i][0] = t.x; fa[i][1] = t.y; fa[i][2] = t.z; fa[i][3] = t.w;
+      } else {
+#pragma unroll
+        for (int s = 0; s < SU; ++s)
+          fa[i][s] = sa[(lh * HK + SU * u + s) * BM + (row ^ (lh << 5))];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+      const int col = (wn * C::TN + j) * 32 + li;
+      if constexpr (TB) {
+        const int slot = col * 8 + ((lh * 4 + u) ^ kswz(col));
+        const v4f t = *reinterpret_cast<const v4f*>(sb + slot * 4);
+        fb[j][0] = t.x; fb[j][1] = t.y; fb[j][2] = t.z; fb[j][3] = t.w;
+      } else {
+#pragma unroll
+        for (int s = 0; s < SU; ++s)
+          fb[j][s] = sb[(lh * HK + SU * u + s) * BN + (col ^ (lh << 5))];
+      }
+    }
+  };
+
+  v16f acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) acc[i][j] = v16f(0.0f);
+  auto mma = [&](const float (&fa)[C::TM][SU], const float (&fb)[C::TN][SU]) {
+#pragma unroll
+    for (int s = 0; s < SU; ++s)
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+  };
+
+  float fa0[C::TM][SU], fb0[C::TN][SU], fa1[C::TM][SU], fb1[C::TN][SU];
+  if (kt0 < kt1) {
+    issue(kt0, 0);
+    // The memory clobber keeps the compiler from moving LDS accesses across.
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+  for (int kt = kt0; kt < kt1; ++kt) {
+    const int cur = (kt - kt0) & 1;
+    // The other stage was last read in the previous iteration, before its
+    // closing barrier.
+    if (kt + 1 < kt1) issue(kt + 1, cur ^ 1);
+    read_frag(cur, 0, fa0, fb0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      if (u + 1 < NU) {
+        if (u % 2 == 0) read_frag(cur, u + 1, fa1, fb1);
+        else read_frag(cur, u + 1, fa0, fb0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (u % 2 == 0) mma(fa0, fb0);
+      else mma(fa1, fb1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Next tile's panels landed (vmcnt) and this stage's reads are done
+    // (lgkmcnt) in every wave before anyone moves on.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+
+  const bool partial = gridDim.z > 1;
+  float* out = g.c;
+  int64_t ld = g.ldc;
+  if (partial) {
+    out = g.c + int64_t(split) * g.m * g.n;
+    ld = g.n;
+  }
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+      const int col = n0 + (wn * C::TN + j) * 32 + li;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + (wm * C::TM + i) * 32 + (r / 4) * 8 + lh * 4 + (r % 4);
+        if (row < g.m && col < g.n) {
+          float* p = out + int64_t(row) * ld + col;
+          const float v = acc[i][j][r];
+          if (!partial && g.accumulate) *p = *p + v;
+          else *p = v;
+        }
+      }
+    }
+  }
+}
+
 // Default split of K: none once there is a tile for every CU; otherwise
 // enough splits to give each CU two workgroups, keeping at least four K tiles
 // per split.
@@ -506,7 +733,10 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
     g.c = part;
   }
   const dim3 grid{uint32_t(tiles), 1u, uint32_t(splits)};
-  if (vec)
+  if (vec && std::is_same_v<C, CfgLarge>)
+    hipLaunchKernelGGL((gemm_f32_lds_direct<TA, TB>), grid, dim3(kThreads), 0,
+                       rt->stream, g);
+  else if (vec)
     hipLaunchKernelGGL((gemm_f32_mfma<C, TA, TB, true>), grid, dim3(kThreads), 0,
                        rt->stream, g);
   else
