@@ -244,10 +244,15 @@ def extras(rsl, abi, a, b, steps, warmup, evict, only=None):
         # --- config 4 and config 0: MLP training loops
         out["c4_wide_mlp"] = mlp_bench(rsl, abi, (4096, 4096, 4096, 1000), 512, 50, onehot=True)
         out["c0_readme_mlp"] = mlp_bench(rsl, abi, (256, 64, 10), 32, 100, onehot=False)
+        # the same loops with each step replayed from a captured HIP graph
+        out["c4_wide_mlp_hip_graph"] = mlp_bench(rsl, abi, (4096, 4096, 4096, 1000), 512, 50,
+                                                 onehot=True, graph=True)
+        out["c0_readme_mlp_hip_graph"] = mlp_bench(rsl, abi, (256, 64, 10), 32, 100,
+                                                   onehot=False, graph=True)
     return out
 
 
-def mlp_bench(rsl, abi, dims, batch, steps, onehot):
+def mlp_bench(rsl, abi, dims, batch, steps, onehot, graph=False):
     from rushlite_amd.nets import layers
     rng = np.random.default_rng(2)
     if onehot:
@@ -282,6 +287,7 @@ def mlp_bench(rsl, abi, dims, batch, steps, onehot):
         loss.backward()
         for name, p in list(model.named_parameters()):
             model.params[name] = rsl.Variable(p.data - 1e-3 * p.grad, requires_grad=True)
+        loss.realize()
         return loss
 
     s0 = rsl._stats()
@@ -289,11 +295,21 @@ def mlp_bench(rsl, abi, dims, batch, steps, onehot):
     s1 = rsl._stats()
     for _ in range(2):
         step()
+    if graph:
+        # the whole step (forward, backward, SGD) as one HIP graph launch
+        g = rsl.hip.Graph()
+        with g.capture(carry=model):
+            loss = step()
+        run = g.replay
+    else:
+        run = step
     abi.synchronize()
     t0 = time.perf_counter()
     with Events(abi) as ev:
         for _ in range(steps):
-            loss = step()
+            out = run()
+            if not graph:
+                loss = out
     wall = time.perf_counter() - t0
     last = loss.tolist()[0]
     launches = (s1["eager_launches"] + s1["fused_launches"]
@@ -305,7 +321,8 @@ def mlp_bench(rsl, abi, dims, batch, steps, onehot):
     return {"steps": steps, "steps/s": round(steps / wall, 2),
             "ms_per_step": round(wall * 1e3 / steps, 3),
             "gpu_event_ms_per_step": round(ev.ms / steps, 3),
-            "kernel_launches_per_step": launches,
+            "kernel_launches_per_step": 1 if graph else launches,
+            "kernels_per_step": launches,
             "gemm_TFLOP/s_effective": round(gemm_flop * steps / wall / 1e12, 2),
             "final_loss": last}
 

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define LMP_HIP_ABI_VERSION 2
+#define LMP_HIP_ABI_VERSION 3
 #define LMP_MAX_DIMS 16 /* align_utils.hpp:7 */
 
 typedef enum {
@@ -164,6 +164,30 @@ int lmp_rt_event_create(void** event);
 int lmp_rt_event_record(void* event);
 int lmp_rt_event_elapsed_ms(void* start, void* stop, float* ms);
 int lmp_rt_event_destroy(void* event);
+
+/* HIP graphs: record the library stream's work once, replay it with one
+ * launch.  No counterpart in the reference, which launches every kernel from
+ * the host each step; here a whole training step (forward, backward, update)
+ * can become one hipGraphLaunch.
+ *   lmp_rt_graph_begin   start capturing the library stream.  Until end or
+ *                        abort, kernel entry points record instead of run,
+ *                        and lmp_rt_malloc serves the graph's private pool:
+ *                        those blocks are never handed to eager allocations,
+ *                        so replays cannot overwrite other tensors.
+ *                        h2d/d2h copies, synchronize and event timing fail
+ *                        with LMP_ERR_INVALID during a capture.
+ *   lmp_rt_graph_end     close the capture and instantiate it (*graph).
+ *   lmp_rt_graph_abort   close and discard an open capture (error paths).
+ *   lmp_rt_graph_launch  enqueue one replay on the library stream.
+ *   lmp_rt_graph_destroy free the graph; its pool's memory returns to HIP once
+ *                        every block allocated in it has been freed.
+ * Buffers allocated before the capture and read by it must outlive the graph.
+ * One capture at a time, from one host thread. */
+int lmp_rt_graph_begin(void);
+int lmp_rt_graph_end(void** graph);
+int lmp_rt_graph_abort(void);
+int lmp_rt_graph_launch(void* graph);
+int lmp_rt_graph_destroy(void* graph);
 
 /* ------------------------------------------------------ elementwise kernels */
 

@@ -22,6 +22,11 @@ from ._C import Variable
 from ._C import _fused_source, _is_deferred, _stats, _storage_ptr  # noqa: F401
 from .capture_mode import capture, capture_on
 from .grad_mode import no_grad
+from .graphs import Graph as _Graph
 from .nets.Module import Module
+
+# rsl.hip.Graph (and its rsl.cuda alias): whole-step HIP graphs.
+hip.Graph = _Graph  # noqa: F405
+cuda.Graph = _Graph  # noqa: F405
 
 __all__ = ["Variable", "Module", "capture_on", "capture", "no_grad"]

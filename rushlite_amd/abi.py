@@ -81,6 +81,11 @@ SIGNATURES = {
     "lmp_rt_event_record": (_i, [_vp]),
     "lmp_rt_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(C.c_float)]),
     "lmp_rt_event_destroy": (_i, [_vp]),
+    "lmp_rt_graph_begin": (_i, []),
+    "lmp_rt_graph_end": (_i, [C.POINTER(_vp)]),
+    "lmp_rt_graph_abort": (_i, []),
+    "lmp_rt_graph_launch": (_i, [_vp]),
+    "lmp_rt_graph_destroy": (_i, [_vp]),
     "lmp_k_binary": (_i, [_i, _i, _vp, _vp, _vp, C.POINTER(Bcast), _d, _d]),
     "lmp_k_unary": (_i, [_i, _i, _vp, _vp, _sz, _d, _d]),
     "lmp_k_fill": (_i, [_i, _vp, _sz, _d]),

@@ -125,6 +125,42 @@ void device_sync() {
 
 Variable s2v(const Variable& like, Scalar s) { return ag::scalar_var(like, s); }
 
+// One captured device graph (lmp_rt_graph_*): the library stream's work
+// between begin() and end(), replayed by launch().  Scalars the capture reads
+// are kept here for the graph's lifetime.
+struct HipGraph {
+  void* handle = nullptr;
+  bool open = false;
+  std::vector<Tensor> keep;
+
+  void begin() {
+    LMP_CHECK(!open && !handle) << "graph: already captured (make a new Graph)";
+    lmp::hip_ok(lmp_rt_graph_begin(), "lmp_rt_graph_begin");
+    open = true;
+    lmp::tensor::set_graph_keep_alive(&keep);
+  }
+  void end() {
+    LMP_CHECK(open) << "graph: no capture is open";
+    lmp::tensor::set_graph_keep_alive(nullptr);
+    open = false;
+    lmp::hip_ok(lmp_rt_graph_end(&handle), "lmp_rt_graph_end");
+  }
+  void abort() {
+    if (!open) return;
+    lmp::tensor::set_graph_keep_alive(nullptr);
+    open = false;
+    lmp_rt_graph_abort();
+  }
+  void launch() {
+    LMP_CHECK(handle) << "graph: nothing captured";
+    lmp::hip_ok(lmp_rt_graph_launch(handle), "lmp_rt_graph_launch");
+  }
+  ~HipGraph() {
+    abort();
+    if (handle) lmp_rt_graph_destroy(handle);
+  }
+};
+
 }  // namespace
 
 PYBIND11_MODULE(_C, m) {
@@ -149,6 +185,14 @@ PYBIND11_MODULE(_C, m) {
     sub.def("sync", &device_sync, "Wait for all queued device work.");
     sub.def("is_available", &device_available);
   }
+  py::class_<HipGraph>(m.attr("hip"), "_Graph")
+      .def(py::init<>())
+      .def("begin", &HipGraph::begin)
+      .def("end", &HipGraph::end)
+      .def("abort", &HipGraph::abort)
+      .def("launch", &HipGraph::launch)
+      .def_property_readonly("captured", [](const HipGraph& g) { return g.handle != nullptr; })
+      .def_property_readonly("capturing", [](const HipGraph& g) { return g.open; });
   m.attr("hip").attr("device_info") = py::cpp_function([]() {
     lmp_rt_info info{};
     lmp::hip_ok(lmp_rt_device_info(&info), "lmp_rt_device_info");

@@ -110,6 +110,8 @@ void add_inplace(Tensor& dst, const Tensor& src);
 // Tensor-level operators with scalar overloads; a scalar becomes a [1] tensor
 // of the other operand's dtype and device (native/overloads.hpp:16-28).
 Tensor scalar_like(const Tensor& t, Scalar s);
+// Route scalars made during a device-graph capture into `keep` (nullptr ends it).
+void set_graph_keep_alive(std::vector<Tensor>* keep);
 #define LMP_TENSOR_OPERATOR(sym, fn)                                        \
   inline Tensor operator sym(const Tensor& a, const Tensor& b) { return ops::fn(a, b); } \
   inline Tensor operator sym(const Tensor& a, Scalar s) {                   \

@@ -275,18 +275,39 @@ Tensor zeros_like(const Tensor& t) { return full_like(t, 0); }
 // to the user and never written in place, so each distinct (device, dtype,
 // value) is built once and shared; a training loop then issues no upload per
 // scalar per step.
+//
+// While a device graph is captured the value upload is only recorded, so a
+// scalar first made then stays out of the cache; every scalar the capture uses
+// is also kept in the graph's keep-alive list, since its buffer is read by
+// each replay.
+namespace {
+std::mutex g_scalar_mu;
+std::vector<Tensor>* g_graph_keep = nullptr;
+}  // namespace
+
+void set_graph_keep_alive(std::vector<Tensor>* keep) {
+  std::lock_guard<std::mutex> lock(g_scalar_mu);
+  g_graph_keep = keep;
+}
+
 Tensor scalar_like(const Tensor& t, Scalar s) {
   using Key = std::tuple<uint64_t, size_t, int>;
-  static std::mutex mu;
   static auto* cache = new std::map<Key, Tensor>();  // outlives static teardown
   uint64_t bits;
   std::memcpy(&bits, &s, sizeof bits);
   const Key key{bits, static_cast<size_t>(t.device()), static_cast<int>(t.type())};
-  std::lock_guard<std::mutex> lock(mu);
+  std::lock_guard<std::mutex> lock(g_scalar_mu);
   auto it = cache->find(key);
-  if (it != cache->end()) return it->second;
-  if (cache->size() >= 4096) cache->clear();
+  if (it != cache->end()) {
+    if (g_graph_keep) g_graph_keep->push_back(it->second);
+    return it->second;
+  }
   Tensor fresh(std::vector<Scalar>{s}, {1}, t.device(), t.type());
+  if (g_graph_keep) {
+    g_graph_keep->push_back(fresh);
+    return fresh;
+  }
+  if (cache->size() >= 4096) cache->clear();
   cache->emplace(key, fresh);
   return fresh;
 }

@@ -5,8 +5,10 @@
 
 #include <algorithm>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "arena.hpp"
 #include "common.hpp"
@@ -22,11 +24,29 @@ thread_local std::string t_error;
 constexpr size_t kAlign = 256;
 constexpr size_t kMinSegment = 128ull << 20;
 
+// Memory of one captured graph.  Every block allocated while the graph is
+// captured comes from here and returns here when freed, so no eager
+// allocation can reuse an address the graph's replays write.  Segments go back
+// to HIP once the graph is destroyed and the last block is freed.
+struct GraphPool {
+  Arena arena{kAlign};
+  bool dead = false;
+};
+
 struct Pool {
   std::mutex mu;
   Arena arena{kAlign};
+  std::vector<std::unique_ptr<GraphPool>> graph_pools;
+  GraphPool* capturing = nullptr;  // allocation target during a graph capture
   uint64_t allocs = 0;
   uint64_t device_mallocs = 0;
+};
+
+// A captured, instantiated graph (the opaque handle of lmp_rt_graph_*).
+struct GraphHandle {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  GraphPool* pool = nullptr;
 };
 
 Pool& pool() {
@@ -69,12 +89,13 @@ int init_locked(int device) {
   return LMP_OK;
 }
 
-int grow_and_allocate(Pool& p, size_t bytes, void** out) {
-  const size_t need = p.arena.round_up(bytes);
+int grow_and_allocate(Pool& p, Arena& arena, size_t bytes, void** out) {
+  const size_t need = arena.round_up(bytes);
   const size_t seg = std::max(kMinSegment, need);
   void* base = nullptr;
   hipError_t e = hipMalloc(&base, seg);
-  if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) {
+  // The release-and-retry path synchronises the stream, which a capture forbids.
+  if ((e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) && !p.capturing) {
     (void)hipGetLastError();
     // Release cached segments once, then retry (allocator.cu:101-125).
     hipError_t se = hipStreamSynchronize(g_rt.stream);
@@ -91,15 +112,51 @@ int grow_and_allocate(Pool& p, size_t bytes, void** out) {
                                  " bytes failed: " + hipGetErrorString(e));
   }
   ++p.device_mallocs;
-  if (!p.arena.add_segment(reinterpret_cast<Arena::Addr>(base), seg))
+  if (!arena.add_segment(reinterpret_cast<Arena::Addr>(base), seg))
     return fail(LMP_ERR_RUNTIME, "allocator: hipMalloc returned a misaligned "
                                  "or overlapping segment");
-  auto span = p.arena.allocate(bytes);
+  auto span = arena.allocate(bytes);
   if (!span)
     return fail(LMP_ERR_RUNTIME, "allocator: new segment cannot serve request");
   *out = reinterpret_cast<void*>(span->addr);
   return LMP_OK;
 }
+
+// Hand the segments of destroyed graphs whose blocks are all freed back to
+// HIP.  Needs an idle stream (a replay may still be running), so it never runs
+// during a capture.  Called with p.mu held.
+int release_dead_pools(Pool& p) {
+  if (p.capturing) return LMP_OK;
+  bool any = false;
+  for (const auto& gp : p.graph_pools) any |= gp->dead && gp->arena.in_use_bytes() == 0;
+  if (!any) return LMP_OK;
+  LMP_HIP_TRY(hipStreamSynchronize(g_rt.stream));
+  for (auto it = p.graph_pools.begin(); it != p.graph_pools.end();) {
+    GraphPool& gp = **it;
+    if (gp.dead && gp.arena.in_use_bytes() == 0) {
+      for (const Arena::Span& s : gp.arena.take_free_segments())
+        LMP_HIP_TRY(hipFree(reinterpret_cast<void*>(s.addr)));
+      it = p.graph_pools.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  return LMP_OK;
+}
+
+bool capturing() {
+  Pool& p = pool();
+  std::lock_guard<std::mutex> lock(p.mu);
+  return p.capturing != nullptr;
+}
+
+#define LMP_NOT_WHILE_CAPTURING(what)                                          \
+  do {                                                                         \
+    if (capturing())                                                           \
+      return fail(LMP_ERR_INVALID, std::string(what) +                         \
+                                       ": not allowed while a graph is being " \
+                                       "captured");                            \
+  } while (0)
 
 }  // namespace
 
@@ -179,30 +236,36 @@ int lmp_rt_malloc(void** ptr, size_t bytes) {
   Pool& p = pool();
   std::lock_guard<std::mutex> lock(p.mu);
   ++p.allocs;
-  if (auto span = p.arena.allocate(bytes)) {
+  Arena& arena = p.capturing ? p.capturing->arena : p.arena;
+  if (auto span = arena.allocate(bytes)) {
     *ptr = reinterpret_cast<void*>(span->addr);
     return LMP_OK;
   }
-  return grow_and_allocate(p, bytes, ptr);
+  return grow_and_allocate(p, arena, bytes, ptr);
 }
 
 int lmp_rt_free(void* ptr) {
   if (!ptr) return LMP_OK;
   Pool& p = pool();
   std::lock_guard<std::mutex> lock(p.mu);
-  if (!p.arena.release(reinterpret_cast<Arena::Addr>(ptr)))
-    return fail(LMP_ERR_INVALID, "lmp_rt_free: pointer not owned by the pool");
-  return LMP_OK;
+  const auto addr = reinterpret_cast<Arena::Addr>(ptr);
+  if (p.arena.release(addr)) return LMP_OK;
+  for (const auto& gp : p.graph_pools) {
+    if (gp->arena.release(addr)) return gp->dead ? release_dead_pools(p) : LMP_OK;
+  }
+  return fail(LMP_ERR_INVALID, "lmp_rt_free: pointer not owned by the pool");
 }
 
 int lmp_rt_empty_cache(void) {
   LMP_RUNTIME_OR_FAIL(rt);
   Pool& p = pool();
   std::lock_guard<std::mutex> lock(p.mu);
+  if (p.capturing)
+    return fail(LMP_ERR_INVALID, "lmp_rt_empty_cache: not allowed while a graph is being captured");
   LMP_HIP_TRY(hipStreamSynchronize(rt->stream));
   for (const Arena::Span& s : p.arena.take_free_segments())
     LMP_HIP_TRY(hipFree(reinterpret_cast<void*>(s.addr)));
-  return LMP_OK;
+  return release_dead_pools(p);
 }
 
 int lmp_rt_pool_stats_get(lmp_rt_pool_stats* stats) {
@@ -220,6 +283,7 @@ int lmp_rt_pool_stats_get(lmp_rt_pool_stats* stats) {
 int lmp_rt_memcpy_h2d(void* dst, const void* src, size_t bytes) {
   if (bytes == 0) return LMP_OK;
   if (!dst || !src) return fail(LMP_ERR_INVALID, "memcpy_h2d: null pointer");
+  LMP_NOT_WHILE_CAPTURING("memcpy_h2d");
   LMP_RUNTIME_OR_FAIL(rt);
   LMP_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, rt->stream));
   // The source may be pageable memory the caller reuses right away.
@@ -230,6 +294,7 @@ int lmp_rt_memcpy_h2d(void* dst, const void* src, size_t bytes) {
 int lmp_rt_memcpy_d2h(void* dst, const void* src, size_t bytes) {
   if (bytes == 0) return LMP_OK;
   if (!dst || !src) return fail(LMP_ERR_INVALID, "memcpy_d2h: null pointer");
+  LMP_NOT_WHILE_CAPTURING("memcpy_d2h");
   LMP_RUNTIME_OR_FAIL(rt);
   LMP_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, rt->stream));
   LMP_HIP_TRY(hipStreamSynchronize(rt->stream));
@@ -245,6 +310,7 @@ int lmp_rt_memcpy_d2d(void* dst, const void* src, size_t bytes) {
 }
 
 int lmp_rt_synchronize(void) {
+  LMP_NOT_WHILE_CAPTURING("synchronize");
   LMP_RUNTIME_OR_FAIL(rt);
   LMP_HIP_TRY(hipStreamSynchronize(rt->stream));
   return LMP_OK;
@@ -274,6 +340,7 @@ int lmp_rt_event_record(void* event) {
 
 int lmp_rt_event_elapsed_ms(void* start, void* stop, float* ms) {
   if (!start || !stop || !ms) return fail(LMP_ERR_INVALID, "null argument");
+  LMP_NOT_WHILE_CAPTURING("event_elapsed_ms");
   LMP_HIP_TRY(hipEventSynchronize(static_cast<hipEvent_t>(stop)));
   LMP_HIP_TRY(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
                                   static_cast<hipEvent_t>(stop)));
@@ -284,6 +351,85 @@ int lmp_rt_event_destroy(void* event) {
   if (!event) return LMP_OK;
   LMP_HIP_TRY(hipEventDestroy(static_cast<hipEvent_t>(event)));
   return LMP_OK;
+}
+
+int lmp_rt_graph_begin(void) {
+  LMP_RUNTIME_OR_FAIL(rt);
+  Pool& p = pool();
+  std::lock_guard<std::mutex> lock(p.mu);
+  if (p.capturing) return fail(LMP_ERR_INVALID, "graph_begin: a capture is already open");
+  // Eager work queued before the capture runs now, outside the graph.
+  LMP_HIP_TRY(hipStreamSynchronize(rt->stream));
+  auto gp = std::make_unique<GraphPool>();
+  // Relaxed mode: pool growth (hipMalloc) stays legal inside the capture.
+  hipError_t e = hipStreamBeginCapture(rt->stream, hipStreamCaptureModeRelaxed);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(LMP_ERR_RUNTIME, std::string("hipStreamBeginCapture: ") + hipGetErrorString(e));
+  }
+  p.capturing = gp.get();
+  p.graph_pools.push_back(std::move(gp));
+  return LMP_OK;
+}
+
+int lmp_rt_graph_end(void** graph) {
+  if (!graph) return fail(LMP_ERR_INVALID, "graph_end: null out pointer");
+  *graph = nullptr;
+  LMP_RUNTIME_OR_FAIL(rt);
+  Pool& p = pool();
+  std::lock_guard<std::mutex> lock(p.mu);
+  if (!p.capturing) return fail(LMP_ERR_INVALID, "graph_end: no capture is open");
+  GraphPool* gp = p.capturing;
+  p.capturing = nullptr;
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(rt->stream, &g);
+  hipGraphExec_t exec = nullptr;
+  if (e == hipSuccess) e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    if (g) (void)hipGraphDestroy(g);
+    gp->dead = true;  // blocks still held by tensors keep it until freed
+    return fail(LMP_ERR_RUNTIME, std::string("graph capture failed: ") + hipGetErrorString(e));
+  }
+  *graph = new GraphHandle{g, exec, gp};
+  return LMP_OK;
+}
+
+int lmp_rt_graph_abort(void) {
+  LMP_RUNTIME_OR_FAIL(rt);
+  Pool& p = pool();
+  std::lock_guard<std::mutex> lock(p.mu);
+  if (!p.capturing) return LMP_OK;
+  p.capturing->dead = true;
+  p.capturing = nullptr;
+  hipGraph_t g = nullptr;
+  (void)hipStreamEndCapture(rt->stream, &g);
+  (void)hipGetLastError();
+  if (g) (void)hipGraphDestroy(g);
+  return LMP_OK;
+}
+
+int lmp_rt_graph_launch(void* graph) {
+  if (!graph) return fail(LMP_ERR_INVALID, "graph_launch: null graph");
+  LMP_NOT_WHILE_CAPTURING("graph_launch");
+  LMP_RUNTIME_OR_FAIL(rt);
+  LMP_HIP_TRY(hipGraphLaunch(static_cast<GraphHandle*>(graph)->exec, rt->stream));
+  return LMP_OK;
+}
+
+int lmp_rt_graph_destroy(void* graph) {
+  if (!graph) return LMP_OK;
+  LMP_NOT_WHILE_CAPTURING("graph_destroy");
+  LMP_RUNTIME_OR_FAIL(rt);
+  auto* h = static_cast<GraphHandle*>(graph);
+  LMP_HIP_TRY(hipStreamSynchronize(rt->stream));
+  LMP_HIP_TRY(hipGraphExecDestroy(h->exec));
+  LMP_HIP_TRY(hipGraphDestroy(h->graph));
+  Pool& p = pool();
+  std::lock_guard<std::mutex> lock(p.mu);
+  h->pool->dead = true;
+  delete h;
+  return release_dead_pools(p);
 }
 
 }  // extern "C"
