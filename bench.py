@@ -244,15 +244,17 @@ def extras(rsl, abi, a, b, steps, warmup, evict, only=None):
         # --- config 4 and config 0: MLP training loops
         out["c4_wide_mlp"] = mlp_bench(rsl, abi, (4096, 4096, 4096, 1000), 512, 50, onehot=True)
         out["c0_readme_mlp"] = mlp_bench(rsl, abi, (256, 64, 10), 32, 100, onehot=False)
-        # the same loops with each step replayed from a captured HIP graph
+        # the SGD update captured (fused), then each step replayed from a HIP graph
+        out["c4_wide_mlp_fused_update"] = mlp_bench(rsl, abi, (4096, 4096, 4096, 1000), 512, 50,
+                                                    onehot=True, fused_update=True)
         out["c4_wide_mlp_hip_graph"] = mlp_bench(rsl, abi, (4096, 4096, 4096, 1000), 512, 50,
-                                                 onehot=True, graph=True)
+                                                 onehot=True, graph=True, fused_update=True)
         out["c0_readme_mlp_hip_graph"] = mlp_bench(rsl, abi, (256, 64, 10), 32, 100,
-                                                   onehot=False, graph=True)
+                                                   onehot=False, graph=True, fused_update=True)
     return out
 
 
-def mlp_bench(rsl, abi, dims, batch, steps, onehot, graph=False):
+def mlp_bench(rsl, abi, dims, batch, steps, onehot, graph=False, fused_update=False):
     from rushlite_amd.nets import layers
     rng = np.random.default_rng(2)
     if onehot:
@@ -285,8 +287,11 @@ def mlp_bench(rsl, abi, dims, batch, steps, onehot, graph=False):
         probs = forward(x)
         loss = (-y * rsl.log(probs + 1e-3)).sum(1).sum(0)
         loss.backward()
-        for name, p in list(model.named_parameters()):
-            model.params[name] = rsl.Variable(p.data - 1e-3 * p.grad, requires_grad=True)
+        # SGD as the reference README writes it; with fused_update the same
+        # expression is captured, so p - lr*g is one fused kernel per parameter
+        with rsl.capture_on(fused_update):
+            for name, p in list(model.named_parameters()):
+                model.params[name] = rsl.Variable(p.data - 1e-3 * p.grad, requires_grad=True)
         loss.realize()
         return loss
 

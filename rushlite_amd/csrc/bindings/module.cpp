@@ -23,6 +23,7 @@ namespace tops = lmp::tensor::ops;
 
 namespace lmp::tensor::hip {
 std::string fused_source_for(TensorImpl* root);
+bool realize_into(TensorImpl* root, const Storage& target);
 }
 
 namespace {
@@ -399,6 +400,22 @@ PYBIND11_MODULE(_C, m) {
   });
   m.def("_is_deferred", [](const Variable& v) {
     return lmp::tensor::detail::UnsafeTensorAccessor::getImpl(v.data())->is_deferred();
+  });
+  // dst receives src's value.  A pending fused elementwise src is computed
+  // straight into dst's buffer and then shares it (True); anything else is
+  // realised and copied (False).
+  m.def("_realize_into", [](Tensor& dst, Tensor& src) {
+    auto di = lmp::tensor::detail::UnsafeTensorAccessor::getImpl(dst);
+    auto si = lmp::tensor::detail::UnsafeTensorAccessor::getImpl(src);
+    LMP_CHECK(di->numel() == si->numel() && di->type() == si->type() &&
+              di->device() == si->device())
+        << "realize_into: tensors differ in size, dtype or device";
+    dst.realize();
+    if (si->device() == DeviceType::HIP &&
+        lmp::tensor::hip::realize_into(si.get(), di->storage()))
+      return true;
+    dst.copy(src);
+    return false;
   });
   m.def("_storage_ptr", [](const Tensor& t) {
     return reinterpret_cast<uintptr_t>(

@@ -592,9 +592,15 @@ struct Compiled {
   std::vector<int64_t> sig;
 };
 
+// Storage the next fused root should be computed into (realize_into); taken
+// by the root's realize() before any leaf is realised.
+thread_local const Storage* t_target = nullptr;
+
 class HipFusionBackend : public lazy::LazyBackend {
  public:
   void realize(TensorImpl* root) override {
+    const Storage* target = t_target;
+    t_target = nullptr;
     if (!root->is_deferred()) return;
     if (!fusible_node(root)) {
       for (const auto& in : root->lazy_op()->inputs) in->data();
@@ -613,7 +619,14 @@ class HipFusionBackend : public lazy::LazyBackend {
     }
     const std::vector<size_t> shape = root->shape();
     const size_t n = shape_numel(shape);
-    Storage out(n * dtype_size(root->type()), DeviceType::HIP);
+    // Writing into the target is safe when every leaf stored there is read at
+    // the output's own index: same shape, elementwise region.
+    bool in_place = target && target->byte_size() == n * dtype_size(root->type()) && !rp.ok;
+    if (in_place) {
+      for (TensorImpl* leaf : r.leaves)
+        if (leaf->raw() == target->data() && leaf->shape() != shape) in_place = false;
+    }
+    Storage out = in_place ? *target : Storage(n * dtype_size(root->type()), DeviceType::HIP);
     if (n == 0) {
       root->set_realized(out);
       return;
@@ -671,6 +684,14 @@ const bool kRegistered = [] {
 }  // namespace
 
 // Source of the kernel a region would compile to; for tests and inspection.
+bool realize_into(TensorImpl* root, const Storage& target) {
+  if (!root->is_deferred()) return false;
+  t_target = &target;
+  root->data();
+  t_target = nullptr;
+  return root->raw() == target.data();
+}
+
 std::string fused_source_for(TensorImpl* root) {
   LMP_CHECK(root->is_deferred()) << "tensor has no pending graph";
   const Region r = build_region(root);

@@ -23,14 +23,18 @@ Rules, as for any stream capture:
     stay valid while the graph lives; each replay writes the same addresses.
   * Inputs made before the capture (x and y above, the parameters) are read at
     their addresses by every replay: update them in place (`Tensor.copy`,
-    `Tensor.fill`) rather than rebinding them.
+    `Tensor.fill`) rather than rebinding them.  Realise pending (captured)
+    inputs before the capture; the carried parameters are realised for you.
   * Host round trips (building a Variable from host data, `tolist()`,
     `numpy()`, synchronising) raise inside a capture.
   * `carry` handles functional parameter updates (`model.params[name] =
     Variable(p.data - lr * p.grad)`): for every parameter whose Variable the
-    step replaced, the capture ends with a device copy of the new value into
-    the old buffer, so the next replay reads the updated parameters.  It takes
-    a Module, a mapping of Variables, or a callable returning one.
+    step replaced, the new value ends up in the old buffer, so the next replay
+    reads the updated parameters.  An update made under `capture_on()` is
+    still pending when the capture ends and is computed straight into the old
+    buffer (one fused kernel, no extra traffic); an eager update is copied
+    there.  `carry` takes a Module, a mapping of Variables, or a callable
+    returning one.
 """
 from __future__ import annotations
 
@@ -65,6 +69,9 @@ class Graph:
         if self._g.captured or self._g.capturing:
             raise RuntimeError("graph: already captured (make a new Graph)")
         before = _snapshot(carry)
+        # Pending updates from an earlier eager step belong outside the graph.
+        for v in before.values():
+            v.realize()
         _C.hip.sync()
         self._g.begin()
         try:
@@ -76,7 +83,10 @@ class Graph:
                     continue
                 src, dst = new.data, old.data
                 if _C._storage_ptr(src) != _C._storage_ptr(dst):
-                    dst.copy(src)
+                    # A pending fused update (made under capture_on) is
+                    # computed straight into the old buffer; anything else is
+                    # copied there.
+                    _C._realize_into(dst, src)
             self._g.end()
         except BaseException:
             self._g.abort()

@@ -46,7 +46,7 @@ def _problem(dims, batch, seed=2):
     return x, y, ws, bs
 
 
-def _stepper(rsl, model, x, y, lr=1e-3):
+def _stepper(rsl, model, x, y, lr=1e-3, fused_update=False):
     @rsl.capture()
     def forward(inp):
         return model(inp)
@@ -55,8 +55,9 @@ def _stepper(rsl, model, x, y, lr=1e-3):
         probs = forward(x)
         loss = (-y * rsl.log(probs + 1e-3)).sum(1).sum(0)
         loss.backward()
-        for name, p in list(model.named_parameters()):
-            model.params[name] = rsl.Variable(p.data - lr * p.grad, requires_grad=True)
+        with rsl.capture_on(fused_update):
+            for name, p in list(model.named_parameters()):
+                model.params[name] = rsl.Variable(p.data - lr * p.grad, requires_grad=True)
         loss.realize()  # inside a capture, so each replay recomputes it
         return loss
     return step
@@ -71,15 +72,19 @@ def _params(model):
 CASES = [((256, 64, 10), 32), ((1024, 512, 256, 10), 32)]
 
 
+@pytest.mark.parametrize("fused_update", [False, True], ids=["eager_sgd", "fused_sgd"])
 @pytest.mark.parametrize("dims,batch", CASES)
-def test_graph_replays_equal_eager_steps(rsl, dims, batch):
+def test_graph_replays_equal_eager_steps(rsl, dims, batch, fused_update):
+    """With the SGD update eager the capture ends with a copy of each new
+    parameter into the buffer the graph reads; with the update captured it is
+    computed straight into that buffer.  Both must equal the eager steps."""
     x_np, y_np, ws, bs = _problem(dims, batch)
     eager = _mlp(rsl, ws, bs)
     graphed = _mlp(rsl, ws, bs)
     xe, ye = rsl.Variable(x_np), rsl.Variable(y_np)
     xg, yg = rsl.Variable(x_np), rsl.Variable(y_np)
-    step_e = _stepper(rsl, eager, xe, ye)
-    step_g = _stepper(rsl, graphed, xg, yg)
+    step_e = _stepper(rsl, eager, xe, ye, fused_update=fused_update)
+    step_g = _stepper(rsl, graphed, xg, yg, fused_update=fused_update)
 
     # step 1: both eager (compiles every kernel the capture will record)
     l_e, l_g = step_e(), step_g()
@@ -89,6 +94,11 @@ def test_graph_replays_equal_eager_steps(rsl, dims, batch):
     with graph.capture(carry=graphed):
         loss_g = step_g()
     assert graph.captured
+    # a captured update writes the parameters in place: no copy-back buffers
+    held = graph._hold[0]
+    same = [rsl._storage_ptr(p.data) == rsl._storage_ptr(held[n].data)
+            for n, p in graphed.named_parameters()]
+    assert all(same) == fused_update and any(same) == fused_update
 
     scratch = []
     for i in range(6):
