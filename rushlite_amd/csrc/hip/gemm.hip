@@ -10,9 +10,9 @@
 // one MFMA chain per block.  K advances BK = 32 at a time through two LDS
 // buffers with one barrier per K step.  gemm_f32_mfma stages the next tile's
 // global loads in registers and writes them to the other LDS buffer after the
-// current tile's MFMAs; gemm_f32_lds_direct (128 x 128 tiles, operands that
-// allow 128-bit loads) loads straight into LDS and pipelines its fragment
-// reads inside the tile.
+// current tile's MFMAs; gemm_f32_lds (operands that allow 128-bit loads;
+// 128 x 128, 256 x 128 and 256 x 256 tiles) loads straight into LDS and
+// pipelines its fragment reads inside the tile.
 //
 // MFMA operand layout.  For 32x32x2 a lane l supplies A[i][kk] and B[kk][j]
 // with i = j = l % 32 and kk = l / 32.  Within a BK tile, MFMA step s pairs
@@ -481,28 +481,52 @@ void gemm_direct(DirectArgs g) {
 
 // ------------------------------------------------------------- LDS-direct
 //
-// The 128 x 128 tile kernel for operands that allow 128-bit loads.  Panels go
-// from global memory straight into LDS with global_load_lds_dwordx4 (no VGPR
-// staging and no ds_write), two stages deep: the loads of K tile t+1 are issued
-// before the MFMAs of tile t, and one barrier per tile (after every wave's
-// loads have landed and its reads of the old stage are done) hands the stages
-// over.  Within a tile the four 4-step sub-steps are software-pipelined: the
-// LDS fragments of sub-step u+1 are read while the MFMAs of sub-step u run.
-// Tile walk, MFMA step order and epilogue are those of gemm_f32_mfma, so both
-// kernels produce identical bits.
+// Tile kernels for operands that allow 128-bit loads.  Panels go from global
+// memory straight into LDS with global_load_lds_dwordx4 (no VGPR staging and
+// no ds_write) through a STAGES-deep ring with one barrier per K tile: at the
+// top of tile t every wave waits for its own loads of tile t, the barrier
+// makes all of them visible (and retires every wave's reads of the stage about
+// to be refilled), then the loads of tile t + STAGES - 1 are issued.  Within a
+// tile the four 4-step sub-steps are software-pipelined: the LDS fragments of
+// sub-step u+1 are read while the MFMAs of sub-step u run.  Each wave owns
+// TM x TN blocks of 32x32 in a WM x WN grid of waves.  Tile walk, MFMA step
+// order and epilogue are those of gemm_f32_mfma, so every configuration
+// produces the same bits for the same split of K.
 //
 // One DMA instruction fills a contiguous 1 KiB of LDS (lane i -> bytes 16i..),
 // so the LDS layout is chosen by which global float4 each lane fetches:
 //   K-major panel (32 k values contiguous in global: A untransposed, B
-//     transposed), 128 rows x 8 chunks of 4 floats: 16-byte slot p holds row
+//     transposed), R rows x 8 chunks of 4 floats: 16-byte slot p holds row
 //     p / 8, chunk (p % 8) ^ kswz(row).  A lane's fragment read (one row, one
 //     chunk) then spreads 16 consecutive rows over all 64 banks.
-//   N-major panel (128 m or n values contiguous: A transposed, B
-//     untransposed), 32 k-rows x 32 chunks: slot p holds k-row p / 32, chunk
-//     (p % 32) ^ 8 * (k-row / 16).  Lanes 32-63 read k-rows 16 apart from
+//   N-major panel (R m or n values contiguous: A transposed, B untransposed),
+//     32 k-rows x R/4 chunks: slot p holds k-row p / (R/4), chunk
+//     (p % (R/4)) ^ 8 * (k-row / 16).  Lanes 32-63 read k-rows 16 apart from
 //     lanes 0-31; the swizzle moves them to the other half of the banks.
 // Lanes whose element lies outside the matrix fetch the zero page.
-constexpr int kPanel = 128 * kBK;  // floats per operand panel
+//
+// Configurations (measured on MI355X against the register-staged kernel):
+//   LdsSmall  128 x 128, 4 waves, 2 stages, two workgroups per CU
+//   LdsWide   256 x 128, 8 waves, 3 stages (144 KiB), for M >= 512 when
+//             256 x 256 tiles cannot fill the CUs (K split)
+//   LdsBig    256 x 256, 8 waves of 128 x 64, 2 stages (128 KiB), whenever its
+//             tiles cover the CUs: 4096^3 130 -> 139 TFLOP/s
+template <int WM_, int WN_, int TM_, int TN_, int STAGES_, int MINB_>
+struct LdsCfg {
+  static constexpr int WM = WM_, WN = WN_, TM = TM_, TN = TN_;
+  static constexpr int STAGES = STAGES_, MINB = MINB_;
+  static constexpr int NW = WM * WN, THREADS = 64 * NW;
+  static constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
+  static constexpr int A_PANEL = BM * kBK, B_PANEL = BN * kBK;
+  static constexpr int STAGE = A_PANEL + B_PANEL;  // floats
+  static constexpr int A_DMA = BM * 8 / 64 / NW;   // DMA instructions per wave and tile
+  static constexpr int B_DMA = BN * 8 / 64 / NW;
+  static_assert(A_DMA * 64 * NW == BM * 8 && B_DMA * 64 * NW == BN * 8, "panels split evenly");
+  static_assert(BM >= 64 && BN >= 64, "N-major swizzle needs 16 or more chunks per k-row");
+};
+using LdsSmall = LdsCfg<2, 2, 2, 2, 2, 2>;
+using LdsWide = LdsCfg<4, 2, 2, 2, 3, 1>;
+using LdsBig = LdsCfg<2, 4, 4, 2, 2, 1>;
 
 __device__ __forceinline__ int kswz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
@@ -513,16 +537,22 @@ __device__ __forceinline__ void lds_dma16(const float* src, float* lds) {
   __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
 }
 
-template <bool TA, bool TB>
-__global__ __launch_bounds__(kThreads, 2) void gemm_f32_lds_direct(GemmArgs g) {
-  using C = CfgLarge;
-  constexpr int BM = C::BM, BN = C::BN;
+// Wait until at most N of this wave's vector-memory loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  else static_assert(N < 0, "add the count used by a new configuration");
+}
+
+template <int NT, int MINB, class C, bool TA, bool TB>
+__global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
+  constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN, S = C::STAGES;
   constexpr int HK = kBK / 2;
   constexpr int SU = 4;           // MFMA steps per sub-step
   constexpr int NU = HK / SU;     // sub-steps per K tile
-  constexpr int STAGE = 2 * kPanel;
-  static_assert(BM == 128 && BN == 128 && NU % 2 == 0, "layout assumes 128 x 128 tiles");
-  __shared__ __attribute__((aligned(1024))) float smem[2 * STAGE];
+  constexpr int DPT = C::A_DMA + C::B_DMA;
+  __shared__ __attribute__((aligned(1024))) float smem[S * C::STAGE];
 
   const int ntiles = g.tiles_m * g.tiles_n;
   int bid = blockIdx.x;
@@ -544,7 +574,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_lds_direct(GemmArgs g) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / C::WGN, wn = wave % C::WGN;
+  const int wm = wave / C::WN, wn = wave % C::WN;
   const int li = lane & 31, lh = lane >> 5;
 
   // The zero page's address, materialised once outside the loop.
@@ -552,32 +582,37 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_lds_direct(GemmArgs g) {
   asm volatile("" : "+s"(zero_bits));
   const float* zero = reinterpret_cast<const float*>(zero_bits);
 
-  // Each wave issues four DMA instructions per operand and K tile.  Per
-  // instruction q: the lane's fixed coordinate along m (or n), its k offset
-  // inside the tile, and its element offset without the tile's k0.
-  int a_mn[4], a_k[4], b_mn[4], b_k[4];
-  int64_t a_off[4], b_off[4];
+  // Per DMA instruction: the lane's fixed coordinate along m (or n), its k
+  // offset inside the tile, and its element offset without the tile's k0.
+  int a_mn[C::A_DMA], a_k[C::A_DMA], b_mn[C::B_DMA], b_k[C::B_DMA];
+  int64_t a_off[C::A_DMA], b_off[C::B_DMA];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int p = (wave * 4 + q) * 64 + lane;
+  for (int q = 0; q < C::A_DMA; ++q) {
+    const int p = (wave * C::A_DMA + q) * 64 + lane;
     if constexpr (!TA) {
       const int r = p >> 3, c = (p & 7) ^ kswz(p >> 3);
       a_mn[q] = m0 + r;
       a_k[q] = 4 * c;
       a_off[q] = int64_t(m0 + r) * g.lda + 4 * c;
     } else {
-      const int kr = p >> 5, c = (p & 31) ^ ((kr >> 4) << 3);
+      constexpr int CH = BM / 4;
+      const int kr = p / CH, c = (p % CH) ^ ((kr >> 4) << 3);
       a_mn[q] = m0 + 4 * c;
       a_k[q] = kr;
       a_off[q] = int64_t(kr) * g.lda + m0 + 4 * c;
     }
+  }
+#pragma unroll
+  for (int q = 0; q < C::B_DMA; ++q) {
+    const int p = (wave * C::B_DMA + q) * 64 + lane;
     if constexpr (TB) {
       const int r = p >> 3, c = (p & 7) ^ kswz(p >> 3);
       b_mn[q] = n0 + r;
       b_k[q] = 4 * c;
       b_off[q] = int64_t(n0 + r) * g.ldb + 4 * c;
     } else {
-      const int kr = p >> 5, c = (p & 31) ^ ((kr >> 4) << 3);
+      constexpr int CH = BN / 4;
+      const int kr = p / CH, c = (p % CH) ^ ((kr >> 4) << 3);
       b_mn[q] = n0 + 4 * c;
       b_k[q] = kr;
       b_off[q] = int64_t(kr) * g.ldb + n0 + 4 * c;
@@ -585,29 +620,29 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_lds_direct(GemmArgs g) {
   }
   auto issue = [&](int kt, int stage) {
     const int k0 = kt * kBK;
-    float* sa = smem + stage * STAGE;
-    float* sb = sa + kPanel;
+    float* sa = smem + stage * C::STAGE;
+    float* sb = sa + C::A_PANEL;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < C::A_DMA; ++q) {
       const bool ok = a_mn[q] < g.m && k0 + a_k[q] < g.k;
       const float* src = ok ? g.a + a_off[q] + (TA ? int64_t(k0) * g.lda : k0) : zero;
-      lds_dma16(src, sa + (wave * 4 + q) * 256);
+      lds_dma16(src, sa + (wave * C::A_DMA + q) * 256);
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < C::B_DMA; ++q) {
       const bool ok = b_mn[q] < g.n && k0 + b_k[q] < g.k;
       const float* src = ok ? g.b + b_off[q] + (TB ? k0 : int64_t(k0) * g.ldb) : zero;
-      lds_dma16(src, sb + (wave * 4 + q) * 256);
+      lds_dma16(src, sb + (wave * C::B_DMA + q) * 256);
     }
   };
   // MFMA operands of sub-step u (steps SU*u .. SU*u+3 of the tile): step s
   // reads k = s + HK*lh, as in gemm_f32_mfma.
-  auto read_frag = [&](int stage, int u, float (&fa)[C::TM][SU], float (&fb)[C::TN][SU]) {
-    const float* sa = smem + stage * STAGE;
-    const float* sb = sa + kPanel;
+  auto read_frag = [&](int stage, int u, float (&fa)[TM][SU], float (&fb)[TN][SU]) {
+    const float* sa = smem + stage * C::STAGE;
+    const float* sb = sa + C::A_PANEL;
 #pragma unroll
-    for (int i = 0; i < C::TM; ++i) {
-      const int row = (wm * C::TM + i) * 32 + li;
+    for (int i = 0; i < TM; ++i) {
+      const int row = (wm * TM + i) * 32 + li;
       if constexpr (!TA) {
         const int slot = row * 8 + ((lh * 4 + u) ^ kswz(row));
         const v4f t = *reinterpret_cast<const v4f*>(sa + slot * 4);
@@ -619,8 +654,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_lds_direct(GemmArgs g) {
       }
     }
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
-      const int col = (wn * C::TN + j) * 32 + li;
+    for (int j = 0; j < TN; ++j) {
+      const int col = (wn * TN + j) * 32 + li;
       if constexpr (TB) {
         const int slot = col * 8 + ((lh * 4 + u) ^ kswz(col));
         const v4f t = *reinterpret_cast<const v4f*>(sb + slot * 4);
@@ -633,48 +668,50 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_lds_direct(GemmArgs g) {
     }
   };
 
-  v16f acc[C::TM][C::TN];
+  v16f acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j) acc[i][j] = v16f(0.0f);
-  auto mma = [&](const float (&fa)[C::TM][SU], const float (&fb)[C::TN][SU]) {
+    for (int j = 0; j < TN; ++j) acc[i][j] = v16f(0.0f);
+  auto mma = [&](const float (&fa)[TM][SU], const float (&fb)[TN][SU]) {
 #pragma unroll
     for (int s = 0; s < SU; ++s)
 #pragma unroll
-      for (int i = 0; i < C::TM; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < C::TN; ++j)
+        for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
   };
 
-  float fa0[C::TM][SU], fb0[C::TN][SU], fa1[C::TM][SU], fb1[C::TN][SU];
-  if (kt0 < kt1) {
-    issue(kt0, 0);
-    // The memory clobber keeps the compiler from moving LDS accesses across.
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  }
+  float fa0[TM][SU], fb0[TN][SU], fa1[TM][SU], fb1[TN][SU];
+#pragma unroll
+  for (int t = 0; t < S - 1; ++t)
+    if (kt0 + t < kt1) issue(kt0 + t, t);
   for (int kt = kt0; kt < kt1; ++kt) {
-    const int cur = (kt - kt0) & 1;
-    // The other stage was last read in the previous iteration, before its
-    // closing barrier.
-    if (kt + 1 < kt1) issue(kt + 1, cur ^ 1);
-    read_frag(cur, 0, fa0, fb0);
+    const int rel = kt - kt0;
+    const int stage = rel % S;
+    // Tile kt has landed once at most the later tiles' loads are in flight.
+    if (kt + S - 2 < kt1) wait_vmcnt<(S - 2) * DPT>();
+    else wait_vmcnt<0>();
+    // The memory clobber keeps the compiler from moving LDS accesses across.
+    asm volatile("s_barrier" ::: "memory");
+    // The stage refilled here was last read in the previous iteration, whose
+    // reads every wave retired before this barrier.
+    if (kt + S - 1 < kt1) issue(kt + S - 1, (rel + S - 1) % S);
+    read_frag(stage, 0, fa0, fb0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
       if (u + 1 < NU) {
-        if (u % 2 == 0) read_frag(cur, u + 1, fa1, fb1);
-        else read_frag(cur, u + 1, fa0, fb0);
+        if (u % 2 == 0) read_frag(stage, u + 1, fa1, fb1);
+        else read_frag(stage, u + 1, fa0, fb0);
       }
       __builtin_amdgcn_sched_barrier(0);
       if (u % 2 == 0) mma(fa0, fb0);
       else mma(fa1, fb1);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // Next tile's panels landed (vmcnt) and this stage's reads are done
-    // (lgkmcnt) in every wave before anyone moves on.
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
 
   const bool partial = gridDim.z > 1;
@@ -685,13 +722,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_lds_direct(GemmArgs g) {
     ld = g.n;
   }
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i) {
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
-      const int col = n0 + (wn * C::TN + j) * 32 + li;
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + (wn * TN + j) * 32 + li;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + (wm * C::TM + i) * 32 + (r / 4) * 8 + lh * 4 + (r % 4);
+        const int row = m0 + (wm * TM + i) * 32 + (r / 4) * 8 + lh * 4 + (r % 4);
         if (row < g.m && col < g.n) {
           float* p = out + int64_t(row) * ld + col;
           const float v = acc[i][j][r];
@@ -734,8 +771,8 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
   }
   const dim3 grid{uint32_t(tiles), 1u, uint32_t(splits)};
   if (vec && std::is_same_v<C, CfgLarge>)
-    hipLaunchKernelGGL((gemm_f32_lds_direct<TA, TB>), grid, dim3(kThreads), 0,
-                       rt->stream, g);
+    hipLaunchKernelGGL((gemm_f32_lds<LdsSmall::THREADS, LdsSmall::MINB, LdsSmall, TA, TB>), grid,
+                       dim3(LdsSmall::THREADS), 0, rt->stream, g);
   else if (vec)
     hipLaunchKernelGGL((gemm_f32_mfma<C, TA, TB, true>), grid, dim3(kThreads), 0,
                        rt->stream, g);
@@ -743,6 +780,40 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
     hipLaunchKernelGGL((gemm_f32_mfma<C, TA, TB, false>), grid, dim3(kThreads), 0,
                        rt->stream, g);
   LMP_LAUNCH_CHECK("gemm_f32_mfma");
+  if (splits > 1) {
+    const int64_t mn = int64_t(g.m) * g.n;
+    hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
+                       rt->stream, final_c, part, g.m, g.n, g.ldc, splits,
+                       g.accumulate);
+    LMP_LAUNCH_CHECK("fold_splits");
+    scratch_free(part);
+  }
+  return LMP_OK;
+}
+
+// One of the one-workgroup-per-CU LDS configurations: K split so the tiles
+// cover the CUs once, keeping at least eight K tiles per split.
+template <class L, bool TA, bool TB>
+int launch_lds(Runtime* rt, GemmArgs g) {
+  g.tiles_m = (g.m + L::BM - 1) / L::BM;
+  g.tiles_n = (g.n + L::BN - 1) / L::BN;
+  const int tiles = g.tiles_m * g.tiles_n;
+  const int k_tiles = (g.k + kBK - 1) / kBK;
+  int splits = std::max(1, std::min(rt->cu_count / tiles, k_tiles / 8));
+  g.k_tiles_per_split = (k_tiles + splits - 1) / splits;
+  splits = std::max(1, (k_tiles + g.k_tiles_per_split - 1) / g.k_tiles_per_split);
+  float* final_c = g.c;
+  float* part = nullptr;
+  if (splits > 1) {
+    part = static_cast<float*>(
+        scratch_alloc(size_t(splits) * size_t(g.m) * size_t(g.n) * sizeof(float)));
+    if (!part) return LMP_ERR_OOM;
+    g.c = part;
+  }
+  const dim3 grid{uint32_t(tiles), 1u, uint32_t(splits)};
+  hipLaunchKernelGGL((gemm_f32_lds<L::THREADS, L::MINB, L, TA, TB>), grid, dim3(L::THREADS), 0,
+                     rt->stream, g);
+  LMP_LAUNCH_CHECK("gemm_f32_lds");
   if (splits > 1) {
     const int64_t mn = int64_t(g.m) * g.n;
     hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
@@ -807,6 +878,12 @@ template <bool TA, bool TB>
 int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok) {
   if (direct_ok && g.m <= 32) return launch_direct<TA, TB>(rt, g);
   if (g.m <= 64) return launch_gemm_cfg<CfgSkinny, TA, TB>(rt, g, vec);
+  if (vec) {
+    const int64_t big_tiles = int64_t((g.m + LdsBig::BM - 1) / LdsBig::BM) *
+                              ((g.n + LdsBig::BN - 1) / LdsBig::BN);
+    if (big_tiles >= rt->cu_count) return launch_lds<LdsBig, TA, TB>(rt, g);
+    if (g.m >= 512 && g.n >= 2048 && g.k >= 2048) return launch_lds<LdsWide, TA, TB>(rt, g);
+  }
   const int64_t large_tiles = int64_t((g.m + CfgLarge::BM - 1) / CfgLarge::BM) *
                               ((g.n + CfgLarge::BN - 1) / CfgLarge::BN);
   const int64_t small_tiles = int64_t((g.m + CfgSmall::BM - 1) / CfgSmall::BM) *

@@ -203,6 +203,28 @@ def test_gemm_config3_square(hip, oracle):
         assert rel_err(got[rows], want) <= 1e-4, (ta, tb)
 
 
+# Shapes routed to the one-workgroup-per-CU LDS tiles, with ragged edges in
+# m, n and k: (4100, 4036, 100) fills the CUs with 256 x 256 tiles (partial
+# last tile row and column, K not a multiple of 32); (520, 2052, 2080) takes
+# 256 x 128 tiles with K split five ways.
+@pytest.mark.parametrize("m,n,k", [(4100, 4036, 100), (520, 2052, 2080)], ids=str)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_wide_tiles(hip, m, n, k, ta, tb):
+    rng = np.random.default_rng(m + n + k + 2 * ta + tb)
+    a = (rng.standard_normal((m, k)) * 0.1).astype(np.float32)
+    b = (rng.standard_normal((k, n)) * 0.1).astype(np.float32)
+    da = up(hip, a.T.copy() if ta else a)
+    db = up(hip, b.T.copy() if tb else b)
+    rows = np.concatenate([rng.choice(m, 48, replace=False), [0, m - 1]])
+    want = a[rows].astype(np.float64) @ b.astype(np.float64)
+    got = hip.gemm(da, db, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert rel_err(got[rows], want) <= 1e-4
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    dc = up(hip, c0)
+    hip.gemm(da, db, trans_a=bool(ta), trans_b=bool(tb), out=dc, accumulate=True)
+    assert rel_err(dc.numpy()[rows], c0[rows].astype(np.float64) + want) <= 1e-4
+
+
 def test_transpose(hip):
     for shape in ((3, 2), (64, 64), (130, 70), (1, 9)):
         a = np.random.default_rng(0).standard_normal(shape).astype(np.float32)
