@@ -881,7 +881,9 @@ int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok) {
   if (vec) {
     const int64_t big_tiles = int64_t((g.m + LdsBig::BM - 1) / LdsBig::BM) *
                               ((g.n + LdsBig::BN - 1) / LdsBig::BN);
-    if (big_tiles >= rt->cu_count) return launch_lds<LdsBig, TA, TB>(rt, g);
+    // (K of a few tiles leaves the kernel bound by writing C: more, smaller
+    // tiles do better there.)
+    if (big_tiles >= rt->cu_count && g.k >= 256) return launch_lds<LdsBig, TA, TB>(rt, g);
     if (g.m >= 512 && g.n >= 2048 && g.k >= 2048) return launch_lds<LdsWide, TA, TB>(rt, g);
   }
   const int64_t large_tiles = int64_t((g.m + CfgLarge::BM - 1) / CfgLarge::BM) *
