@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define LMP_HIP_ABI_VERSION 3
+#define LMP_HIP_ABI_VERSION 4
 #define LMP_MAX_DIMS 16 /* align_utils.hpp:7 */
 
 typedef enum {
@@ -237,6 +237,15 @@ int lmp_k_reduce(int op, int dtype, void* out, const void* in, size_t outer,
 int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
                    const float* a, size_t lda, const float* b, size_t ldb,
                    float* c, size_t ldc, int accumulate);
+
+/* C = op(A) * op(B) + bias, bias a row vector of n values added to every row
+ * of the finished fp32 product (after any split-K fold): one pass instead of
+ * the reference's matmul followed by a broadcast add (LinearImpl::forward,
+ * layers/linear.cpp:21-26; linear.py:31-34).  Same rounding as the two-step
+ * form: the product is complete before the bias is added. */
+int lmp_k_linear_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
+                     const float* a, size_t lda, const float* b, size_t ldb,
+                     const float* bias, float* c, size_t ldc);
 
 /* The same product for any dtype, operands and C all of `dtype`
  * (LMP_FLOAT32 is lmp_k_gemm_f32).  float64 accumulates on the f64 matrix

@@ -350,6 +350,9 @@ PYBIND11_MODULE(_C, m) {
     m.def(name, fn, py::arg("a"));
   m.def("clamp", &ag::ops::clamp, py::arg("a"), py::arg("min"), py::arg("max"));
   m.def("matmul", &ag::ops::matmul, py::arg("a"), py::arg("b"));
+  m.def("linear", &ag::ops::linear, py::arg("x"), py::arg("w"), py::arg("b"),
+        "x @ w + b in one GEMM (the bias added in its epilogue); the same values as "
+        "matmul followed by the broadcast add.");
   m.def("sum", &ag::ops::sum, py::arg("a"), py::arg("axis"));
   m.def("max", &ag::ops::max, py::arg("a"), py::arg("axis"));
   m.def("min", &ag::ops::min, py::arg("a"), py::arg("axis"));

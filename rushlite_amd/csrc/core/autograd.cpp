@@ -320,6 +320,18 @@ Variable matmul(const Variable& a, const Variable& b) {
                 });
 }
 
+// x @ w + b as one node: the gradients of the reference's AddBackward (bias
+// branch, functions/expand_ops.cpp:15-40) and MatrixMultiplicationBackward
+// (functions/matrix_ops.cpp:8-35), in that order.
+Variable linear(const Variable& x, const Variable& w, const Variable& b) {
+  return record(tops::linear(x.data(), w.data(), b.data()), {x, w, b}, "LinearBackward",
+                [](LMP_BW_ARGS) {
+                  if (in[2].requires_grad()) in[2].incr_grad(sba(G, in[2]));
+                  if (in[0].requires_grad()) in[0].incr_grad_matmul(G, in[1].data(), false, true);
+                  if (in[1].requires_grad()) in[1].incr_grad_matmul(in[0].data(), G, true, false);
+                });
+}
+
 Variable transpose(const Variable& a) {
   return record(tops::transpose(a.data()), {a}, "TransposeBackward", [](LMP_BW_ARGS) {
     if (SELF.requires_grad()) SELF.incr_grad(tops::transpose(G));

@@ -300,6 +300,22 @@ void matmul_acc_hip(TensorImpl& c, const TensorImpl& a, const TensorImpl& b, boo
   gemm_into(c.data(), dt, a, b, ta, tb, s, true);
 }
 
+TensorImpl linear_hip(const TensorImpl& x, const TensorImpl& w, const TensorImpl& b) {
+  const GemmShape s = gemm_shape(x, w, false, false);
+  Storage out(s.m * s.n * sizeof(float), DeviceType::HIP);
+  if (s.m && s.n) {
+    const void* px = mut(x);
+    const void* pw = mut(w);
+    const void* pb = mut(b);
+    count_launch();
+    hip_ok(lmp_k_linear_f32(0, 0, s.m, s.n, s.k, static_cast<const float*>(px), s.k,
+                            static_cast<const float*>(pw), s.n, static_cast<const float*>(pb),
+                            static_cast<float*>(out.data()), s.n),
+           "lmp_k_linear_f32");
+  }
+  return TensorImpl(out, {s.m, s.n}, DataType::Float32);
+}
+
 TensorImpl transpose_hip(const TensorImpl& a) {
   LMP_CHECK(a.shape().size() == 2)
       << "Invalid argument, transpose can only be performed on matrices of dim 2";
@@ -375,6 +391,7 @@ LMP_REGISTER_DISPATCH(clamp_backward_stub, kHip, clamp_backward_hip)
 LMP_REGISTER_DISPATCH(matmul_stub, kHip, matmul_hip)
 LMP_REGISTER_DISPATCH(matmul_t_stub, kHip, matmul_t_hip)
 LMP_REGISTER_DISPATCH(matmul_acc_stub, kHip, matmul_acc_hip)
+LMP_REGISTER_DISPATCH(linear_stub, kHip, linear_hip)
 LMP_REGISTER_DISPATCH(transpose_stub, kHip, transpose_hip)
 
 }  // namespace lmp::tensor::hip

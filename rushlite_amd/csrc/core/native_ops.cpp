@@ -30,6 +30,7 @@ LMP_DEFINE_DISPATCH(matmul_fn, matmul_stub)
 LMP_DEFINE_DISPATCH(transpose_fn, transpose_stub)
 LMP_DEFINE_DISPATCH(matmul_t_fn, matmul_t_stub)
 LMP_DEFINE_DISPATCH(matmul_acc_fn, matmul_acc_stub)
+LMP_DEFINE_DISPATCH(linear_fn, linear_stub)
 
 namespace {
 using Acc = detail::UnsafeTensorAccessor;
@@ -156,6 +157,19 @@ void matmul_acc(Tensor& c, const Tensor& a, const Tensor& b, bool trans_a, bool 
   }
   matmul_acc_stub()(c.device(), *Acc::getImpl(c), *Acc::getImpl(a), *Acc::getImpl(b),
                     trans_a, trans_b);
+}
+
+Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b) {
+  LMP_CHECK(x.device() == w.device() && x.device() == b.device())
+      << "Tensors must be on the same device";
+  const bool fused = linear_stub().has(x.device()) && x.type() == DataType::Float32 &&
+                     w.type() == DataType::Float32 && b.type() == DataType::Float32 &&
+                     x.shape().size() == 2 && w.shape().size() == 2 &&
+                     x.shape()[1] == w.shape()[0] &&
+                     (b.shape() == std::vector<size_t>{w.shape()[1]} ||
+                      b.shape() == std::vector<size_t>{1, w.shape()[1]});
+  if (!fused) return add(matmul(x, w), b);
+  return wrap(linear_stub()(x.device(), *Acc::getImpl(x), *Acc::getImpl(w), *Acc::getImpl(b)));
 }
 
 Tensor transpose(const Tensor& a) {

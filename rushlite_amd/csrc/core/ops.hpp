@@ -59,6 +59,12 @@ using matmul_t_fn = TensorImpl (*)(const TensorImpl&, const TensorImpl&, bool,
 // epilogue adds the finished fp32 product to C once).
 using matmul_acc_fn = void (*)(TensorImpl& c, const TensorImpl&, const TensorImpl&,
                                bool, bool);
+// x @ w + b with the bias added in the GEMM epilogue; the reference spells it
+// matmul then broadcast add (LinearImpl::forward, layers/linear.cpp:21-26),
+// with the same rounding.  Called only for float32 operands, a 2-D x and w,
+// and a bias of w's column count.
+using linear_fn = TensorImpl (*)(const TensorImpl& x, const TensorImpl& w,
+                                 const TensorImpl& b);
 
 #define LMP_FOR_BINARY_OPS(_) \
   _(add) _(sub) _(mul) _(div) _(pow) _(eq) _(ne) _(ge) _(le) _(gt) _(lt)
@@ -89,6 +95,7 @@ LMP_DECLARE_DISPATCH(matmul_fn, matmul_stub)
 LMP_DECLARE_DISPATCH(transpose_fn, transpose_stub)
 LMP_DECLARE_DISPATCH(matmul_t_fn, matmul_t_stub)
 LMP_DECLARE_DISPATCH(matmul_acc_fn, matmul_acc_stub)
+LMP_DECLARE_DISPATCH(linear_fn, linear_stub)
 
 Tensor clamp(const Tensor& a, Scalar lo, Scalar hi);
 Tensor abs_backward(const Tensor& input, const Tensor& grad);
@@ -98,6 +105,8 @@ Tensor matmul(const Tensor& a, const Tensor& b);
 Tensor matmul_t(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b);
 // c += op(a) @ op(b) in place (shapes must match exactly).
 void matmul_acc(Tensor& c, const Tensor& a, const Tensor& b, bool trans_a, bool trans_b);
+// x @ w + b (Linear's forward); one fused GEMM where the backend has one.
+Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b);
 Tensor transpose(const Tensor& a);
 Tensor reshape(const Tensor& a, std::vector<size_t> shape);
 Tensor squeeze(const Tensor& a, size_t dim);

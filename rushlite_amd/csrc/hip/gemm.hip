@@ -77,7 +77,8 @@ struct GemmArgs {
   int lda, ldb, ldc;
   int tiles_m, tiles_n;
   int k_tiles_per_split;
-  int accumulate;  // only honoured when writing the final output
+  int accumulate;      // only honoured when writing the final output
+  const float* bias;   // per-column bias added to the final output (or null)
 };
 
 // Load one [rows x cols] panel of a row-major matrix (leading dim ld) starting
@@ -266,6 +267,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma(GemmArgs g) {
           float* p = out + int64_t(row) * ld + col;
           const float v = acc[i][j][r];
           if (!partial && g.accumulate) *p = *p + v;
+          else if (!partial && g.bias) *p = v + g.bias[col];
           else *p = v;
         }
       }
@@ -277,7 +279,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma(GemmArgs g) {
 __global__ __launch_bounds__(256) void fold_splits(float* __restrict__ c,
                                                    const float* __restrict__ part,
                                                    int m, int n, int ldc,
-                                                   int splits, int accumulate) {
+                                                   int splits, int accumulate,
+                                                   const float* __restrict__ bias) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   const int64_t mn = int64_t(m) * n;
   if (i >= mn) return;
@@ -285,7 +288,8 @@ __global__ __launch_bounds__(256) void fold_splits(float* __restrict__ c,
   float acc = part[i];
   for (int s = 1; s < splits; ++s) acc += part[int64_t(s) * mn + i];
   float* p = c + int64_t(row) * ldc + col;
-  *p = accumulate ? *p + acc : acc;
+  if (accumulate) *p = *p + acc;
+  else *p = bias ? acc + bias[col] : acc;
 }
 
 // ------------------------------------------------------------------ direct
@@ -317,6 +321,7 @@ struct DirectArgs {
   int n_blocks;    // ceil(n / 128)
   int k_per_wg;    // K range of one workgroup (a multiple of 32)
   int accumulate;  // only honoured when writing the final output
+  const float* bias;  // per-column bias added to the final output (or null)
 };
 
 constexpr int kDirectN = 128;
@@ -426,6 +431,7 @@ void gemm_direct(DirectArgs g) {
   float* out = partial ? g.c + int64_t(blockIdx.y) * g.m * g.n : g.c;
   const int64_t ld = partial ? int64_t(g.n) : int64_t(g.ldc);
   const bool acc_out = !partial && g.accumulate;
+  const float* bias = partial ? nullptr : g.bias;
 
   // Blocks are added over the waves through LDS in rounds of BPR blocks
   // (32 KiB), laid out [wave][block][r][lane] so writes and reads are
@@ -467,13 +473,18 @@ void gemm_direct(DirectArgs g) {
       const int col = n0 + 4 * (ln & 31);
       if (col < g.n) {
         v4f* o = reinterpret_cast<v4f*>(base + col);
-        *o = acc_out ? *o + v[u] : v[u];
+        if (acc_out) *o = *o + v[u];
+        else if (bias) *o = v[u] + *reinterpret_cast<const v4f*>(bias + col);
+        else *o = v[u];
       }
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int col = n0 + 32 * q + (ln & 31);
-        if (col < g.n) base[col] = acc_out ? base[col] + v[u][q] : v[u][q];
+        if (col < g.n) {
+          if (acc_out) base[col] = base[col] + v[u][q];
+          else base[col] = bias ? v[u][q] + bias[col] : v[u][q];
+        }
       }
     }
   }
@@ -733,6 +744,7 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
           float* p = out + int64_t(row) * ld + col;
           const float v = acc[i][j][r];
           if (!partial && g.accumulate) *p = *p + v;
+          else if (!partial && g.bias) *p = v + g.bias[col];
           else *p = v;
         }
       }
@@ -784,7 +796,7 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
     const int64_t mn = int64_t(g.m) * g.n;
     hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
                        rt->stream, final_c, part, g.m, g.n, g.ldc, splits,
-                       g.accumulate);
+                       g.accumulate, g.bias);
     LMP_LAUNCH_CHECK("fold_splits");
     scratch_free(part);
   }
@@ -818,7 +830,7 @@ int launch_lds(Runtime* rt, GemmArgs g) {
     const int64_t mn = int64_t(g.m) * g.n;
     hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
                        rt->stream, final_c, part, g.m, g.n, g.ldc, splits,
-                       g.accumulate);
+                       g.accumulate, g.bias);
     LMP_LAUNCH_CHECK("fold_splits");
     scratch_free(part);
   }
@@ -841,6 +853,7 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
   d.ldb = g0.ldb;
   d.ldc = g0.ldc;
   d.accumulate = g0.accumulate;
+  d.bias = g0.bias;
   d.n_blocks = (g0.n + kDirectN - 1) / kDirectN;
   constexpr int kGrain = 8 * kDirectWaves;
   const int max_splits = std::max(1, g0.k / (64 * kDirectWaves));
@@ -862,7 +875,8 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
   if (splits > 1) {
     const int64_t mn = int64_t(g0.m) * g0.n;
     hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
-                       rt->stream, g0.c, part, g0.m, g0.n, g0.ldc, splits, g0.accumulate);
+                       rt->stream, g0.c, part, g0.m, g0.n, g0.ldc, splits, g0.accumulate,
+                       g0.bias);
     LMP_LAUNCH_CHECK("fold_splits");
     scratch_free(part);
   }
@@ -926,12 +940,15 @@ __global__ __launch_bounds__(256) void transpose_tiled(T* __restrict__ out,
 
 using namespace lmp_hip;
 
-extern "C" int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n,
-                              size_t k, const float* a, size_t lda,
-                              const float* b, size_t ldb, float* c, size_t ldc,
-                              int accumulate) {
+namespace {
+
+int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
+                   const float* a, size_t lda, const float* b, size_t ldb,
+                   const float* bias, float* c, size_t ldc, int accumulate) {
   if (m == 0 || n == 0) return LMP_OK;
   if (!c) return fail(LMP_ERR_INVALID, "gemm: null output");
+  if (k == 0 && bias)
+    return fail(LMP_ERR_UNSUPPORTED, "linear: k == 0");
   if (k == 0) {
     if (accumulate) return LMP_OK;
     if (ldc != n) return fail(LMP_ERR_UNSUPPORTED, "gemm: k == 0 with ldc != n");
@@ -955,6 +972,7 @@ extern "C" int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n,
   g.ldb = int(ldb);
   g.ldc = int(ldc);
   g.accumulate = accumulate ? 1 : 0;
+  g.bias = bias;
   // 128-bit panel loads need 16-byte rows and a contiguous extent that is a
   // multiple of four.
   const size_t a_contig = trans_a ? m : k;
@@ -962,11 +980,31 @@ extern "C" int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n,
   const bool vec = lda % 4 == 0 && ldb % 4 == 0 && a_contig % 4 == 0 &&
                    b_contig % 4 == 0 && aligned16(a) && aligned16(b);
   // The direct kernel's float4 C stores (trans_b == 0) need 16-byte C rows.
-  const bool direct_ok = vec && (trans_b || (ldc % 4 == 0 && aligned16(c)));
+  // (and a float4 bias read when there is a bias).
+  const bool direct_ok =
+      vec && (trans_b || (ldc % 4 == 0 && aligned16(c) && (!bias || aligned16(bias))));
   if (!trans_a && !trans_b) return launch_gemm<false, false>(rt, g, vec, direct_ok);
   if (!trans_a && trans_b) return launch_gemm<false, true>(rt, g, vec, direct_ok);
   if (trans_a && !trans_b) return launch_gemm<true, false>(rt, g, vec, direct_ok);
   return launch_gemm<true, true>(rt, g, vec, direct_ok);
+}
+
+}  // namespace
+
+extern "C" int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n,
+                              size_t k, const float* a, size_t lda,
+                              const float* b, size_t ldb, float* c, size_t ldc,
+                              int accumulate) {
+  return gemm_f32_entry(trans_a, trans_b, m, n, k, a, lda, b, ldb, nullptr, c, ldc,
+                        accumulate);
+}
+
+extern "C" int lmp_k_linear_f32(int trans_a, int trans_b, size_t m, size_t n,
+                                size_t k, const float* a, size_t lda,
+                                const float* b, size_t ldb, const float* bias,
+                                float* c, size_t ldc) {
+  if (!bias) return fail(LMP_ERR_INVALID, "linear: null bias");
+  return gemm_f32_entry(trans_a, trans_b, m, n, k, a, lda, b, ldb, bias, c, ldc, 0);
 }
 
 extern "C" int lmp_k_transpose(int dtype, void* out, const void* in, size_t m,

@@ -577,3 +577,27 @@ def test_loss_row_chain_fuses(rsl):
     got = r.numpy()
     assert rsl._stats()["fused_launches"] - s0["fused_launches"] == 1
     assert np.array_equal(got.view(np.uint32), eager.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,k,n", [(32, 256, 64), (20, 70, 10), (512, 2048, 2048), (64, 130, 33)],
+                         ids=str)
+def test_linear_op_matches_matmul_plus_bias(rsl, m, k, n):
+    """rsl.linear (Linear's forward: one GEMM with the bias in its epilogue)
+    gives the values and gradients of matmul followed by the broadcast add,
+    bit for bit."""
+    rng = np.random.default_rng(m * k + n)
+    x_np = rng.standard_normal((m, k)).astype(np.float32)
+    w_np = rng.standard_normal((k, n)).astype(np.float32)
+    b_np = rng.standard_normal(n).astype(np.float32)
+    outs, grads = [], []
+    for fused in (True, False):
+        x = rsl.Variable(x_np, requires_grad=True)
+        w = rsl.Variable(w_np, requires_grad=True)
+        b = rsl.Variable(b_np, requires_grad=True)
+        y = rsl.linear(x, w, b) if fused else rsl.matmul(x, w) + b
+        (rsl.exp(y * 0.01) * 2.0).sum(1).sum(0).backward()
+        outs.append(y.numpy())
+        grads.append([x.grad.numpy(), w.grad.numpy(), b.grad.numpy()])
+    assert np.array_equal(outs[0], outs[1])
+    for g0, g1 in zip(*grads):
+        assert np.array_equal(g0, g1)

@@ -267,3 +267,28 @@ def test_errors_are_reported(hip):
         == hip.ERR_INVALID
     assert b"unknown op" in L.lmp_rt_last_error()
     assert L.lmp_rt_free(C.c_void_p(0xdead00)) == hip.ERR_INVALID
+
+
+# lmp_k_linear_f32: the bias rides in every GEMM path's epilogue (register-
+# direct M <= 32, skinny M <= 64, the scalar-load kernel for odd strides, the
+# split-K fold, the 128/256-wide LDS tiles), so C must equal the plain GEMM
+# followed by a float32 bias add, bit for bit.
+LINEAR_SHAPES = [(32, 64, 256), (20, 132, 1028), (48, 96, 64), (200, 130, 70),
+                 (256, 1000, 128), (512, 2048, 2048), (4096, 4096, 256)]
+
+
+@pytest.mark.parametrize("m,n,k", LINEAR_SHAPES, ids=str)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_linear_bias_epilogue_equals_gemm_then_add(hip, m, n, k, ta, tb):
+    rng = np.random.default_rng(m + 3 * n + 7 * k + ta + 2 * tb)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    da = up(hip, a.T.copy() if ta else a)
+    db = up(hip, b.T.copy() if tb else b)
+    dbias = up(hip, bias)
+    plain = hip.gemm(da, db, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    out = hip.DeviceBuffer((m, n), np.float32)
+    hip.check(hip.lib().lmp_k_linear_f32(ta, tb, m, n, k, da.ptr, da.shape[1], db.ptr,
+                                         db.shape[1], dbias.ptr, out.ptr, n))
+    assert np.array_equal(out.numpy(), plain + bias[None, :])
