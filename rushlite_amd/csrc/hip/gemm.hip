@@ -79,6 +79,7 @@ struct GemmArgs {
   int k_tiles_per_split;
   int accumulate;      // only honoured when writing the final output
   const float* bias;   // per-column bias added to the final output (or null)
+  int vec_out;         // C (and the bias) take 128-bit stores: n, ldc % 4 == 0, 16-byte aligned
 };
 
 // Load one [rows x cols] panel of a row-major matrix (leading dim ld) starting
@@ -732,6 +733,42 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
     out = g.c + int64_t(split) * g.m * g.n;
     ld = g.n;
   }
+  const float* bias = partial ? nullptr : g.bias;
+  const bool acc_out = !partial && g.accumulate;
+  if (g.vec_out) {
+    // Rows of C as 128-bit stores: each 32x32 block goes through a wave-private
+    // 32 x 36 LDS tile (rows padded to keep float4 alignment) so a lane holds
+    // four consecutive columns of one row.  LDS requests of one wave complete
+    // in order, so the wave's own writes are visible to its reads.
+    asm volatile("s_barrier" ::: "memory");  // every wave is done with the stages
+    float* tile = smem + wave * (32 * 36);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          tile[((r / 4) * 8 + lh * 4 + (r % 4)) * 36 + li] = acc[i][j][r];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int row0 = m0 + (wm * TM + i) * 32, col0 = n0 + (wn * TN + j) * 32;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int idx = lane + 64 * t;
+          const int rr = idx >> 3, cc = (idx & 7) * 4;
+          const v4f v = *reinterpret_cast<const v4f*>(tile + rr * 36 + cc);
+          const int row = row0 + rr, col = col0 + cc;
+          if (row < g.m && col < g.n) {
+            v4f* p = reinterpret_cast<v4f*>(out + int64_t(row) * ld + col);
+            if (acc_out) *p = *p + v;
+            else if (bias) *p = v + *reinterpret_cast<const v4f*>(bias + col);
+            else *p = v;
+          }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -743,8 +780,8 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
         if (row < g.m && col < g.n) {
           float* p = out + int64_t(row) * ld + col;
           const float v = acc[i][j][r];
-          if (!partial && g.accumulate) *p = *p + v;
-          else if (!partial && g.bias) *p = v + g.bias[col];
+          if (acc_out) *p = *p + v;
+          else if (bias) *p = v + bias[col];
           else *p = v;
         }
       }
@@ -973,6 +1010,7 @@ int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
   g.ldc = int(ldc);
   g.accumulate = accumulate ? 1 : 0;
   g.bias = bias;
+  g.vec_out = n % 4 == 0 && ldc % 4 == 0 && aligned16(c) && (!bias || aligned16(bias));
   // 128-bit panel loads need 16-byte rows and a contiguous extent that is a
   // multiple of four.
   const size_t a_contig = trans_a ? m : k;
