@@ -285,10 +285,12 @@ def mlp_bench(rsl, abi, dims, batch, steps, onehot, graph=False, fused_update=Fa
 
     def step():
         probs = forward(x)
-        loss = (-y * rsl.log(probs + 1e-3)).sum(1).sum(0)
+        # with fused_update the loss and the SGD update are captured as well
+        # (the reference README captures the forward only): the loss rows
+        # become one fused row kernel, p - lr*g one kernel per parameter
+        with rsl.capture_on(fused_update):
+            loss = (-y * rsl.log(probs + 1e-3)).sum(1).sum(0)
         loss.backward()
-        # SGD as the reference README writes it; with fused_update the same
-        # expression is captured, so p - lr*g is one fused kernel per parameter
         with rsl.capture_on(fused_update):
             for name, p in list(model.named_parameters()):
                 model.params[name] = rsl.Variable(p.data - 1e-3 * p.grad, requires_grad=True)

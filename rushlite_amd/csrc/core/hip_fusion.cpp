@@ -319,6 +319,7 @@ std::vector<int64_t> signature(const Region& r, const std::vector<size_t>& shape
       s.push_back(bound_bits(fn->param1(), f64));
     }
     if (fn->kind() == lazy::OpKind::Reduce) s.push_back(static_cast<int64_t>(fn->param0()));
+    if (fn->kind() == lazy::OpKind::Fill) s.push_back(bound_bits(fn->param0(), f64));
     for (const auto& in : fn->inputs) {
       auto it = r.leaf_of.find(in.get());
       s.push_back(it != r.leaf_of.end() ? it->second : -1 - r.node_of.at(in.get()));
@@ -608,6 +609,12 @@ class HipFusionBackend : public lazy::LazyBackend {
       return;
     }
     const Region r = build_region(root);
+    if (r.leaves.empty()) {
+      // Constants only (a fill, or arithmetic on fills): eager.
+      for (const auto& in : root->lazy_op()->inputs) in->data();
+      root->lazy_op()->run_eager(*root);
+      return;
+    }
     realise_leaves(r);
     const bool f64 = root->type() == DataType::Float64;
     const RowPlan rp = row_plan(r);

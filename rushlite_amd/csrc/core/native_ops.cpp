@@ -387,6 +387,33 @@ struct ReduceFn : LazyFunction {
   std::string codegen_expr() const override { return ""; }
 };
 
+// A constant (full_like under capture).  Fused, it is a literal in the
+// generated kernel, so `ones_like(x) * g` costs neither a fill nor its read.
+struct FillFn : LazyFunction {
+  std::vector<size_t> shape;
+  DeviceType dev;
+  DataType dt;
+  Scalar value;
+  FillFn(std::vector<size_t> s, DeviceType d, DataType t, Scalar v)
+      : LazyFunction({}), shape(std::move(s)), dev(d), dt(t), value(v) {}
+  std::shared_ptr<TensorImpl> infer_output() const override {
+    return std::make_shared<TensorImpl>(Storage(0, dev), shape, dt);
+  }
+  bool is_fusible() const override { return true; }
+  OpKind kind() const override { return OpKind::Fill; }
+  int code() const override { return 0; }
+  Scalar param0() const override { return value; }
+  void run_eager(TensorImpl& out) override {
+    Storage st(shape_numel(shape) * dtype_size(dt), dev);
+    if (st.byte_size()) ops::fill_stub()(dev, st.data(), shape_numel(shape), value, dt);
+    out.set_realized(st);
+  }
+  // The value converted to the tensor's type on the host, as the fill does.
+  std::string codegen_expr() const override {
+    return float_literal(value, dt == DataType::Float64);
+  }
+};
+
 }  // namespace
 
 bool is_capture_enabled() { return t_capture; }
@@ -426,6 +453,11 @@ std::shared_ptr<LazyFunction> make_unary(int code, std::shared_ptr<TensorImpl> a
                                          Scalar p0, Scalar p1) {
   return std::make_shared<UnaryFn>(code, std::vector<std::shared_ptr<TensorImpl>>{std::move(a)},
                                    p0, p1);
+}
+
+std::shared_ptr<LazyFunction> make_fill(const std::vector<size_t>& shape, DeviceType device,
+                                        DataType dtype, Scalar value) {
+  return std::make_shared<FillFn>(shape, device, dtype, value);
 }
 
 std::shared_ptr<LazyFunction> make_reduce(int code, std::shared_ptr<TensorImpl> a,

@@ -162,8 +162,10 @@ class CaptureGuard {
 // Op kinds shared by the lazy nodes, the structural graph hash and the code
 // generator; codes equal lmp_binary_op / lmp_unary_op / lmp_reduce_op.
 // Reduce nodes are keep-dims reductions over the last axis, recorded under
-// capture so a region can end in (or pass through) a row reduction.
-enum class OpKind : uint8_t { Binary, Unary, Reduce };
+// capture so a region can end in (or pass through) a row reduction.  Fill
+// nodes are constants (full_like under capture, e.g. the ones of
+// SummationBackward): no inputs, param0() is the value.
+enum class OpKind : uint8_t { Binary, Unary, Reduce, Fill };
 
 // A deferred elementwise node (lazy_function.hpp:11-22).  codegen_expr()
 // returns the node's expression with {0}/{1} for its operands, in the HIP
@@ -201,6 +203,9 @@ std::shared_ptr<LazyFunction> make_unary(int code, std::shared_ptr<TensorImpl> a
 // param0() of a reduce node is its axis.
 std::shared_ptr<LazyFunction> make_reduce(int code, std::shared_ptr<TensorImpl> a,
                                           size_t axis);
+// A float32 / float64 constant of `shape` on `device`.
+std::shared_ptr<LazyFunction> make_fill(const std::vector<size_t>& shape, DeviceType device,
+                                        DataType dtype, Scalar value);
 
 }  // namespace lazy
 

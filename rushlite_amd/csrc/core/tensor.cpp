@@ -263,6 +263,12 @@ Tensor empty(const std::vector<size_t>& shape, DeviceType device, DataType dtype
 }
 
 Tensor full_like(const Tensor& t, Scalar value) {
+  // Under capture a float constant stays pending, so a consumer region can
+  // take it as a literal (fill_like.cpp:8-20 fills eagerly).
+  if (lazy::should_capture(t.device()) &&
+      (t.type() == DataType::Float32 || t.type() == DataType::Float64) && t.numel() > 0)
+    return detail::UnsafeTensorAccessor::fromImpl(
+        lazy::record(lazy::make_fill(t.shape(), t.device(), t.type(), value)));
   Tensor out = empty(t.shape(), t.device(), t.type());
   out.fill(value);
   return out;
