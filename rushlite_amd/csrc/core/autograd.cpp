@@ -80,6 +80,14 @@ void Variable::incr_grad(const Tensor& g) {
   }
   LMP_INTERNAL_ASSERT(g.shape() == impl_->grad.shape())
       << "There should be no broadcasting in incr_grad";
+  // A gradient still pending was started in this backward pass (every
+  // gradient is realised before backward() returns), so nothing outside the
+  // pass holds its storage yet: the sum can stay pending too and fuse with the
+  // pending terms, in the same order as the in-place add.
+  if (tensor::detail::UnsafeTensorAccessor::getImpl(impl_->grad)->is_deferred()) {
+    impl_->grad = tops::add(impl_->grad, g);
+    return;
+  }
   tops::add_inplace(impl_->grad, g);  // variable.cpp:30-35
 }
 
