@@ -5,7 +5,10 @@
 // elementwise nodes of one float type (float32, or float64 on the indexed
 // path); every other input (already realised tensors, and
 // non-fusible or too-distant pending nodes, which are realised first) becomes
-// a leaf, deduplicated by identity so `a*a` loads `a` once.  Unlike the
+// a leaf, deduplicated by identity so `a*a` loads `a` once.  Interior nodes
+// that are also owned elsewhere (autograd keeps every forward value) are
+// stored by the same kernel as extra outputs, so a softmax and its loss, with
+// every value the backward pass reads, is one kernel instead of one per value.  Unlike the
 // reference, operands of different shapes fuse: every leaf is indexed from
 // the root's output index through its right-aligned broadcast strides, so
 // `a*a + b` with b [M,1] and `exp(a)*b - relu(a)/(b+1)` each become a single
@@ -35,6 +38,7 @@ namespace {
 
 constexpr size_t kMaxNodes = 96;
 constexpr size_t kMaxLeaves = 16;
+constexpr size_t kMaxOutputs = 16;  // interior nodes stored beside the root
 constexpr int kBlock = 256;
 
 struct Region {
@@ -43,6 +47,13 @@ struct Region {
   std::unordered_map<TensorImpl*, int> leaf_of;
   std::unordered_map<TensorImpl*, int> node_of;
   std::unordered_map<TensorImpl*, long> owners;  // shared_ptr owners of each input
+  // Interior nodes the kernel also stores (in node order), and their index.
+  std::vector<TensorImpl*> outputs;
+  std::unordered_map<TensorImpl*, int> out_of;
+  // Keeps every node and leaf alive while the region exists: realising a
+  // leaf, or storing an interior node, drops lazy edges that may have been the
+  // only owners of nodes beneath.
+  std::vector<std::shared_ptr<TensorImpl>> hold;
 };
 
 // Regions are homogeneous float32 or float64: a node fuses when it and all
@@ -83,7 +94,10 @@ void grow(TensorImpl* t, Region& r, bool is_root,
     return;
   }
   for (const auto& in : t->lazy_op()->inputs) {
-    r.owners[in.get()] = in.use_count();
+    if (!r.owners.count(in.get())) {
+      r.owners[in.get()] = in.use_count();  // before the region's own hold
+      r.hold.push_back(in);
+    }
     grow(in.get(), r, false, forced);
   }
   r.node_of[t] = static_cast<int>(r.nodes.size());
@@ -173,10 +187,13 @@ RowPlan row_plan(const Region& r) {
   return p;
 }
 
-// Grow the region for `root`, then turn every interior node that something
+// Grow the region for `root` and close it.  An interior node that something
 // outside the region still owns (a variable, a saved input, another pending
-// node) into a leaf, which realises it once as its own region; inlining it
-// would compute it again whenever that other owner is realised.  Interior
+// node) must exist on its own after the kernel; inlining it alone would
+// compute it again whenever that other owner is realised.  It becomes a
+// second output of the same kernel where every lane can store it at its own
+// index (any node of a row kernel; a node of the root's shape otherwise), and
+// a leaf elsewhere, which realises it first as its own region.  Interior
 // reduce nodes that cannot share a row kernel with the rest are made leaves
 // too.  Repeats until the region is closed.
 Region build_region(TensorImpl* root) {
@@ -188,19 +205,39 @@ Region build_region(TensorImpl* root) {
     for (TensorImpl* n : r.nodes)
       for (const auto& in : n->lazy_op()->inputs)
         if (r.node_of.count(in.get())) ++refs[in.get()];
+    std::vector<TensorImpl*> shared;
+    for (TensorImpl* n : r.nodes)
+      if (n != root && r.owners.at(n) > refs[n]) shared.push_back(n);
+    bool has_reduce = false;
+    for (TensorImpl* n : r.nodes) has_reduce |= is_reduce(n);
+    const bool rows = has_reduce && row_plan(r).ok;
     bool changed = false;
-    for (TensorImpl* n : r.nodes) {
-      if (n == root) continue;
-      if (r.owners.at(n) > refs[n]) changed |= forced.insert(n).second;
-    }
-    if (!changed) {
-      bool has_reduce = false;
-      for (TensorImpl* n : r.nodes) has_reduce |= is_reduce(n);
-      if (has_reduce && !row_plan(r).ok)
+    if (!rows) {
+      for (TensorImpl* n : shared)
+        if (n->shape() != root->shape()) changed |= forced.insert(n).second;
+      if (!changed && has_reduce)
         for (TensorImpl* n : r.nodes)
           if (n != root && is_reduce(n)) changed |= forced.insert(n).second;
     }
-    if (!changed) return r;
+    for (size_t k = kMaxOutputs; k < shared.size(); ++k) changed |= forced.insert(shared[k]).second;
+    if (changed) continue;
+    r.outputs = std::move(shared);
+    for (size_t k = 0; k < r.outputs.size(); ++k) r.out_of[r.outputs[k]] = static_cast<int>(k);
+    return r;
+  }
+}
+
+// Build the region for `root` and realise its leaves.  A leaf's own region
+// can reach an interior node of this one that both share, and store it as
+// one of its outputs; the region is then built again with that node as a
+// leaf.
+Region settle_region(TensorImpl* root) {
+  for (;;) {
+    Region r = build_region(root);
+    realise_leaves(r);
+    bool stale = false;
+    for (TensorImpl* n : r.nodes) stale |= !n->is_deferred();
+    if (!stale) return r;
   }
 }
 
@@ -325,6 +362,8 @@ std::vector<int64_t> signature(const Region& r, const std::vector<size_t>& shape
       s.push_back(it != r.leaf_of.end() ? it->second : -1 - r.node_of.at(in.get()));
     }
   }
+  s.push_back(static_cast<int64_t>(r.outputs.size()));
+  for (TensorImpl* n : r.outputs) s.push_back(r.node_of.at(n));
   return s;
 }
 
@@ -368,15 +407,22 @@ __device__ __forceinline__ double lmp_clamp(double x, double lo, double hi) {
 }
 )";
 
+// Kernel signature: the root's output, the interior outputs xo0.., the leaves.
+void emit_params(std::ostringstream& os, const Region& r, const std::string& name,
+                 const char* T) {
+  os << "extern \"C\" __global__ __launch_bounds__(" << kBlock << ") void " << name
+     << "(" << T << "* __restrict__ out";
+  for (size_t k = 0; k < r.outputs.size(); ++k) os << ", " << T << "* __restrict__ xo" << k;
+  for (size_t l = 0; l < r.leaves.size(); ++l)
+    os << ", const " << T << "* __restrict__ in" << l;
+  os << ") {\n";
+}
+
 std::string codegen(const Region& r, const Plan& p, const std::string& name, bool f64) {
   const char* T = f64 ? "double" : "float";
   std::ostringstream os;
   os << kPrelude;
-  os << "extern \"C\" __global__ __launch_bounds__(" << kBlock << ") void " << name
-     << "(" << T << "* __restrict__ out";
-  for (size_t l = 0; l < r.leaves.size(); ++l)
-    os << ", const " << T << "* __restrict__ in" << l;
-  os << ") {\n";
+  emit_params(os, r, name, T);
   const size_t nl = r.leaves.size();
   if (p.vec) {
     // One-shot: workgroup b owns output float4s [256b, 256b + 256).
@@ -400,6 +446,7 @@ std::string codegen(const Region& r, const Plan& p, const std::string& name, boo
            << "ul];\n";
     }
     os << "  lmp_v4 o;\n";
+    for (size_t k = 0; k < r.outputs.size(); ++k) os << "  lmp_v4 x" << k << ";\n";
     const char* comp[4] = {"x", "y", "z", "w"};
     for (int c = 0; c < 4; ++c) {
       os << "  {\n";
@@ -407,8 +454,13 @@ std::string codegen(const Region& r, const Plan& p, const std::string& name, boo
         const bool contig = !p.groups.empty() && p.groups[0].stride[l] == 1;
         return "s" + std::to_string(l) + (contig ? std::string(".") + comp[c] : "");
       });
+      for (size_t k = 0; k < r.outputs.size(); ++k)
+        os << "    x" << k << "." << comp[c] << " = t" << r.node_of.at(r.outputs[k]) << ";\n";
       os << "  }\n";
     }
+    for (size_t k = 0; k < r.outputs.size(); ++k)
+      os << "  __builtin_nontemporal_store(x" << k << ", reinterpret_cast<lmp_v4*>(xo" << k
+         << ") + v);\n";
     os << "  __builtin_nontemporal_store(o, reinterpret_cast<lmp_v4*>(out) + v);\n}\n";
   } else {
     os << "  const unsigned long n = " << p.n << "ul;\n";
@@ -429,6 +481,8 @@ std::string codegen(const Region& r, const Plan& p, const std::string& name, boo
     emit_chain(os, r, "      ", "res", T, [&](int l) {
       return "in" + std::to_string(l) + "[o" + std::to_string(l) + "]";
     });
+    for (size_t k = 0; k < r.outputs.size(); ++k)
+      os << "      xo" << k << "[i] = t" << r.node_of.at(r.outputs[k]) << ";\n";
     os << "    }\n    out[i] = res;\n  }\n}\n";
   }
   return os.str();
@@ -455,10 +509,7 @@ std::string codegen_rows(const Region& r, const RowPlan& rp, const std::string& 
 
   std::ostringstream os;
   os << kPrelude;
-  os << "extern \"C\" __global__ __launch_bounds__(" << kBlock << ") void " << name << "("
-     << T << "* __restrict__ out";
-  for (size_t l = 0; l < r.leaves.size(); ++l) os << ", const " << T << "* __restrict__ in" << l;
-  os << ") {\n";
+  emit_params(os, r, name, T);
   os << "  const unsigned lane = threadIdx.x & 63u;\n";
   os << "  const unsigned long row = (unsigned long)blockIdx.x * " << kBlock / 64
      << "ul + (threadIdx.x >> 6);\n";
@@ -565,23 +616,27 @@ std::string codegen_rows(const Region& r, const RowPlan& rp, const std::string& 
     os << "    v" << m << " = " << P << "v;\n  }\n";
   }
   os << "  // stores\n";
-  const size_t root = r.nodes.size() - 1;
-  if (node_full[root]) {
-    const std::string obase = "out + row * " + std::to_string(rp.N) + "ul";
+  const auto store = [&](size_t m, const std::string& ptr) {
+    if (!node_full[m]) {
+      os << "  if (lane == 0u) " << ptr << "[row] = v" << m << ";\n";
+      return;
+    }
+    const std::string obase = ptr + " + row * " + std::to_string(rp.N) + "ul";
     if (vo) {
       for (int64_t t = 0; t < TT; ++t)
         os << "  if (ok" << t << ") *reinterpret_cast<lmp_v4*>(" << obase << " + 4u * (lane + "
-           << 64 * t << "u)) = lmp_v4{v" << root << "_" << 4 * t << ", v" << root << "_"
-           << 4 * t + 1 << ", v" << root << "_" << 4 * t + 2 << ", v" << root << "_"
+           << 64 * t << "u)) = lmp_v4{v" << m << "_" << 4 * t << ", v" << m << "_"
+           << 4 * t + 1 << ", v" << m << "_" << 4 * t + 2 << ", v" << m << "_"
            << 4 * t + 3 << "};\n";
     } else {
       for (int64_t e = 0; e < E; ++e)
-        os << "  if (ok" << e << ") (" << obase << ")[" << elem_col(e) << "] = v" << root << "_"
+        os << "  if (ok" << e << ") (" << obase << ")[" << elem_col(e) << "] = v" << m << "_"
            << e << ";\n";
     }
-  } else {
-    os << "  if (lane == 0u) out[row] = v" << root << ";\n";
-  }
+  };
+  for (size_t k = 0; k < r.outputs.size(); ++k)
+    store(static_cast<size_t>(r.node_of.at(r.outputs[k])), "xo" + std::to_string(k));
+  store(r.nodes.size() - 1, "out");
   os << "}\n";
   return os.str();
 }
@@ -608,14 +663,13 @@ class HipFusionBackend : public lazy::LazyBackend {
       root->lazy_op()->run_eager(*root);
       return;
     }
-    const Region r = build_region(root);
+    const Region r = settle_region(root);
     if (r.leaves.empty()) {
       // Constants only (a fill, or arithmetic on fills): eager.
       for (const auto& in : root->lazy_op()->inputs) in->data();
       root->lazy_op()->run_eager(*root);
       return;
     }
-    realise_leaves(r);
     const bool f64 = root->type() == DataType::Float64;
     const RowPlan rp = row_plan(r);
     if (is_reduce(root) && !rp.ok) {
@@ -634,7 +688,12 @@ class HipFusionBackend : public lazy::LazyBackend {
         if (leaf->raw() == target->data() && leaf->shape() != shape) in_place = false;
     }
     Storage out = in_place ? *target : Storage(n * dtype_size(root->type()), DeviceType::HIP);
+    std::vector<Storage> extra;
+    extra.reserve(r.outputs.size());
+    for (TensorImpl* x : r.outputs)
+      extra.emplace_back(shape_numel(x->shape()) * dtype_size(x->type()), DeviceType::HIP);
     if (n == 0) {
+      for (size_t k = 0; k < r.outputs.size(); ++k) r.outputs[k]->set_realized(extra[k]);
       root->set_realized(out);
       return;
     }
@@ -658,8 +717,9 @@ class HipFusionBackend : public lazy::LazyBackend {
     uint64_t grid = (work + kBlock - 1) / kBlock;
     grid = std::max<uint64_t>(1, std::min<uint64_t>(grid, uint64_t(1) << 30));
     std::vector<void*> ptrs;
-    ptrs.reserve(r.leaves.size() + 1);
+    ptrs.reserve(r.leaves.size() + r.outputs.size() + 1);
     ptrs.push_back(out.data());
+    for (const Storage& x : extra) ptrs.push_back(x.data());
     for (TensorImpl* leaf : r.leaves) ptrs.push_back(leaf->raw());
     std::vector<void*> args(ptrs.size());
     for (size_t i = 0; i < ptrs.size(); ++i) args[i] = &ptrs[i];
@@ -667,6 +727,7 @@ class HipFusionBackend : public lazy::LazyBackend {
            "lmp_jit_launch");
     ++backend_stats().fused_launches;
     backend_stats().fused_nodes += r.nodes.size();
+    for (size_t k = 0; k < r.outputs.size(); ++k) r.outputs[k]->set_realized(extra[k]);
     root->set_realized(out);
   }
 
@@ -701,8 +762,7 @@ bool realize_into(TensorImpl* root, const Storage& target) {
 
 std::string fused_source_for(TensorImpl* root) {
   LMP_CHECK(root->is_deferred()) << "tensor has no pending graph";
-  const Region r = build_region(root);
-  realise_leaves(r);
+  const Region r = settle_region(root);
   const bool f64 = root->type() == DataType::Float64;
   const RowPlan rp = row_plan(r);
   if (rp.ok) return codegen_rows(r, rp, "lmp_fused", f64);

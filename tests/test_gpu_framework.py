@@ -579,6 +579,118 @@ def test_loss_row_chain_fuses(rsl):
     assert np.array_equal(got.view(np.uint32), eager.view(np.uint32))
 
 
+def _softmax_loss(rsl, z, y):
+    m = rsl.max(z, 1)
+    sh = z - m
+    e = rsl.exp(sh)
+    s = rsl.sum(e, 1)
+    p = e / s
+    q = p + 1e-3
+    lg = rsl.log(q)
+    ny = -y
+    t = ny * lg
+    r = rsl.sum(t, 1)
+    return r, [m, sh, e, s, p, q, lg, ny, t]
+
+
+@pytest.mark.parametrize("shape", [(512, 1000), (32, 10), (7, 333)], ids=str)
+def test_softmax_loss_with_autograd_is_one_kernel(rsl, shape):
+    """With autograd on, every forward value is held by its Variable for the
+    backward pass.  Under capture the whole softmax + loss row chain is still
+    one kernel: the values autograd holds are stored by that kernel as extra
+    outputs.  Every stored value, the loss and the gradient equal the eager
+    ones bit for bit."""
+    rng = np.random.default_rng(shape[1] + 3)
+    z_np = (rng.standard_normal(shape) * 3).astype(np.float32)
+    y_np = rng.random(shape, dtype=np.float32)
+
+    def run(captured):
+        z = rsl.Variable(z_np, requires_grad=True)
+        y = rsl.Variable(y_np)
+        s0 = rsl._stats()
+        with rsl.capture_on(captured):
+            r, vals = _softmax_loss(rsl, z, y)
+        r.realize()
+        s1 = rsl._stats()
+        assert all(not rsl._is_deferred(v) for v in vals)
+        out = [r.numpy()] + [v.numpy() for v in vals]
+        rsl.sum(r, 0).backward()
+        return out, z.grad.numpy(), (s1["fused_launches"] - s0["fused_launches"],
+                                     s1["eager_launches"] - s0["eager_launches"])
+
+    eager, g_eager, _ = run(False)
+    fused, g_fused, (nf, ne) = run(True)
+    assert (nf, ne) == (1, 0)
+    for i, (a, b) in enumerate(zip(fused, eager)):
+        assert a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
+    assert np.array_equal(g_fused.view(np.uint32), g_eager.view(np.uint32))
+
+
+def test_held_interior_value_is_stored_by_the_same_kernel(rsl):
+    """An interior value that something else holds is an extra output of the
+    root's kernel when it has the root's shape, and a separate kernel (a leaf)
+    when it is broadcast, as b + 1 here."""
+    rng = np.random.default_rng(11)
+    a_np = rng.random((300, 128), dtype=np.float32)
+    b_np = rng.random((300, 1), dtype=np.float32)
+    a, b = V(rsl, a_np), V(rsl, b_np)
+    eager = [(a * b), (b + 1.0), (a * b) / (b + 1.0) - a]
+    s0 = rsl._stats()["fused_launches"]
+    with rsl.capture_on():
+        t = a * b
+        u = b + 1.0
+        c = t / u - a
+    c.realize()
+    assert rsl._stats()["fused_launches"] - s0 == 2
+    assert not rsl._is_deferred(t) and not rsl._is_deferred(u)
+    for got, want in zip([t, u, c], eager):
+        assert np.array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32))
+    # float64, indexed path (no float4 plan)
+    a64, b64 = V(rsl, a_np.astype(np.float64)), V(rsl, b_np.astype(np.float64))
+    want = [(a64 * a64), (a64 * a64) * b64 + 1.0]
+    s0 = rsl._stats()["fused_launches"]
+    with rsl.capture_on():
+        t = a64 * a64
+        c = t * b64 + 1.0
+    c.realize()
+    assert rsl._stats()["fused_launches"] - s0 == 1
+    for got, w in zip([t, c], want):
+        assert np.array_equal(got.numpy().view(np.uint64), w.numpy().view(np.uint64))
+
+
+def test_leaf_region_storing_a_shared_node(rsl):
+    """Rows of 4096 are too long for a row kernel, so the row sum L below is a
+    leaf of c's region, and realising it first reaches n, which c's region
+    also holds; c's region is then rebuilt with n as a leaf.  Values equal
+    eager."""
+    rng = np.random.default_rng(12)
+    a_np = rng.standard_normal((4, 4096), dtype=np.float32)
+    a = V(rsl, a_np)
+    n_e = a * 2.0
+    want = [n_e.numpy(), (n_e - rsl.sum(n_e, 1)).numpy()]
+    with rsl.capture_on():
+        n = a * 2.0
+        c = n - rsl.sum(n, 1)
+    got = [n.numpy(), c.numpy()]
+    for g, w in zip(got, want):
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
+    # Here L's own region is a row kernel and stores n as one of its outputs
+    # (the [1, N] node d * 2 keeps c's region off the row path).
+    a_np = rng.standard_normal((64, 200), dtype=np.float32)
+    d_np = rng.standard_normal((1, 200), dtype=np.float32)
+    a, d = V(rsl, a_np), V(rsl, d_np)
+    n_e = a * 2.0
+    want = [n_e.numpy(), ((n_e - rsl.sum(n_e, 1)) * (d * 2.0)).numpy()]
+    s0 = rsl._stats()["fused_launches"]
+    with rsl.capture_on():
+        n = a * 2.0
+        c = (n - rsl.sum(n, 1)) * (d * 2.0)
+    got = [c.numpy(), n.numpy()][::-1]
+    assert rsl._stats()["fused_launches"] - s0 == 2
+    for g, w in zip(got, want):
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
+
+
 @pytest.mark.parametrize("m,k,n", [(32, 256, 64), (20, 70, 10), (512, 2048, 2048), (64, 130, 33)],
                          ids=str)
 def test_linear_op_matches_matmul_plus_bias(rsl, m, k, n):
