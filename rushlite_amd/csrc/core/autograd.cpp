@@ -150,9 +150,12 @@ void Variable::backward() {
       if (node.impl_->grad_fn) node.impl_->grad_fn->apply({node});
   }
   // No pending gradient outlives backward(): later in-place updates of the
-  // tensors a pending gradient reads must not change it.
-  for (Variable& node : topo)
-    if (node.impl_->grad.defined()) node.impl_->grad.realize();
+  // tensors a pending gradient reads must not change it.  Deepest first: the
+  // region of an input's gradient reaches back to the seed and stores the
+  // gradients held on the way as extra outputs, so a chain of pending
+  // gradients is one kernel rather than one per gradient.
+  for (auto it = topo.rbegin(); it != topo.rend(); ++it)
+    if (it->impl_->grad.defined()) it->impl_->grad.realize();
 }
 
 // ------------------------------------------------------------ op recording

@@ -25,6 +25,8 @@
 // extents.  Kernels launch on the library stream without a
 // device synchronisation (the reference synchronises every launch,
 // nvrtc_backend.cpp:135-141).
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <sstream>
@@ -40,6 +42,29 @@ constexpr size_t kMaxNodes = 96;
 constexpr size_t kMaxLeaves = 16;
 constexpr size_t kMaxOutputs = 16;  // interior nodes stored beside the root
 constexpr int kBlock = 256;
+
+// LMP_FUSION_LOG=1 prints one line per fused region (and why nodes were cut
+// out of it) to stderr, to see how a graph splits into kernels.
+bool fusion_log() {
+  static const bool on = [] {
+    const char* v = std::getenv("LMP_FUSION_LOG");
+    return v && *v && *v != '0';
+  }();
+  return on;
+}
+
+std::string shape_text(const std::vector<size_t>& sh) {
+  std::string t = "[";
+  for (size_t i = 0; i < sh.size(); ++i) t += (i ? "," : "") + std::to_string(sh[i]);
+  return t + "]";
+}
+
+void log_cut(const TensorImpl* n, const char* why) {
+  if (fusion_log())
+    std::fprintf(stderr, "[lmp fusion]   cut %s node %s kind %d code %d\n", why,
+                 shape_text(n->shape()).c_str(), static_cast<int>(n->lazy_op()->kind()),
+                 n->lazy_op()->code());
+}
 
 struct Region {
   std::vector<TensorImpl*> leaves;
@@ -90,6 +115,7 @@ void grow(TensorImpl* t, Region& r, bool is_root,
   if (r.node_of.count(t) || r.leaf_of.count(t)) return;
   if (!is_root && (!fusible_node(t) || forced.count(t) || r.nodes.size() >= kMaxNodes ||
                    r.leaves.size() >= kMaxLeaves)) {
+    if (fusible_node(t) && !forced.count(t) && !r.leaf_of.count(t)) log_cut(t, "size limit");
     add_leaf(t, r);
     return;
   }
@@ -112,8 +138,10 @@ bool is_reduce(const TensorImpl* t) {
 //
 // A region holding reduce nodes runs as a row kernel: one wave per row of the
 // reduced shape S = [..., N], each lane holding its share of the row in
-// registers.  Every node is either full (shape S) or a row value (shape S
-// with last dim 1); a reduce node turns a full value into a row value with
+// registers.  Every node is either full (a shape that broadcasts to S with
+// last dim N) or a row value (one that broadcasts to S with last dim 1, e.g.
+// a [1, 1] loss seed), computed for each row; a reduce node turns a full value
+// of shape S into a row value of shape S1 (S with last dim 1) with
 // exactly the order of the eager wave-per-row kernel (row_reduce_wave_f32 for
 // float32 rows with N % 4 == 0, row_reduce_wave otherwise: four interleaved
 // accumulators, their pairwise combination, then a wave butterfly), so a
@@ -130,6 +158,26 @@ struct RowPlan {
   std::vector<bool> full;               // per leaf: varies along the row
   std::vector<int64_t> row_stride;      // per leaf, in elements
 };
+
+// `sh` broadcasts to `S` (right-aligned, each dim equal or 1).
+bool bcast_to(const std::vector<size_t>& sh, const std::vector<size_t>& S) {
+  if (sh.size() > S.size()) return false;
+  for (size_t i = 0; i < sh.size(); ++i) {
+    const size_t d = sh[sh.size() - 1 - i];
+    if (d != 1 && d != S[S.size() - 1 - i]) return false;
+  }
+  return true;
+}
+
+size_t last_dim(const std::vector<size_t>& sh) { return sh.empty() ? 1 : sh.back(); }
+
+// A row kernel can store a node when every row owns its own slot (S or S1)
+// or the node is a single value (stored once, by row 0).
+bool row_storable(const TensorImpl* n, const std::vector<size_t>& S) {
+  std::vector<size_t> S1 = S;
+  S1.back() = 1;
+  return n->shape() == S || n->shape() == S1 || shape_numel(n->shape()) == 1;
+}
 
 RowPlan row_plan(const Region& r) {
   RowPlan p;
@@ -150,7 +198,7 @@ RowPlan row_plan(const Region& r) {
   std::vector<size_t> S1 = p.S;
   S1.back() = 1;
   for (TensorImpl* n : r.nodes) {
-    if (n->shape() != p.S && n->shape() != S1) return p;
+    if (!bcast_to(n->shape(), p.S)) return p;
     if (is_reduce(n)) {
       const auto& fn = n->lazy_op();
       if (fn->inputs[0]->shape() != p.S || n->shape() != S1 ||
@@ -158,7 +206,9 @@ RowPlan row_plan(const Region& r) {
         return p;
     }
   }
-  const bool f32 = r.nodes.back()->type() == DataType::Float32;
+  const TensorImpl* root = r.nodes.back();
+  if (root->shape() != p.S && root->shape() != S1) return p;
+  const bool f32 = root->type() == DataType::Float32;
   p.vec_order = f32 && p.N % 4 == 0;
   p.vec_load = p.vec_order;
   for (TensorImpl* leaf : r.leaves) {
@@ -210,16 +260,26 @@ Region build_region(TensorImpl* root) {
       if (n != root && r.owners.at(n) > refs[n]) shared.push_back(n);
     bool has_reduce = false;
     for (TensorImpl* n : r.nodes) has_reduce |= is_reduce(n);
-    const bool rows = has_reduce && row_plan(r).ok;
+    const RowPlan rp = has_reduce ? row_plan(r) : RowPlan{};
+    const bool rows = rp.ok;
     bool changed = false;
-    if (!rows) {
+    const auto cut = [&](TensorImpl* n, const char* why) {
+      if (forced.insert(n).second) {
+        changed = true;
+        log_cut(n, why);
+      }
+    };
+    if (rows) {
       for (TensorImpl* n : shared)
-        if (n->shape() != root->shape()) changed |= forced.insert(n).second;
+        if (!row_storable(n, rp.S)) cut(n, "held, not storable by rows");
+    } else {
+      for (TensorImpl* n : shared)
+        if (n->shape() != root->shape()) cut(n, "held, not the root's shape");
       if (!changed && has_reduce)
         for (TensorImpl* n : r.nodes)
-          if (n != root && is_reduce(n)) changed |= forced.insert(n).second;
+          if (n != root && is_reduce(n)) cut(n, "reduce outside a row plan");
     }
-    for (size_t k = kMaxOutputs; k < shared.size(); ++k) changed |= forced.insert(shared[k]).second;
+    for (size_t k = kMaxOutputs; k < shared.size(); ++k) cut(shared[k], "held, output limit");
     if (changed) continue;
     r.outputs = std::move(shared);
     for (size_t k = 0; k < r.outputs.size(); ++k) r.out_of[r.outputs[k]] = static_cast<int>(k);
@@ -351,7 +411,10 @@ std::vector<int64_t> signature(const Region& r, const std::vector<size_t>& shape
   for (TensorImpl* n : r.nodes) {
     const auto& fn = n->lazy_op();
     s.push_back(static_cast<int64_t>(fn->kind()) * 256 + fn->code());
-    if (fn->kind() == lazy::OpKind::Unary && fn->code() == LMP_UN_CLAMP) {
+    s.push_back(static_cast<int64_t>(n->shape().size()));
+    for (size_t d : n->shape()) s.push_back(static_cast<int64_t>(d));
+    if ((fn->kind() == lazy::OpKind::Unary && fn->code() == LMP_UN_CLAMP) ||
+        (fn->kind() == lazy::OpKind::Binary && fn->code() == LMP_BIN_CLAMP_BACKWARD)) {
       s.push_back(bound_bits(fn->param0(), f64));
       s.push_back(bound_bits(fn->param1(), f64));
     }
@@ -505,7 +568,7 @@ std::string codegen_rows(const Region& r, const RowPlan& rp, const std::string& 
   const auto ok_of = [&](int64_t e) { return "ok" + std::to_string(vo ? e / 4 : e); };
   std::vector<bool> node_full(r.nodes.size());
   for (size_t m = 0; m < r.nodes.size(); ++m)
-    node_full[m] = !is_reduce(r.nodes[m]) && r.nodes[m]->shape() == rp.S;
+    node_full[m] = !is_reduce(r.nodes[m]) && static_cast<int64_t>(last_dim(r.nodes[m]->shape())) == rp.N;
 
   std::ostringstream os;
   os << kPrelude;
@@ -618,7 +681,10 @@ std::string codegen_rows(const Region& r, const RowPlan& rp, const std::string& 
   os << "  // stores\n";
   const auto store = [&](size_t m, const std::string& ptr) {
     if (!node_full[m]) {
-      os << "  if (lane == 0u) " << ptr << "[row] = v" << m << ";\n";
+      if (shape_numel(r.nodes[m]->shape()) == 1 && rp.R > 1)
+        os << "  if (lane == 0u && row == 0ul) " << ptr << "[0] = v" << m << ";\n";
+      else
+        os << "  if (lane == 0u) " << ptr << "[row] = v" << m << ";\n";
       return;
     }
     const std::string obase = ptr + " + row * " + std::to_string(rp.N) + "ul";
@@ -665,6 +731,8 @@ class HipFusionBackend : public lazy::LazyBackend {
     }
     const Region r = settle_region(root);
     if (r.leaves.empty()) {
+      if (fusion_log())
+        std::fprintf(stderr, "[lmp fusion] eager constants root %s\n", shape_text(root->shape()).c_str());
       // Constants only (a fill, or arithmetic on fills): eager.
       for (const auto& in : root->lazy_op()->inputs) in->data();
       root->lazy_op()->run_eager(*root);
@@ -673,6 +741,8 @@ class HipFusionBackend : public lazy::LazyBackend {
     const bool f64 = root->type() == DataType::Float64;
     const RowPlan rp = row_plan(r);
     if (is_reduce(root) && !rp.ok) {
+      if (fusion_log())
+        std::fprintf(stderr, "[lmp fusion] eager reduce root %s\n", shape_text(root->shape()).c_str());
       // A reduction no row kernel can take (long rows, other layouts): eager.
       for (const auto& in : root->lazy_op()->inputs) in->data();
       root->lazy_op()->run_eager(*root);
@@ -727,6 +797,10 @@ class HipFusionBackend : public lazy::LazyBackend {
            "lmp_jit_launch");
     ++backend_stats().fused_launches;
     backend_stats().fused_nodes += r.nodes.size();
+    if (fusion_log())
+      std::fprintf(stderr, "[lmp fusion] %s root %s nodes %zu leaves %zu outputs %zu\n",
+                   rp.ok ? "rows" : p.vec ? "vec" : "indexed", shape_text(shape).c_str(),
+                   r.nodes.size(), r.leaves.size(), r.outputs.size());
     for (size_t k = 0; k < r.outputs.size(); ++k) r.outputs[k]->set_realized(extra[k]);
     root->set_realized(out);
   }

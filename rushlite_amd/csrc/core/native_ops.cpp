@@ -94,6 +94,9 @@ Tensor abs_backward(const Tensor& input, const Tensor& grad) {
       << "abs_backward requires tensors with identical shapes";
   LMP_CHECK(input.type() == grad.type())
       << "abs_backward requires tensors with identical dtypes";
+  if (lazy::should_capture(input.device()))
+    return Acc::fromImpl(lazy::record(lazy::make_binary(
+        LMP_BIN_ABS_BACKWARD, Acc::getImpl(input), Acc::getImpl(grad))));
   return wrap(abs_backward_stub()(input.device(), *Acc::getImpl(input),
                                   *Acc::getImpl(grad)));
 }
@@ -105,6 +108,9 @@ Tensor clamp_backward(const Tensor& input, const Tensor& grad, Scalar lo, Scalar
       << "clamp_backward requires tensors with identical shapes";
   LMP_CHECK(input.type() == grad.type())
       << "clamp_backward requires tensors with identical dtypes";
+  if (lazy::should_capture(input.device()))
+    return Acc::fromImpl(lazy::record(lazy::make_binary(
+        LMP_BIN_CLAMP_BACKWARD, Acc::getImpl(input), Acc::getImpl(grad), lo, hi)));
   return wrap(clamp_backward_stub()(input.device(), *Acc::getImpl(input),
                                     *Acc::getImpl(grad), lo, hi));
 }
@@ -244,10 +250,13 @@ bool is_f64(const std::vector<std::shared_ptr<TensorImpl>>& ins) {
   return ins[0]->type() == DataType::Float64;
 }
 
+// Also the two backward functors of abs and clamp (input, grad), whose
+// shapes and dtypes the frontends require to be equal.
 struct BinaryFn : LazyFunction {
   int op;
-  BinaryFn(int code, std::vector<std::shared_ptr<TensorImpl>> ins)
-      : LazyFunction(std::move(ins)), op(code) {}
+  Scalar lo, hi;  // clamp backward's bounds
+  BinaryFn(int code, std::vector<std::shared_ptr<TensorImpl>> ins, Scalar p0, Scalar p1)
+      : LazyFunction(std::move(ins)), op(code), lo(p0), hi(p1) {}
   std::shared_ptr<TensorImpl> infer_output() const override {
     OpMeta m = infer_binary(*inputs[0], *inputs[1]);
     return std::make_shared<TensorImpl>(Storage(0, inputs[0]->device()), m.shape,
@@ -258,11 +267,16 @@ struct BinaryFn : LazyFunction {
   bool is_fusible() const override { return true; }
   OpKind kind() const override { return OpKind::Binary; }
   int code() const override { return op; }
+  Scalar param0() const override { return lo; }
+  Scalar param1() const override { return hi; }
   void run_eager(TensorImpl& out) override {
     using namespace ops;
     const DeviceType d = inputs[0]->device();
     TensorImpl r = [&]() -> TensorImpl {
       switch (op) {
+        case LMP_BIN_ABS_BACKWARD: return abs_backward_stub()(d, *inputs[0], *inputs[1]);
+        case LMP_BIN_CLAMP_BACKWARD:
+          return clamp_backward_stub()(d, *inputs[0], *inputs[1], lo, hi);
         case LMP_BIN_ADD: return add_stub()(d, *inputs[0], *inputs[1]);
         case LMP_BIN_SUB: return sub_stub()(d, *inputs[0], *inputs[1]);
         case LMP_BIN_MUL: return mul_stub()(d, *inputs[0], *inputs[1]);
@@ -295,7 +309,14 @@ struct BinaryFn : LazyFunction {
       case LMP_BIN_GE: return cmp(">=");
       case LMP_BIN_LE: return cmp("<=");
       case LMP_BIN_GT: return cmp(">");
-      default: return cmp("<");
+      case LMP_BIN_LT: return cmp("<");
+      // The eager functors: sign(x) * g with 0 at x == 0 (and NaN), and g
+      // strictly inside (lo, hi), 0 elsewhere (and at NaN).
+      case LMP_BIN_ABS_BACKWARD:
+        return "({0} > " + zero + " ? {1} : ({0} < " + zero + " ? (-{1}) : " + zero + "))";
+      default:
+        return "(({0} > " + float_literal(lo, d) + " && {0} < " + float_literal(hi, d) +
+               ") ? {1} : " + zero + ")";
     }
   }
 };
@@ -443,10 +464,11 @@ void realize(TensorImpl* t) {
 }
 
 std::shared_ptr<LazyFunction> make_binary(int code, std::shared_ptr<TensorImpl> a,
-                                          std::shared_ptr<TensorImpl> b) {
+                                          std::shared_ptr<TensorImpl> b, Scalar p0,
+                                          Scalar p1) {
   LMP_CHECK(a->device() == b->device()) << "Tensors are on different devices";
   return std::make_shared<BinaryFn>(
-      code, std::vector<std::shared_ptr<TensorImpl>>{std::move(a), std::move(b)});
+      code, std::vector<std::shared_ptr<TensorImpl>>{std::move(a), std::move(b)}, p0, p1);
 }
 
 std::shared_ptr<LazyFunction> make_unary(int code, std::shared_ptr<TensorImpl> a,

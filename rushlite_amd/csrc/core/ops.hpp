@@ -195,9 +195,11 @@ void register_backend(DeviceType dev, LazyBackend* b);
 std::shared_ptr<TensorImpl> record(std::shared_ptr<LazyFunction> fn);
 void realize(TensorImpl* t);
 
+// p0/p1 are clamp backward's bounds (LMP_BIN_CLAMP_BACKWARD).
 std::shared_ptr<LazyFunction> make_binary(int code,
                                           std::shared_ptr<TensorImpl> a,
-                                          std::shared_ptr<TensorImpl> b);
+                                          std::shared_ptr<TensorImpl> b, Scalar p0 = 0,
+                                          Scalar p1 = 0);
 std::shared_ptr<LazyFunction> make_unary(int code, std::shared_ptr<TensorImpl> a,
                                          Scalar p0 = 0, Scalar p1 = 0);
 // param0() of a reduce node is its axis.

@@ -621,9 +621,58 @@ def test_softmax_loss_with_autograd_is_one_kernel(rsl, shape):
     eager, g_eager, _ = run(False)
     fused, g_fused, (nf, ne) = run(True)
     assert (nf, ne) == (1, 0)
+    # The backward of the row chain, from the [1, 1] seed through both row
+    # sums and the max, is one row kernel too (after the loss's column sum).
+    z = rsl.Variable(z_np, requires_grad=True)
+    y = rsl.Variable(y_np)
+    with rsl.capture_on():
+        r, _ = _softmax_loss(rsl, z, y)
+    loss = rsl.sum(r, 0)
+    s0 = rsl._stats()
+    loss.backward()
+    s1 = rsl._stats()
+    assert (s1["fused_launches"] - s0["fused_launches"], s1["eager_launches"] - s0["eager_launches"]) == (1, 0)
+    assert np.array_equal(z.grad.numpy().view(np.uint32), g_eager.view(np.uint32))
+    assert np.all(loss.grad.numpy() == 1.0)
     for i, (a, b) in enumerate(zip(fused, eager)):
         assert a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
     assert np.array_equal(g_fused.view(np.uint32), g_eager.view(np.uint32))
+
+
+@pytest.mark.parametrize("dt", ["float32", "float64"])
+def test_fused_abs_and_clamp_backward(rsl, dt):
+    """The backward functors of abs and clamp are fusible nodes (the backward
+    pass runs captured): the gradient equals the functors' definition --
+    g strictly inside (lo, hi), sign(x) * g with 0 at x == 0 and at NaN -- bit
+    for bit, at 0, -0, the bounds, infinities and NaN."""
+    rng = np.random.default_rng(21)
+    x_np = rng.standard_normal((96, 130)).astype(dt)
+    flat = x_np.reshape(-1)
+    flat[:8] = [0.0, -0.0, 0.5, -0.5, np.inf, -np.inf, np.nan, 1e-30]
+    g_np = rng.standard_normal((96, 130)).astype(dt)
+    x = rsl.Variable(x_np, dtype=getattr(rsl.dtype, dt), requires_grad=True)
+    g = rsl.Variable(g_np, dtype=getattr(rsl.dtype, dt))
+    y = rsl.clamp(x, -0.5, 0.5) * g + rsl.clamp(x, 0.0, DBL_MAX) * (g * 2.0) + rsl.abs(x) * g
+    rsl.sum(rsl.sum(y, 1), 0).backward()
+    got = x.grad.numpy()
+    zero = np.zeros((), dt)
+    with np.errstate(invalid="ignore"):
+        t1 = np.where((x_np > -0.5) & (x_np < 0.5), g_np, zero)
+        hi = np.array(DBL_MAX if dt == "float64" else np.inf, dt)
+        t2 = np.where((x_np > 0) & (x_np < hi), g_np * np.array(2.0, dt), zero)
+        t3 = np.where(x_np > 0, g_np, np.where(x_np < 0, -g_np, zero))
+    terms = {"c1": t1, "c2": t2, "a": t3}
+    view = np.uint32 if dt == "float32" else np.uint64
+    # Accumulation order of the three terms follows the graph; each term is
+    # exact, so any order of two IEEE adds from +0 is checked by trying all.
+    import itertools
+    ok = False
+    for order in itertools.permutations(terms):
+        acc = zero + terms[order[0]]
+        for k in order[1:]:
+            acc = acc + terms[k]
+        ok |= np.array_equal(acc.view(view), got.view(view))
+    assert ok
 
 
 def test_held_interior_value_is_stored_by_the_same_kernel(rsl):
@@ -675,16 +724,17 @@ def test_leaf_region_storing_a_shared_node(rsl):
     for g, w in zip(got, want):
         assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
     # Here L's own region is a row kernel and stores n as one of its outputs
-    # (the [1, N] node d * 2 keeps c's region off the row path).
-    a_np = rng.standard_normal((64, 200), dtype=np.float32)
-    d_np = rng.standard_normal((1, 200), dtype=np.float32)
+    # (the [2, 1, 200] operand d, whose rows are not evenly spaced in the
+    # [2, 64, 200] row layout, keeps c's region off the row path).
+    a_np = rng.standard_normal((2, 64, 200), dtype=np.float32)
+    d_np = rng.standard_normal((2, 1, 200), dtype=np.float32)
     a, d = V(rsl, a_np), V(rsl, d_np)
     n_e = a * 2.0
-    want = [n_e.numpy(), ((n_e - rsl.sum(n_e, 1)) * (d * 2.0)).numpy()]
+    want = [n_e.numpy(), ((n_e - rsl.sum(n_e, 2)) * d).numpy()]
     s0 = rsl._stats()["fused_launches"]
     with rsl.capture_on():
         n = a * 2.0
-        c = (n - rsl.sum(n, 1)) * (d * 2.0)
+        c = (n - rsl.sum(n, 2)) * d
     got = [c.numpy(), n.numpy()][::-1]
     assert rsl._stats()["fused_launches"] - s0 == 2
     for g, w in zip(got, want):
