@@ -18,8 +18,12 @@
 //   of the reduced axis (8 loads in flight per lane), then combine in LDS in
 //   fixed wave order.  The axis is cut into S chunks so the grid holds about
 //   four workgroups per CU; chunk partials [outer, S, inner] are folded by a
-//   second pass, S float4 loads per lane issued together.  No atomics:
-//   results are deterministic.
+//   second pass, S float4 loads per lane issued together.  An axis of at
+//   most 4096 rows that would need chunks (bias gradients: [batch, out] with
+//   a batch of a few hundred) is reduced in one pass instead: a workgroup
+//   owns a narrow strip of float4 columns and every row, its lanes split into
+//   row groups that combine in LDS, so there is no second launch.  No
+//   atomics: results are deterministic.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -208,6 +212,52 @@ __global__ __launch_bounds__(kBlock) void col_reduce_f32(
   }
 }
 
+// Column reduction in one pass for a short axis.  grid = (ceil(inner4/cw),
+// 1, outer), cw = 1 << cw_log2 float4 columns per workgroup; the 256/cw row
+// groups take rows g, g + 256/cw, ... (eight loads in flight per lane), then
+// fold in LDS by halving in fixed order.  out layout [outer, inner4].
+constexpr uint32_t kStripMaxLen = 4096;
+template <int OP>
+__global__ __launch_bounds__(kBlock) void col_reduce_strip_f32(
+    float* __restrict__ out, const float* __restrict__ in, uint32_t inner4, uint32_t len,
+    uint32_t cw_log2) {
+  using R = Reducer<OP, float>;
+  const uint32_t t = threadIdx.x;
+  const uint32_t cw = 1u << cw_log2, rg = uint32_t(kBlock) >> cw_log2;
+  const uint32_t col = t & (cw - 1), g = t >> cw_log2;
+  const uint32_t c4 = blockIdx.x * cw + col;
+  const uint32_t o = blockIdx.z;
+  const v4f id = v4f(R::identity());
+  v4f acc[kColUnroll];
+#pragma unroll
+  for (int u = 0; u < kColUnroll; ++u) acc[u] = id;
+  if (c4 < inner4) {
+    const v4f* src = reinterpret_cast<const v4f*>(in) + uint64_t(o) * len * inner4 + c4;
+    uint32_t r = g;
+    for (; r + rg * (kColUnroll - 1) < len; r += rg * kColUnroll) {
+      v4f x[kColUnroll];
+#pragma unroll
+      for (int u = 0; u < kColUnroll; ++u) x[u] = src[uint64_t(r + rg * u) * inner4];
+#pragma unroll
+      for (int u = 0; u < kColUnroll; ++u) acc[u] = combine4<OP>(acc[u], x[u]);
+    }
+    for (; r < len; r += rg) acc[0] = combine4<OP>(acc[0], src[uint64_t(r) * inner4]);
+  }
+  v4f a = acc[0];
+#pragma unroll
+  for (int u = 1; u < kColUnroll; ++u) a = combine4<OP>(a, acc[u]);
+  __shared__ v4f lds[kBlock];
+  lds[t] = a;  // row group g, column col
+  for (uint32_t half = rg >> 1; half >= 1; half >>= 1) {
+    __syncthreads();
+    if (g < half) {
+      a = combine4<OP>(a, lds[t + half * cw]);
+      lds[t] = a;
+    }
+  }
+  if (g == 0 && c4 < inner4) reinterpret_cast<v4f*>(out)[uint64_t(o) * inner4 + c4] = a;
+}
+
 // Fold S chunk partials [outer, S, inner4] -> [outer, inner4], float4 lanes,
 // in chunk order with the loads of eight chunks issued before their combines.
 template <int OP>
@@ -346,6 +396,21 @@ int reduce_cols(Runtime* rt, T* out, const T* in, uint64_t outer, uint64_t len,
   if (base < target) S = std::min<uint64_t>((target + base - 1) / base,
                                             std::max<uint64_t>(1, len / 64));
   S = std::min<uint64_t>(S, 65535);
+  if constexpr (std::is_same_v<T, float>) {
+    if (vec && S > 1 && len <= kStripMaxLen) {
+      // One pass: about 128 workgroups where the columns allow, 4..64 float4
+      // columns each.
+      const uint64_t inner4 = inner / 4;
+      uint32_t cw_log2 = 2;
+      while (cw_log2 < 6 && (inner4 >> (cw_log2 + 1)) >= 128) ++cw_log2;
+      const uint64_t gx1 = (inner4 + (1u << cw_log2) - 1) >> cw_log2;
+      const dim3 grid1{uint32_t(gx1), 1u, uint32_t(outer)};
+      hipLaunchKernelGGL((col_reduce_strip_f32<OP>), grid1, dim3(kBlock), 0, rt->stream, out,
+                         in, uint32_t(inner4), uint32_t(len), cw_log2);
+      LMP_LAUNCH_CHECK("col_reduce_strip_f32");
+      return LMP_OK;
+    }
+  }
   const uint64_t chunk = (len + S - 1) / S;
   S = (len + chunk - 1) / chunk;
   T* dst = out;

@@ -119,7 +119,11 @@ REDUCE_CASES = [((300, 257), 0), ((300, 257), 1), ((4, 37, 5), 0), ((4, 37, 5), 
                 ((4, 37, 5), 2), ((64, 16384), 1), ((16, 8192), 1), ((2, 65536), 1),
                 ((2048, 1024), 0), ((512, 4096), 0), ((32, 10), 1), ((32, 10), 0),
                 ((512, 1000), 1), ((3, 2), 0), ((1, 1), 0), ((7, 1, 9), 1),
-                ((5, 3000, 12), 1)]
+                ((5, 3000, 12), 1),
+                # one-pass column strips (axis of at most 4096 rows): ragged
+                # strip, several outer slices, the length limit and one past it
+                ((512, 1000), 0), ((6, 700, 16), 1), ((4096, 64), 0), ((4097, 64), 0),
+                ((100, 4), 0)]
 
 
 @pytest.mark.parametrize("shape,axis", REDUCE_CASES, ids=str)
