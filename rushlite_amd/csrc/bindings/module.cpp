@@ -389,6 +389,8 @@ PYBIND11_MODULE(_C, m) {
     d["fused_nodes"] = s.fused_nodes;
     d["jit_compiles"] = s.jit_compiles;
     d["jit_cache_hits"] = s.jit_cache_hits;
+    d["fused_host_ns"] = s.fused_host_ns;
+    d["gemm_host_ns"] = s.gemm_host_ns;
     lmp_rt_pool_stats ps{};
     if (lmp_rt_pool_stats_get(&ps) == LMP_OK) {
       d["pool_reserved_bytes"] = ps.reserved_bytes;

@@ -262,6 +262,7 @@ GemmShape gemm_shape(const TensorImpl& a, const TensorImpl& b, bool ta, bool tb)
 void gemm_into(void* c, DataType dt, const TensorImpl& a, const TensorImpl& b, bool ta,
                bool tb, const GemmShape& s, bool accumulate) {
   if (!s.m || !s.n) return;
+  HostTimer timer(&backend_stats().gemm_host_ns);
   void *pa = nullptr, *pb = nullptr;
   Storage ka = as_dtype(a, dt, &pa);
   Storage kb = as_dtype(b, dt, &pb);
@@ -304,6 +305,7 @@ TensorImpl linear_hip(const TensorImpl& x, const TensorImpl& w, const TensorImpl
   const GemmShape s = gemm_shape(x, w, false, false);
   Storage out(s.m * s.n * sizeof(float), DeviceType::HIP);
   if (s.m && s.n) {
+    HostTimer timer(&backend_stats().gemm_host_ns);
     const void* px = mut(x);
     const void* pw = mut(w);
     const void* pb = mut(b);

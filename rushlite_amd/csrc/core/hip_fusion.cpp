@@ -279,7 +279,10 @@ Region build_region(TensorImpl* root) {
         for (TensorImpl* n : r.nodes)
           if (n != root && is_reduce(n)) cut(n, "reduce outside a row plan");
     }
-    for (size_t k = kMaxOutputs; k < shared.size(); ++k) cut(shared[k], "held, output limit");
+    // Past the output limit the deepest held nodes become leaves: each of
+    // them realises the part of the graph below it (again storing up to the
+    // limit), so a long chain splits into a few regions, not one per node.
+    for (size_t k = 0; k + kMaxOutputs < shared.size(); ++k) cut(shared[k], "held, output limit");
     if (changed) continue;
     r.outputs = std::move(shared);
     for (size_t k = 0; k < r.outputs.size(); ++k) r.out_of[r.outputs[k]] = static_cast<int>(k);
@@ -367,16 +370,19 @@ Plan make_plan(const Region& r, const std::vector<size_t>& shape, bool f64) {
 
 // ---------------------------------------------------------- signature
 
-uint64_t fnv1a(const std::vector<int64_t>& words) {
-  uint64_t h = 1469598103934665603ull;
+// 64-bit hash of the signature, a word at a time (a multiply-rotate round
+// per word and a final avalanche); a hit is confirmed against the stored
+// signature, so the hash only has to spread keys well.
+uint64_t sig_hash(const std::vector<int64_t>& words) {
+  uint64_t h = 0x243f6a8885a308d3ull ^ words.size();
   for (int64_t w : words) {
-    uint64_t v = static_cast<uint64_t>(w);
-    for (int b = 0; b < 8; ++b) {
-      h ^= (v >> (8 * b)) & 0xff;
-      h *= 1099511628211ull;
-    }
+    uint64_t v = static_cast<uint64_t>(w) * 0x9e3779b97f4a7c15ull;
+    v ^= v >> 32;
+    h = ((h ^ v) << 27 | (h ^ v) >> 37) * 0xbf58476d1ce4e5b9ull;
   }
-  return h;
+  h ^= h >> 31;
+  h *= 0x94d049bb133111ebull;
+  return h ^ (h >> 29);
 }
 
 // A clamp bound as the kernel will see it: float bits, or double bits.
@@ -721,6 +727,18 @@ thread_local const Storage* t_target = nullptr;
 class HipFusionBackend : public lazy::LazyBackend {
  public:
   void realize(TensorImpl* root) override {
+    // Host time of outermost realisations only (nested ones are inside).
+    thread_local int depth = 0;
+    struct Depth {
+      int& d;
+      ~Depth() { --d; }
+    } guard{++depth};
+    HostTimer timer(depth == 1 ? &backend_stats().fused_host_ns : nullptr);
+    realize_region(root);
+  }
+
+ private:
+  void realize_region(TensorImpl* root) {
     const Storage* target = t_target;
     t_target = nullptr;
     if (!root->is_deferred()) return;
@@ -769,7 +787,7 @@ class HipFusionBackend : public lazy::LazyBackend {
     }
     const Plan p = make_plan(r, shape, f64);
     std::vector<int64_t> sig = signature(r, shape, p, f64, rp);
-    const uint64_t key = fnv1a(sig);
+    const uint64_t key = sig_hash(sig);
     void* handle = lookup(key, sig);
     if (!handle) {
       const std::string name = "lmp_fused";

@@ -9,6 +9,7 @@
 // reading their inputs realises any pending graph (tensor_impl.cpp:33-36).
 #pragma once
 
+#include <chrono>
 #include <memory>
 #include <string>
 #include <vector>
@@ -218,7 +219,29 @@ struct BackendStats {
   uint64_t fused_nodes = 0;
   uint64_t jit_compiles = 0;
   uint64_t jit_cache_hits = 0;
+  // Host time spent issuing work (ns): fused regions (region build, kernel
+  // lookup, launch; leaves realised inside count too) and GEMMs.
+  uint64_t fused_host_ns = 0;
+  uint64_t gemm_host_ns = 0;
 };
 BackendStats& backend_stats();
+
+// Adds the lifetime of the scope to a host-time counter.
+class HostTimer {
+ public:
+  explicit HostTimer(uint64_t* acc) : acc_(acc), t0_(std::chrono::steady_clock::now()) {}
+  ~HostTimer() {
+    if (acc_)
+      *acc_ += static_cast<uint64_t>(std::chrono::duration_cast<std::chrono::nanoseconds>(
+                                         std::chrono::steady_clock::now() - t0_)
+                                         .count());
+  }
+  HostTimer(const HostTimer&) = delete;
+  HostTimer& operator=(const HostTimer&) = delete;
+
+ private:
+  uint64_t* acc_;
+  std::chrono::steady_clock::time_point t0_;
+};
 
 }  // namespace lmp::tensor
