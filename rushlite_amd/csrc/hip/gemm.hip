@@ -491,6 +491,179 @@ void gemm_direct(DirectArgs g) {
   }
 }
 
+// ------------------------------------------------------------------ tiny
+//
+// Latency-bound GEMMs (up to about two million multiply-adds with K <= 512,
+// e.g. the README MLP's layers): one workgroup per BS x BS block of C (BS =
+// 32 with 32x32x2 MFMAs, or 16 with 16x16x4 MFMAs when 32-wide blocks would
+// leave most CUs idle), its four waves taking consecutive quarters of K in
+// groups of G = 4 * (64 / BS) k values and adding their blocks through LDS
+// in wave order.  Lane l holds row / column l % BS; within group j, MFMA step
+// s (0..3) gives lane part q = l / BS the k value G*j + 4q + s, so a lane's
+// four values of an operand whose k is contiguous in memory (A untransposed,
+// B transposed) are one 128-bit load when the rows allow it; the other
+// operand is read a k value per load, consecutive lanes reading consecutive
+// addresses.  All of a wave's loads are issued before its first MFMA, so a
+// block costs about one memory latency plus the wave's MFMAs, where the tiled
+// kernels pay a pipeline fill per K tile and the register-direct kernel a
+// 32x128 block per wave.
+//
+// Operands are read through buffer resources: an offset at or past the
+// resource's size (kTinyOob) reads zero, so rows or columns outside the matrix
+// and k past the wave's range cost one select each.
+constexpr int64_t kTinyMaxMacs = int64_t(1) << 21;
+constexpr int kTinyMaxK = 512;
+constexpr uint32_t kTinyOob = 0x80000000u;
+constexpr uint32_t kTinyMaxBytes = 1u << 30;  // operand extents stay below kTinyOob
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tiny_rsrc(const float* p, uint32_t bytes) {
+  // Third dword 0x00020000: a raw 32-bit buffer on gfx9-family targets.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, int(bytes), 0x00020000);
+}
+
+// One operand of one lane: `base` is the byte offset of the lane's row of
+// op(A) or column of op(B) (kTinyOob outside the matrix), `kstep` the byte
+// distance between consecutive k.  VEC: k is contiguous and rows are 16-byte
+// multiples, K % 4 == 0, so a lane's four k values of a group come in one
+// load that is either wholly inside or wholly past K.
+template <bool VEC>
+struct TinyOperand {
+  __amdgpu_buffer_rsrc_t r;
+  uint32_t base, kstep;
+  __device__ __forceinline__ v4f load(int k, int kend) const {  // k, k+1, k+2, k+3
+    v4f v;
+    if constexpr (VEC) {
+      const uint32_t o = k < kend ? base + 4u * uint32_t(k) : kTinyOob;
+      v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r, int(o), 0, 0));
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t o = k + s < kend ? base + uint32_t(k + s) * kstep : kTinyOob;
+        v[s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, int(o), 0, 0));
+      }
+    }
+    return v;
+  }
+};
+
+template <int BS>
+struct TinyMma;
+template <>
+struct TinyMma<32> {
+  using Acc = v16f;
+  static constexpr int kRegs = 16;
+  __device__ __forceinline__ static Acc step(float a, float b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+  // Row of accumulator register r for lane part q (l / 32).
+  __device__ __forceinline__ static int row(int r, int q) { return direct_row(r, q); }
+};
+template <>
+struct TinyMma<16> {
+  using Acc = v4f;
+  static constexpr int kRegs = 4;
+  __device__ __forceinline__ static Acc step(float a, float b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static int row(int r, int q) { return q * 4 + r; }
+};
+
+template <int BS, bool TA, bool TB, bool VA, bool VB>
+__global__ __launch_bounds__(256) void gemm_tiny(GemmArgs g) {
+  using M = TinyMma<BS>;
+  constexpr int G = 4 * (64 / BS);              // k values per group
+  constexpr int kGroups = kTinyMaxK / G / 4;    // a wave's quarter of K <= 512
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int li = lane % BS, q = lane / BS;
+  const int m0 = int(blockIdx.x) * BS, n0 = int(blockIdx.y) * BS;
+  const int groups = (g.k + G - 1) / G;
+  const int per = (groups + 3) / 4;
+  const int j0 = min(groups, wave * per), j1 = min(groups, j0 + per);
+  const int kend = min(g.k, G * j1);
+  // Stored extents: A is [k, m] (TA) or [m, k]; B is [n, k] (TB) or [k, n].
+  const uint32_t a_bytes = 4u * uint32_t(TA ? (g.k - 1) * g.lda + g.m : (g.m - 1) * g.lda + g.k);
+  const uint32_t b_bytes = 4u * uint32_t(TB ? (g.n - 1) * g.ldb + g.k : (g.k - 1) * g.ldb + g.n);
+  const int row = m0 + li, col = n0 + li;
+  const TinyOperand<VA> opa{tiny_rsrc(g.a, a_bytes),
+                            row < g.m ? 4u * uint32_t(TA ? row : row * g.lda) : kTinyOob,
+                            TA ? 4u * uint32_t(g.lda) : 4u};
+  const TinyOperand<VB> opb{tiny_rsrc(g.b, b_bytes),
+                            col < g.n ? 4u * uint32_t(TB ? col * g.ldb : col) : kTinyOob,
+                            TB ? 4u : 4u * uint32_t(g.ldb)};
+  // Every load of the wave's range is issued before the first MFMA (group
+  // branches are uniform), so the range costs one memory latency.
+  v4f a[kGroups], b[kGroups];
+#pragma unroll
+  for (int c = 0; c < kGroups; ++c)
+    if (j0 + c < j1) {
+      a[c] = opa.load(G * (j0 + c) + 4 * q, kend);
+      b[c] = opb.load(G * (j0 + c) + 4 * q, kend);
+    }
+  typename M::Acc acc = typename M::Acc(0.0f);
+#pragma unroll
+  for (int c = 0; c < kGroups; ++c)
+    if (j0 + c < j1)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) acc = M::step(a[c][s], b[c][s], acc);
+  // Blocks of the four waves summed in wave order: [wave][r][lane].
+  constexpr int R = M::kRegs;
+  __shared__ float red[4 * R * 64];
+#pragma unroll
+  for (int r = 0; r < R; ++r) red[(wave * R + r) * 64 + lane] = acc[r];
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < R / 4; ++u) {
+    const int p = int(threadIdx.x) + 256 * u;  // (r, lane) pair
+    const int r = p >> 6, ln = p & 63;
+    float v = red[p];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) v += red[w * R * 64 + p];
+    const int orow = m0 + M::row(r, ln / BS), ocol = n0 + ln % BS;
+    if (orow >= g.m || ocol >= g.n) continue;
+    float* o = g.c + int64_t(orow) * g.ldc + ocol;
+    if (g.accumulate) *o = *o + v;
+    else *o = g.bias ? v + g.bias[ocol] : v;
+  }
+}
+
+bool tiny_ok(const GemmArgs& g) {
+  if (g.k > kTinyMaxK || int64_t(g.m) * g.n * g.k > kTinyMaxMacs) return false;
+  const int64_t a_elems = int64_t(g.lda) * (g.k > g.m ? g.k : g.m);  // bounds either layout
+  const int64_t b_elems = int64_t(g.ldb) * (g.k > g.n ? g.k : g.n);
+  return 4 * a_elems < kTinyMaxBytes && 4 * b_elems < kTinyMaxBytes;
+}
+
+bool aligned16(const void* p);
+
+template <int BS, bool TA, bool TB>
+void launch_tiny_bs(Runtime* rt, const GemmArgs& g, bool va, bool vb) {
+  const dim3 grid{uint32_t((g.m + BS - 1) / BS), uint32_t((g.n + BS - 1) / BS), 1u};
+  if (va && vb)
+    hipLaunchKernelGGL((gemm_tiny<BS, TA, TB, !TA, TB>), grid, dim3(256), 0, rt->stream, g);
+  else if (va)
+    hipLaunchKernelGGL((gemm_tiny<BS, TA, TB, !TA, false>), grid, dim3(256), 0, rt->stream, g);
+  else if (vb)
+    hipLaunchKernelGGL((gemm_tiny<BS, TA, TB, false, TB>), grid, dim3(256), 0, rt->stream, g);
+  else
+    hipLaunchKernelGGL((gemm_tiny<BS, TA, TB, false, false>), grid, dim3(256), 0, rt->stream,
+                       g);
+}
+
+template <bool TA, bool TB>
+int launch_tiny(Runtime* rt, const GemmArgs& g) {
+  // 128-bit k loads for an operand whose k is contiguous, with 16-byte rows.
+  const bool k4 = g.k % 4 == 0;
+  const bool va = !TA && k4 && g.lda % 4 == 0 && aligned16(g.a);
+  const bool vb = TB && k4 && g.ldb % 4 == 0 && aligned16(g.b);
+  // 16x16 blocks unless 32x32 blocks already cover a quarter of the CUs.
+  const int64_t blocks32 = int64_t((g.m + 31) / 32) * ((g.n + 31) / 32);
+  if (blocks32 * 4 >= rt->cu_count) launch_tiny_bs<32, TA, TB>(rt, g, va, vb);
+  else launch_tiny_bs<16, TA, TB>(rt, g, va, vb);
+  LMP_LAUNCH_CHECK("gemm_tiny");
+  return LMP_OK;
+}
+
 // ------------------------------------------------------------- LDS-direct
 //
 // Tile kernels for operands that allow 128-bit loads.  Panels go from global
@@ -920,13 +1093,15 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
   return LMP_OK;
 }
 
-// Tile choice (measured on MI355X, fp32): 128x128 whenever its tiles cover
+// Tile choice (measured on MI355X, fp32): the tiny kernel for small
+// latency-bound products (K <= 512, at most 2^21 multiply-adds); 128x128 whenever its tiles cover
 // the CUs; with a short K (<= 2048) and too few 128x128 tiles, 64x64 tiles
 // without a split (no partial round trip) win; otherwise 128x128 with split
 // K.  M <= 64 uses 32x256 tiles, and M <= 32 the register-direct kernel when
 // its alignment requirements hold.
 template <bool TA, bool TB>
 int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok) {
+  if (tiny_ok(g)) return launch_tiny<TA, TB>(rt, g);
   if (direct_ok && g.m <= 32) return launch_direct<TA, TB>(rt, g);
   if (g.m <= 64) return launch_gemm_cfg<CfgSkinny, TA, TB>(rt, g, vec);
   if (vec) {

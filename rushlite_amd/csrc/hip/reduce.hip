@@ -294,8 +294,18 @@ __global__ __launch_bounds__(kBlock) void col_reduce_scalar(
   const uint64_t r0 = s * chunk;
   const uint64_t r1 = min(len, r0 + chunk);
   const T* src = in + (o * len + r0) * inner + c;
+  // Eight loads in flight, combined in row order (the result is the
+  // sequential fold, as without the batching).
   T acc = R::identity();
-  for (uint64_t r = r0; r < r1; ++r, src += inner) acc = R::combine(acc, *src);
+  uint64_t r = r0;
+  for (; r + 8 <= r1; r += 8, src += 8 * inner) {
+    T x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = src[u * inner];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = R::combine(acc, x[u]);
+  }
+  for (; r < r1; ++r, src += inner) acc = R::combine(acc, *src);
   dst[(o * S + s) * inner + c] = acc;
 }
 

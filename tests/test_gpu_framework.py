@@ -707,6 +707,31 @@ def test_held_interior_value_is_stored_by_the_same_kernel(rsl):
         assert np.array_equal(got.numpy().view(np.uint64), w.numpy().view(np.uint64))
 
 
+def test_long_held_chain_splits_into_few_regions(rsl):
+    """48 captured ops whose every intermediate is held (as autograd holds
+    forward values) exceed one kernel's output limit: the chain splits into a
+    few regions, each storing its part, and every value equals eager."""
+    rng = np.random.default_rng(13)
+    a, b = V(rsl, rng.random((64, 96), dtype=np.float32)), V(rsl, rng.random((64, 96), dtype=np.float32))
+
+    def chain():
+        held, t = [], a
+        for i in range(32):
+            t = t * b + a if i % 2 == 0 else t - b
+            held.append(t)
+        return held
+
+    eager = [t.numpy() for t in chain()]
+    s0 = rsl._stats()["fused_launches"]
+    with rsl.capture_on():
+        held = chain()
+    held[-1].realize()
+    assert rsl._stats()["fused_launches"] - s0 <= 4
+    for i, (t, w) in enumerate(zip(held, eager)):
+        assert not rsl._is_deferred(t), i
+        assert np.array_equal(t.numpy().view(np.uint32), w.view(np.uint32)), i
+
+
 def test_leaf_region_storing_a_shared_node(rsl):
     """Rows of 4096 are too long for a row kernel, so the row sum L below is a
     leaf of c's region, and realising it first reaches n, which c's region

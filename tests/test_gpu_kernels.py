@@ -166,7 +166,11 @@ def test_reduce_ones_column_is_exact(hip):
 GEMM_SHAPES = [(64, 64, 64), (128, 256, 96), (33, 17, 70), (32, 512, 1024),
                (256, 1000, 128), (32, 64, 256), (32, 10, 64), (200, 3, 5),
                (1, 7, 3), (512, 512, 2048), (130, 260, 33), (32, 132, 1028),
-               (20, 132, 1028), (4, 260, 2048), (1, 8, 8)]
+               (20, 132, 1028), (4, 260, 2048), (1, 8, 8),
+               # the tiny kernel's limits (K <= 512, at most 2^21 multiply-adds)
+               # and odd K; just past them, the 32 x 256 and 64 x 64 tiles
+               (64, 64, 512), (64, 65, 512), (40, 33, 1), (31, 70, 3),
+               (48, 300, 1000), (130, 260, 600)]
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES, ids=str)
