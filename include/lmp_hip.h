@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define LMP_HIP_ABI_VERSION 4
+#define LMP_HIP_ABI_VERSION 5
 #define LMP_MAX_DIMS 16 /* align_utils.hpp:7 */
 
 typedef enum {
@@ -246,6 +246,15 @@ int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
 int lmp_k_linear_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
                      const float* a, size_t lda, const float* b, size_t ldb,
                      const float* bias, float* c, size_t ldc);
+
+/* C = relu(op(A) * op(B) + bias): lmp_k_linear_f32 with ReLU applied in the
+ * same epilogue, as the clamp functor computes clamp(t, 0, DBL_MAX) in float32
+ * (t < 0 ? 0 : t; NaN and -0.0 pass through).  Replaces a Sequential's Linear
+ * followed by ReLU (layers/linear.cpp:21-26 then layers/activation.cpp:14),
+ * which the reference runs as matmul, broadcast add and clamp. */
+int lmp_k_linear_relu_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
+                          const float* a, size_t lda, const float* b, size_t ldb,
+                          const float* bias, float* c, size_t ldc);
 
 /* The same product for any dtype, operands and C all of `dtype`
  * (LMP_FLOAT32 is lmp_k_gemm_f32).  float64 accumulates on the f64 matrix

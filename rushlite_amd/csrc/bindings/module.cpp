@@ -353,6 +353,10 @@ PYBIND11_MODULE(_C, m) {
   m.def("linear", &ag::ops::linear, py::arg("x"), py::arg("w"), py::arg("b"),
         "x @ w + b in one GEMM (the bias added in its epilogue); the same values as "
         "matmul followed by the broadcast add.");
+  m.def("linear_relu", &ag::ops::linear_relu, py::arg("x"), py::arg("w"), py::arg("b"),
+        "clamp(x @ w + b, 0, DBL_MAX) (Linear then ReLU) as one node: on the HIP device one "
+        "GEMM whose epilogue adds the bias and applies ReLU; the same values and gradients "
+        "as the two layers.");
   m.def("sum", &ag::ops::sum, py::arg("a"), py::arg("axis"));
   m.def("max", &ag::ops::max, py::arg("a"), py::arg("axis"));
   m.def("min", &ag::ops::min, py::arg("a"), py::arg("axis"));

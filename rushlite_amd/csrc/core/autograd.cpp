@@ -8,6 +8,7 @@
 // need not be a scalar (it is seeded with ones).  Linear's backward products
 // dY*W^T and X^T*dY run as transposed-operand GEMMs instead of a transpose
 // followed by a GEMM.
+#include <limits>
 #include "autograd.hpp"
 
 #include <algorithm>
@@ -340,6 +341,24 @@ Variable linear(const Variable& x, const Variable& w, const Variable& b) {
                   if (in[2].requires_grad()) in[2].incr_grad(sba(G, in[2]));
                   if (in[0].requires_grad()) in[0].incr_grad_matmul(G, in[1].data(), false, true);
                   if (in[1].requires_grad()) in[1].incr_grad_matmul(in[0].data(), G, true, false);
+                });
+}
+
+Variable linear_relu(const Variable& x, const Variable& w, const Variable& b) {
+  const DataType dt = x.data().type();
+  if (dt != DataType::Float32 && dt != DataType::Float64)
+    return clamp(linear(x, w, b), 0.0, std::numeric_limits<double>::max());
+  // One node for Linear followed by ReLU.  ReLU's backward masks the gradient
+  // by its input t (ClampBackward: g where 0 < t < max, functions/
+  // unary_ops.cpp:27); for clamp(t, 0, max) the output gives the same mask for
+  // every t, including NaN, +-0 and +-inf, so the pre-activation is not kept.
+  return record(tops::linear(x.data(), w.data(), b.data(), true), {x, w, b},
+                "LinearReluBackward", [](LMP_BW_ARGS) {
+                  const Tensor gt = tops::clamp_backward(out.data(), G, 0.0,
+                                                         std::numeric_limits<double>::max());
+                  if (in[2].requires_grad()) in[2].incr_grad(sba(gt, in[2]));
+                  if (in[0].requires_grad()) in[0].incr_grad_matmul(gt, in[1].data(), false, true);
+                  if (in[1].requires_grad()) in[1].incr_grad_matmul(in[0].data(), gt, true, false);
                 });
 }
 

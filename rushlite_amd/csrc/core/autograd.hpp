@@ -103,6 +103,8 @@ LMP_FOR_REDUCT_OPS(LMP_AG_REDUCT)
 Variable clamp(const Variable& a, Scalar lo, Scalar hi);
 Variable matmul(const Variable& a, const Variable& b);
 Variable linear(const Variable& x, const Variable& w, const Variable& b);
+// relu(linear(x, w, b)) as one node (Sequential's Linear -> ReLU pairs).
+Variable linear_relu(const Variable& x, const Variable& w, const Variable& b);
 Variable transpose(const Variable& a);
 Variable reshape(const Variable& a, const std::vector<size_t>& shape);
 Variable squeeze(const Variable& a, size_t axis);

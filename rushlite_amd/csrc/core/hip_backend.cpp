@@ -301,7 +301,8 @@ void matmul_acc_hip(TensorImpl& c, const TensorImpl& a, const TensorImpl& b, boo
   gemm_into(c.data(), dt, a, b, ta, tb, s, true);
 }
 
-TensorImpl linear_hip(const TensorImpl& x, const TensorImpl& w, const TensorImpl& b) {
+TensorImpl linear_hip(const TensorImpl& x, const TensorImpl& w, const TensorImpl& b,
+                      bool relu) {
   const GemmShape s = gemm_shape(x, w, false, false);
   Storage out(s.m * s.n * sizeof(float), DeviceType::HIP);
   if (s.m && s.n) {
@@ -310,10 +311,11 @@ TensorImpl linear_hip(const TensorImpl& x, const TensorImpl& w, const TensorImpl
     const void* pw = mut(w);
     const void* pb = mut(b);
     count_launch();
-    hip_ok(lmp_k_linear_f32(0, 0, s.m, s.n, s.k, static_cast<const float*>(px), s.k,
-                            static_cast<const float*>(pw), s.n, static_cast<const float*>(pb),
-                            static_cast<float*>(out.data()), s.n),
-           "lmp_k_linear_f32");
+    const auto entry = relu ? lmp_k_linear_relu_f32 : lmp_k_linear_f32;
+    hip_ok(entry(0, 0, s.m, s.n, s.k, static_cast<const float*>(px), s.k,
+                 static_cast<const float*>(pw), s.n, static_cast<const float*>(pb),
+                 static_cast<float*>(out.data()), s.n),
+           relu ? "lmp_k_linear_relu_f32" : "lmp_k_linear_f32");
   }
   return TensorImpl(out, {s.m, s.n}, DataType::Float32);
 }

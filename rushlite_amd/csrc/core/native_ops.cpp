@@ -165,7 +165,7 @@ void matmul_acc(Tensor& c, const Tensor& a, const Tensor& b, bool trans_a, bool 
                     trans_a, trans_b);
 }
 
-Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b) {
+Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b, bool relu) {
   LMP_CHECK(x.device() == w.device() && x.device() == b.device())
       << "Tensors must be on the same device";
   const bool fused = linear_stub().has(x.device()) && x.type() == DataType::Float32 &&
@@ -174,8 +174,12 @@ Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b) {
                      x.shape()[1] == w.shape()[0] &&
                      (b.shape() == std::vector<size_t>{w.shape()[1]} ||
                       b.shape() == std::vector<size_t>{1, w.shape()[1]});
-  if (!fused) return add(matmul(x, w), b);
-  return wrap(linear_stub()(x.device(), *Acc::getImpl(x), *Acc::getImpl(w), *Acc::getImpl(b)));
+  if (!fused) {
+    Tensor y = add(matmul(x, w), b);
+    return relu ? clamp(y, 0.0, std::numeric_limits<double>::max()) : y;
+  }
+  return wrap(linear_stub()(x.device(), *Acc::getImpl(x), *Acc::getImpl(w), *Acc::getImpl(b),
+                            relu));
 }
 
 Tensor transpose(const Tensor& a) {

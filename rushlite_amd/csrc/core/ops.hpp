@@ -62,10 +62,12 @@ using matmul_acc_fn = void (*)(TensorImpl& c, const TensorImpl&, const TensorImp
                                bool, bool);
 // x @ w + b with the bias added in the GEMM epilogue; the reference spells it
 // matmul then broadcast add (LinearImpl::forward, layers/linear.cpp:21-26),
-// with the same rounding.  Called only for float32 operands, a 2-D x and w,
+// with the same rounding.  With `relu` the epilogue also applies ReLU,
+// clamp(t, 0, DBL_MAX) (layers/activation.cpp:14), as the Linear -> ReLU pair
+// of a Sequential would.  Called only for float32 operands, a 2-D x and w,
 // and a bias of w's column count.
 using linear_fn = TensorImpl (*)(const TensorImpl& x, const TensorImpl& w,
-                                 const TensorImpl& b);
+                                 const TensorImpl& b, bool relu);
 
 #define LMP_FOR_BINARY_OPS(_) \
   _(add) _(sub) _(mul) _(div) _(pow) _(eq) _(ne) _(ge) _(le) _(gt) _(lt)
@@ -106,8 +108,9 @@ Tensor matmul(const Tensor& a, const Tensor& b);
 Tensor matmul_t(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b);
 // c += op(a) @ op(b) in place (shapes must match exactly).
 void matmul_acc(Tensor& c, const Tensor& a, const Tensor& b, bool trans_a, bool trans_b);
-// x @ w + b (Linear's forward); one fused GEMM where the backend has one.
-Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b);
+// x @ w + b (Linear's forward), followed by ReLU when `relu`; one fused GEMM
+// where the backend has one.
+Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b, bool relu = false);
 Tensor transpose(const Tensor& a);
 Tensor reshape(const Tensor& a, std::vector<size_t> shape);
 Tensor squeeze(const Tensor& a, size_t dim);

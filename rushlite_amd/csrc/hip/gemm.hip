@@ -80,7 +80,19 @@ struct GemmArgs {
   int accumulate;      // only honoured when writing the final output
   const float* bias;   // per-column bias added to the final output (or null)
   int vec_out;         // C (and the bias) take 128-bit stores: n, ldc % 4 == 0, 16-byte aligned
+  int relu;            // with a bias: ReLU after it (Linear followed by ReLU)
 };
+
+// Linear's epilogue: v + b, then, when asked, ReLU as the clamp functor
+// computes clamp(t, 0, +inf) in float32: t < 0 ? 0 : t (NaN and -0.0 pass).
+__device__ __forceinline__ float lin_epi(float v, float b, int relu) {
+  const float t = v + b;
+  return relu && t < 0.0f ? 0.0f : t;
+}
+__device__ __forceinline__ v4f lin_epi4(v4f v, v4f b, int relu) {
+  return v4f{lin_epi(v.x, b.x, relu), lin_epi(v.y, b.y, relu), lin_epi(v.z, b.z, relu),
+             lin_epi(v.w, b.w, relu)};
+}
 
 // Load one [rows x cols] panel of a row-major matrix (leading dim ld) starting
 // at (r0, c0) into registers as float4, bounds-checked against (R, Cn).
@@ -268,7 +280,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma(GemmArgs g) {
           float* p = out + int64_t(row) * ld + col;
           const float v = acc[i][j][r];
           if (!partial && g.accumulate) *p = *p + v;
-          else if (!partial && g.bias) *p = v + g.bias[col];
+          else if (!partial && g.bias) *p = lin_epi(v, g.bias[col], g.relu);
           else *p = v;
         }
       }
@@ -281,7 +293,7 @@ __global__ __launch_bounds__(256) void fold_splits(float* __restrict__ c,
                                                    const float* __restrict__ part,
                                                    int m, int n, int ldc,
                                                    int splits, int accumulate,
-                                                   const float* __restrict__ bias) {
+                                                   const float* __restrict__ bias, int relu) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   const int64_t mn = int64_t(m) * n;
   if (i >= mn) return;
@@ -290,7 +302,7 @@ __global__ __launch_bounds__(256) void fold_splits(float* __restrict__ c,
   for (int s = 1; s < splits; ++s) acc += part[int64_t(s) * mn + i];
   float* p = c + int64_t(row) * ldc + col;
   if (accumulate) *p = *p + acc;
-  else *p = bias ? acc + bias[col] : acc;
+  else *p = bias ? lin_epi(acc, bias[col], relu) : acc;
 }
 
 // ------------------------------------------------------------------ direct
@@ -323,6 +335,7 @@ struct DirectArgs {
   int k_per_wg;    // K range of one workgroup (a multiple of 32)
   int accumulate;  // only honoured when writing the final output
   const float* bias;  // per-column bias added to the final output (or null)
+  int relu;           // with a bias: ReLU after it
 };
 
 constexpr int kDirectN = 128;
@@ -475,7 +488,7 @@ void gemm_direct(DirectArgs g) {
       if (col < g.n) {
         v4f* o = reinterpret_cast<v4f*>(base + col);
         if (acc_out) *o = *o + v[u];
-        else if (bias) *o = v[u] + *reinterpret_cast<const v4f*>(bias + col);
+        else if (bias) *o = lin_epi4(v[u], *reinterpret_cast<const v4f*>(bias + col), g.relu);
         else *o = v[u];
       }
     } else {
@@ -484,7 +497,7 @@ void gemm_direct(DirectArgs g) {
         const int col = n0 + 32 * q + (ln & 31);
         if (col < g.n) {
           if (acc_out) base[col] = base[col] + v[u][q];
-          else base[col] = bias ? v[u][q] + bias[col] : v[u][q];
+          else base[col] = bias ? lin_epi(v[u][q], bias[col], g.relu) : v[u][q];
         }
       }
     }
@@ -623,7 +636,7 @@ __global__ __launch_bounds__(256) void gemm_tiny(GemmArgs g) {
     if (orow >= g.m || ocol >= g.n) continue;
     float* o = g.c + int64_t(orow) * g.ldc + ocol;
     if (g.accumulate) *o = *o + v;
-    else *o = g.bias ? v + g.bias[ocol] : v;
+    else *o = g.bias ? lin_epi(v, g.bias[ocol], g.relu) : v;
   }
 }
 
@@ -933,7 +946,7 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
           if (row < g.m && col < g.n) {
             v4f* p = reinterpret_cast<v4f*>(out + int64_t(row) * ld + col);
             if (acc_out) *p = *p + v;
-            else if (bias) *p = v + *reinterpret_cast<const v4f*>(bias + col);
+            else if (bias) *p = lin_epi4(v, *reinterpret_cast<const v4f*>(bias + col), g.relu);
             else *p = v;
           }
         }
@@ -954,7 +967,7 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
           float* p = out + int64_t(row) * ld + col;
           const float v = acc[i][j][r];
           if (acc_out) *p = *p + v;
-          else if (bias) *p = v + bias[col];
+          else if (bias) *p = lin_epi(v, bias[col], g.relu);
           else *p = v;
         }
       }
@@ -1006,7 +1019,7 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
     const int64_t mn = int64_t(g.m) * g.n;
     hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
                        rt->stream, final_c, part, g.m, g.n, g.ldc, splits,
-                       g.accumulate, g.bias);
+                       g.accumulate, g.bias, g.relu);
     LMP_LAUNCH_CHECK("fold_splits");
     scratch_free(part);
   }
@@ -1040,7 +1053,7 @@ int launch_lds(Runtime* rt, GemmArgs g) {
     const int64_t mn = int64_t(g.m) * g.n;
     hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
                        rt->stream, final_c, part, g.m, g.n, g.ldc, splits,
-                       g.accumulate, g.bias);
+                       g.accumulate, g.bias, g.relu);
     LMP_LAUNCH_CHECK("fold_splits");
     scratch_free(part);
   }
@@ -1064,6 +1077,7 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
   d.ldc = g0.ldc;
   d.accumulate = g0.accumulate;
   d.bias = g0.bias;
+  d.relu = g0.relu;
   d.n_blocks = (g0.n + kDirectN - 1) / kDirectN;
   constexpr int kGrain = 8 * kDirectWaves;
   const int max_splits = std::max(1, g0.k / (64 * kDirectWaves));
@@ -1086,7 +1100,7 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
     const int64_t mn = int64_t(g0.m) * g0.n;
     hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
                        rt->stream, g0.c, part, g0.m, g0.n, g0.ldc, splits, g0.accumulate,
-                       g0.bias);
+                       g0.bias, g0.relu);
     LMP_LAUNCH_CHECK("fold_splits");
     scratch_free(part);
   }
@@ -1156,7 +1170,7 @@ namespace {
 
 int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
                    const float* a, size_t lda, const float* b, size_t ldb,
-                   const float* bias, float* c, size_t ldc, int accumulate) {
+                   const float* bias, float* c, size_t ldc, int accumulate, int relu = 0) {
   if (m == 0 || n == 0) return LMP_OK;
   if (!c) return fail(LMP_ERR_INVALID, "gemm: null output");
   if (k == 0 && bias)
@@ -1185,6 +1199,7 @@ int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
   g.ldc = int(ldc);
   g.accumulate = accumulate ? 1 : 0;
   g.bias = bias;
+  g.relu = bias && relu ? 1 : 0;
   g.vec_out = n % 4 == 0 && ldc % 4 == 0 && aligned16(c) && (!bias || aligned16(bias));
   // 128-bit panel loads need 16-byte rows and a contiguous extent that is a
   // multiple of four.
@@ -1218,6 +1233,15 @@ extern "C" int lmp_k_linear_f32(int trans_a, int trans_b, size_t m, size_t n,
                                 float* c, size_t ldc) {
   if (!bias) return fail(LMP_ERR_INVALID, "linear: null bias");
   return gemm_f32_entry(trans_a, trans_b, m, n, k, a, lda, b, ldb, bias, c, ldc, 0);
+}
+
+extern "C" int lmp_k_linear_relu_f32(int trans_a, int trans_b, size_t m, size_t n,
+                                     size_t k, const float* a, size_t lda,
+                                     const float* b, size_t ldb, const float* bias,
+                                     float* c, size_t ldc) {
+  if (!bias) return fail(LMP_ERR_INVALID, "linear_relu: null bias");
+  if (k == 0) return fail(LMP_ERR_UNSUPPORTED, "linear_relu: k == 0");
+  return gemm_f32_entry(trans_a, trans_b, m, n, k, a, lda, b, ldb, bias, c, ldc, 0, 1);
 }
 
 extern "C" int lmp_k_transpose(int dtype, void* out, const void* in, size_t m,

@@ -28,6 +28,10 @@ class Linear(Module):
             return _C.linear(x, self.weights, self.bias)
         return _C.matmul(x, self.weights)
 
+    def forward_relu(self, x):
+        """relu(forward(x)) as one node (Sequential's Linear -> ReLU pairs)."""
+        return _C.linear_relu(x, self.weights, self.bias)
+
 
 class Flatten(Module):
     def __init__(self, start_dim: int = 1, end_dim: int = -1) -> None:

@@ -766,6 +766,65 @@ def test_leaf_region_storing_a_shared_node(rsl):
         assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
 
 
+@pytest.mark.parametrize("dt", ["float32", "float64"])
+@pytest.mark.parametrize("m,k,n", [(32, 256, 64), (20, 70, 10), (512, 2048, 2048), (64, 130, 33)],
+                         ids=str)
+def test_linear_relu_node_matches_linear_then_relu(rsl, m, k, n, dt):
+    """linear_relu (Sequential's Linear -> ReLU as one node, ReLU in the GEMM
+    epilogue for float32) gives the values and the x, w, b gradients of linear
+    followed by clamp(., 0, DBL_MAX), bit for bit, with infinities and NaN in
+    x (the backward masks by the output, which must equal masking by the
+    input)."""
+    rng = np.random.default_rng(m * k + n + 1)
+    x_np = rng.standard_normal((m, k)).astype(dt)
+    x_np[0, :3] = [np.inf, -np.inf, np.nan] if m > 1 else x_np[0, :3]
+    w_np = rng.standard_normal((k, n)).astype(dt)
+    b_np = rng.standard_normal(n).astype(dt)
+    view = np.uint32 if dt == "float32" else np.uint64
+    outs, grads = [], []
+    for fused in (True, False):
+        x = rsl.Variable(x_np, dtype=getattr(rsl.dtype, dt), requires_grad=True)
+        w = rsl.Variable(w_np, dtype=getattr(rsl.dtype, dt), requires_grad=True)
+        b = rsl.Variable(b_np, dtype=getattr(rsl.dtype, dt), requires_grad=True)
+        y = rsl._C.linear_relu(x, w, b) if fused else rsl.clamp(rsl.linear(x, w, b), 0, DBL_MAX)
+        (y * 0.5 + 1.0).sum(1).sum(0).backward()
+        outs.append(y.numpy())
+        grads.append([x.grad.numpy(), w.grad.numpy(), b.grad.numpy()])
+    assert np.array_equal(outs[0].view(view), outs[1].view(view))
+    for g0, g1 in zip(*grads):
+        assert np.array_equal(g0.view(view), g1.view(view))
+
+
+def test_sequential_fuses_linear_relu_pairs(rsl):
+    """Sequential runs Linear -> ReLU as one node; a model whose ReLU is a
+    subclass (not fused) gives the same loss and gradients bit for bit."""
+    from rushlite_amd.nets import layers
+
+    class PlainReLU(layers.ReLU):
+        pass
+
+    rng = np.random.default_rng(17)
+    x_np = rng.standard_normal((48, 96)).astype(np.float32)
+    ws = [rng.standard_normal((96, 80)).astype(np.float32), rng.standard_normal((80, 10)).astype(np.float32)]
+    bs = [rng.standard_normal(80).astype(np.float32), rng.standard_normal(10).astype(np.float32)]
+    results = []
+    for relu_cls in (layers.ReLU, PlainReLU):
+        model = layers.Sequential([layers.Linear(96, 80), relu_cls(), layers.Linear(80, 10)])
+        for i, idx in enumerate((0, 2)):
+            model.params[f"{idx}.weights"] = rsl.Variable(ws[i], requires_grad=True)
+            model.params[f"{idx}.bias"] = rsl.Variable(bs[i], requires_grad=True)
+        s0 = rsl._stats()["eager_launches"]
+        out = model(rsl.Variable(x_np))
+        launches = rsl._stats()["eager_launches"] - s0
+        out.sum(1).sum(0).backward()
+        results.append((out.numpy(), [p.grad.numpy() for _, p in model.named_parameters()], launches))
+    (o0, g0, n0), (o1, g1, n1) = results
+    assert np.array_equal(o0.view(np.uint32), o1.view(np.uint32))
+    for a, b in zip(g0, g1):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert n0 == n1 - 1  # the ReLU launch is gone
+
+
 @pytest.mark.parametrize("m,k,n", [(32, 256, 64), (20, 70, 10), (512, 2048, 2048), (64, 130, 33)],
                          ids=str)
 def test_linear_op_matches_matmul_plus_bias(rsl, m, k, n):

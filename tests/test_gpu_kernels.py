@@ -299,4 +299,10 @@ def test_linear_bias_epilogue_equals_gemm_then_add(hip, m, n, k, ta, tb):
     out = hip.DeviceBuffer((m, n), np.float32)
     hip.check(hip.lib().lmp_k_linear_f32(ta, tb, m, n, k, da.ptr, da.shape[1], db.ptr,
                                          db.shape[1], dbias.ptr, out.ptr, n))
-    assert np.array_equal(out.numpy(), plain + bias[None, :])
+    want = plain + bias[None, :]
+    assert np.array_equal(out.numpy(), want)
+    # ReLU in the same epilogue: clamp(t, 0, DBL_MAX) in float32, t < 0 -> +0
+    hip.check(hip.lib().lmp_k_linear_relu_f32(ta, tb, m, n, k, da.ptr, da.shape[1], db.ptr,
+                                              db.shape[1], dbias.ptr, out.ptr, n))
+    relu = np.where(want < 0, np.float32(0), want)
+    assert np.array_equal(out.numpy().view(np.uint32), relu.view(np.uint32))
