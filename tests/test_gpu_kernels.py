@@ -277,6 +277,34 @@ def test_errors_are_reported(hip):
     assert L.lmp_rt_free(C.c_void_p(0xdead00)) == hip.ERR_INVALID
 
 
+# Short-K products with a large C (write-bound, like config 3's skinny weight
+# gradient): ragged M and N, odd K, K = 1.
+@pytest.mark.parametrize("m,n,k", [(4100, 1030, 31), (2048, 2048, 32), (3000, 1500, 1),
+                                   (4100, 1030, 33)], ids=str)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_short_k_large_c(hip, m, n, k, ta, tb):
+    rng = np.random.default_rng(m + n + k + 10 * ta + 20 * tb)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    da = up(hip, a.T.copy() if ta else a)
+    db = up(hip, b.T.copy() if tb else b)
+    got = hip.gemm(da, db, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert rel_err(got, want) <= 1e-5
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    dc = up(hip, c0)
+    hip.gemm(da, db, trans_a=bool(ta), trans_b=bool(tb), out=dc, accumulate=True)
+    assert np.array_equal(dc.numpy(), c0 + got)
+    bias = rng.standard_normal(n).astype(np.float32)
+    dbias = up(hip, bias)
+    out = hip.DeviceBuffer((m, n), np.float32)
+    hip.check(hip.lib().lmp_k_linear_relu_f32(ta, tb, m, n, k, da.ptr, da.shape[1], db.ptr,
+                                              db.shape[1], dbias.ptr, out.ptr, n))
+    t = got + bias[None, :]
+    assert np.array_equal(out.numpy().view(np.uint32),
+                          np.where(t < 0, np.float32(0), t).view(np.uint32))
+
+
 # lmp_k_linear_f32: the bias rides in every GEMM path's epilogue (register-
 # direct M <= 32, skinny M <= 64, the scalar-load kernel for odd strides, the
 # split-K fold, the 128/256-wide LDS tiles), so C must equal the plain GEMM
