@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define LMP_HIP_ABI_VERSION 5
+#define LMP_HIP_ABI_VERSION 6
 #define LMP_MAX_DIMS 16 /* align_utils.hpp:7 */
 
 typedef enum {
@@ -246,6 +246,20 @@ int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
 int lmp_k_linear_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
                      const float* a, size_t lda, const float* b, size_t ldb,
                      const float* bias, float* c, size_t ldc);
+
+/* C (+)= op(A) * op(B) and colsum[j] (+)= sum over k of op(B)[k][j]: a
+ * Linear's weight gradient X^T dY and bias gradient (the dim-0 sum of dY)
+ * together.  LinearBackward in the reference computes them apart: the bias
+ * through AddBackward's grad-of-broadcast reduction (grad_utils.cpp:10-36)
+ * and the weight through transpose + matmul (functions/matrix_ops.cpp:15-20).
+ * Small products (K <= 512, at most 2^21 multiply-adds) take one launch, the
+ * column sums formed from the B fragments the GEMM already loads; larger ones
+ * run the GEMM and then the dim-0 reduction (B must then be contiguous).
+ * accumulate / colsum_accumulate add into C / colsum instead of writing. */
+int lmp_k_gemm_colsum_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
+                          const float* a, size_t lda, const float* b, size_t ldb,
+                          float* c, size_t ldc, int accumulate, float* colsum,
+                          int colsum_accumulate);
 
 /* C = relu(op(A) * op(B) + bias): lmp_k_linear_f32 with ReLU applied in the
  * same epilogue, as the clamp functor computes clamp(t, 0, DBL_MAX) in float32

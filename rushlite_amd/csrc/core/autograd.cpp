@@ -105,6 +105,28 @@ void Variable::incr_grad_matmul(const Tensor& a, const Tensor& b, bool trans_a,
   tops::matmul_acc(impl_->grad, a, b, trans_a, trans_b);
 }
 
+bool Variable::incr_grad_linear(Variable& w, Variable& b, const Tensor& x, const Tensor& g) {
+  LMP_CHECK(w.requires_grad() && b.requires_grad())
+      << "Cannot access grad() if requires_grad = false";
+  const size_t n = g.shape().size() == 2 ? g.shape()[1] : 0;
+  if (b.impl_->data.numel() != n || w.impl_->data.shape().size() != 2) return false;
+  Tensor wg = w.impl_->grad, bg = b.impl_->grad;
+  // Accumulation is in place on realised buffers (their identity is kept).
+  if (wg.defined()) wg.realize();
+  if (bg.defined()) bg.realize();
+  if (!tops::matmul_colsum(x, g, true, false, &wg, &bg)) return false;
+  if (!w.impl_->grad.defined()) {
+    // A GEMM accumulates from +0, so its product equals 0 + product exactly;
+    // the column sums start from +0 as well.
+    LMP_INTERNAL_ASSERT(wg.shape() == w.impl_->data.shape())
+        << "There should be no broadcasting in incr_grad";
+    w.impl_->grad = wg;
+  }
+  if (!b.impl_->grad.defined())
+    b.impl_->grad = bg.shape() == b.impl_->data.shape() ? bg : bg.reshape(b.impl_->data.shape());
+  return true;
+}
+
 void Variable::set_grad_fn(std::shared_ptr<Function> fn) {
   LMP_CHECK(requires_grad()) << "Cannot access grad() if requires_grad = false";
   impl_->grad_fn = std::move(fn);
@@ -335,13 +357,23 @@ Variable matmul(const Variable& a, const Variable& b) {
 // x @ w + b as one node: the gradients of the reference's AddBackward (bias
 // branch, functions/expand_ops.cpp:15-40) and MatrixMultiplicationBackward
 // (functions/matrix_ops.cpp:8-35), in that order.
+namespace {
+// Gradients of y = x @ w + b for the output gradient g (LinearImpl's
+// matmul + broadcast add, layers/linear.cpp:21-26): dx = g w^T, and dw = x^T g
+// with db = the dim-0 sum of g in one launch where the backend has the form.
+void linear_backward(const Tensor& g, variable_list& in) {
+  if (in[0].requires_grad()) in[0].incr_grad_matmul(g, in[1].data(), false, true);
+  if (in[1].requires_grad() && in[2].requires_grad() &&
+      Variable::incr_grad_linear(in[1], in[2], in[0].data(), g))
+    return;
+  if (in[2].requires_grad()) in[2].incr_grad(sba(g, in[2]));
+  if (in[1].requires_grad()) in[1].incr_grad_matmul(in[0].data(), g, true, false);
+}
+}  // namespace
+
 Variable linear(const Variable& x, const Variable& w, const Variable& b) {
   return record(tops::linear(x.data(), w.data(), b.data()), {x, w, b}, "LinearBackward",
-                [](LMP_BW_ARGS) {
-                  if (in[2].requires_grad()) in[2].incr_grad(sba(G, in[2]));
-                  if (in[0].requires_grad()) in[0].incr_grad_matmul(G, in[1].data(), false, true);
-                  if (in[1].requires_grad()) in[1].incr_grad_matmul(in[0].data(), G, true, false);
-                });
+                [](LMP_BW_ARGS) { linear_backward(G, in); });
 }
 
 Variable linear_relu(const Variable& x, const Variable& w, const Variable& b) {
@@ -354,11 +386,9 @@ Variable linear_relu(const Variable& x, const Variable& w, const Variable& b) {
   // every t, including NaN, +-0 and +-inf, so the pre-activation is not kept.
   return record(tops::linear(x.data(), w.data(), b.data(), true), {x, w, b},
                 "LinearReluBackward", [](LMP_BW_ARGS) {
-                  const Tensor gt = tops::clamp_backward(out.data(), G, 0.0,
-                                                         std::numeric_limits<double>::max());
-                  if (in[2].requires_grad()) in[2].incr_grad(sba(gt, in[2]));
-                  if (in[0].requires_grad()) in[0].incr_grad_matmul(gt, in[1].data(), false, true);
-                  if (in[1].requires_grad()) in[1].incr_grad_matmul(in[0].data(), gt, true, false);
+                  linear_backward(tops::clamp_backward(out.data(), G, 0.0,
+                                                       std::numeric_limits<double>::max()),
+                                  in);
                 });
 }
 

@@ -61,6 +61,10 @@ class Variable {
   void incr_grad(const Tensor& g);
   // grad += op(a) @ op(b), fused into the GEMM epilogue.
   void incr_grad_matmul(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b);
+  // A Linear's weight and bias gradients together: w.grad += x^T @ g and
+  // b.grad += the column sums of g, in one launch where the backend has the
+  // form (false, nothing done, otherwise).
+  static bool incr_grad_linear(Variable& w, Variable& b, const Tensor& x, const Tensor& g);
   void set_grad_fn(std::shared_ptr<Function> fn);
   void copy(const Variable& other);
   void fill(Scalar value);

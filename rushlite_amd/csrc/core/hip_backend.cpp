@@ -301,6 +301,26 @@ void matmul_acc_hip(TensorImpl& c, const TensorImpl& a, const TensorImpl& b, boo
   gemm_into(c.data(), dt, a, b, ta, tb, s, true);
 }
 
+void matmul_colsum_hip(const TensorImpl& a, const TensorImpl& b, bool ta, bool tb,
+                       TensorImpl& c, bool acc_c, TensorImpl& s, bool acc_s) {
+  const GemmShape sh = gemm_shape(a, b, ta, tb);
+  LMP_CHECK(c.shape().size() == 2 && c.shape()[0] == sh.m && c.shape()[1] == sh.n)
+      << "add_inplace requires tensors with identical shapes";
+  LMP_CHECK(s.numel() == sh.n) << "add_inplace requires tensors with identical shapes";
+  if (!sh.m || !sh.n) return;
+  HostTimer timer(&backend_stats().gemm_host_ns);
+  const void* pa = mut(a);
+  const void* pb = mut(b);
+  void* pc = c.data();
+  void* ps = s.data();
+  count_launch();
+  hip_ok(lmp_k_gemm_colsum_f32(ta, tb, sh.m, sh.n, sh.k, static_cast<const float*>(pa),
+                               a.shape()[1], static_cast<const float*>(pb), b.shape()[1],
+                               static_cast<float*>(pc), sh.n, acc_c ? 1 : 0,
+                               static_cast<float*>(ps), acc_s ? 1 : 0),
+         "lmp_k_gemm_colsum_f32");
+}
+
 TensorImpl linear_hip(const TensorImpl& x, const TensorImpl& w, const TensorImpl& b,
                       bool relu) {
   const GemmShape s = gemm_shape(x, w, false, false);
@@ -396,6 +416,7 @@ LMP_REGISTER_DISPATCH(matmul_stub, kHip, matmul_hip)
 LMP_REGISTER_DISPATCH(matmul_t_stub, kHip, matmul_t_hip)
 LMP_REGISTER_DISPATCH(matmul_acc_stub, kHip, matmul_acc_hip)
 LMP_REGISTER_DISPATCH(linear_stub, kHip, linear_hip)
+LMP_REGISTER_DISPATCH(matmul_colsum_stub, kHip, matmul_colsum_hip)
 LMP_REGISTER_DISPATCH(transpose_stub, kHip, transpose_hip)
 
 }  // namespace lmp::tensor::hip

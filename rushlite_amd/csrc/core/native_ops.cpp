@@ -31,6 +31,7 @@ LMP_DEFINE_DISPATCH(transpose_fn, transpose_stub)
 LMP_DEFINE_DISPATCH(matmul_t_fn, matmul_t_stub)
 LMP_DEFINE_DISPATCH(matmul_acc_fn, matmul_acc_stub)
 LMP_DEFINE_DISPATCH(linear_fn, linear_stub)
+LMP_DEFINE_DISPATCH(matmul_colsum_fn, matmul_colsum_stub)
 
 namespace {
 using Acc = detail::UnsafeTensorAccessor;
@@ -163,6 +164,24 @@ void matmul_acc(Tensor& c, const Tensor& a, const Tensor& b, bool trans_a, bool 
   }
   matmul_acc_stub()(c.device(), *Acc::getImpl(c), *Acc::getImpl(a), *Acc::getImpl(b),
                     trans_a, trans_b);
+}
+
+bool matmul_colsum(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b, Tensor* c,
+                   Tensor* s) {
+  const DeviceType dev = a.device();
+  if (!matmul_colsum_stub().has(dev) || b.device() != dev) return false;
+  const auto f32 = [](const Tensor& t) { return t.type() == DataType::Float32; };
+  if (!f32(a) || !f32(b) || a.shape().size() != 2 || b.shape().size() != 2) return false;
+  if (c->defined() && (!f32(*c) || c->device() != dev)) return false;
+  if (s->defined() && (!f32(*s) || s->device() != dev)) return false;
+  const size_t m = a.shape()[trans_a ? 1 : 0], n = b.shape()[trans_b ? 0 : 1];
+  const bool acc_c = c->defined(), acc_s = s->defined();
+  if (!acc_c)
+    *c = wrap(TensorImpl(Storage(m * n * sizeof(float), dev), {m, n}, DataType::Float32));
+  if (!acc_s) *s = wrap(TensorImpl(Storage(n * sizeof(float), dev), {n}, DataType::Float32));
+  matmul_colsum_stub()(dev, *Acc::getImpl(a), *Acc::getImpl(b), trans_a, trans_b,
+                       *Acc::getImpl(*c), acc_c, *Acc::getImpl(*s), acc_s);
+  return true;
 }
 
 Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b, bool relu) {

@@ -69,6 +69,12 @@ using matmul_acc_fn = void (*)(TensorImpl& c, const TensorImpl&, const TensorImp
 using linear_fn = TensorImpl (*)(const TensorImpl& x, const TensorImpl& w,
                                  const TensorImpl& b, bool relu);
 
+// A Linear's weight and bias gradients in one launch: c (+)= op(a) op(b) and
+// s (+)= the column sums of op(b) (c [m, n], s n values; accumulate when
+// acc_c / acc_s).  Float32 2-D operands only.
+using matmul_colsum_fn = void (*)(const TensorImpl& a, const TensorImpl& b, bool ta, bool tb,
+                                  TensorImpl& c, bool acc_c, TensorImpl& s, bool acc_s);
+
 #define LMP_FOR_BINARY_OPS(_) \
   _(add) _(sub) _(mul) _(div) _(pow) _(eq) _(ne) _(ge) _(le) _(gt) _(lt)
 #define LMP_FOR_UNARY_OPS(_) _(neg) _(exp) _(log) _(sqrt) _(abs) _(sin) _(cos) _(tan)
@@ -99,6 +105,7 @@ LMP_DECLARE_DISPATCH(transpose_fn, transpose_stub)
 LMP_DECLARE_DISPATCH(matmul_t_fn, matmul_t_stub)
 LMP_DECLARE_DISPATCH(matmul_acc_fn, matmul_acc_stub)
 LMP_DECLARE_DISPATCH(linear_fn, linear_stub)
+LMP_DECLARE_DISPATCH(matmul_colsum_fn, matmul_colsum_stub)
 
 Tensor clamp(const Tensor& a, Scalar lo, Scalar hi);
 Tensor abs_backward(const Tensor& input, const Tensor& grad);
@@ -111,6 +118,11 @@ void matmul_acc(Tensor& c, const Tensor& a, const Tensor& b, bool trans_a, bool 
 // x @ w + b (Linear's forward), followed by ReLU when `relu`; one fused GEMM
 // where the backend has one.
 Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b, bool relu = false);
+// *c (+)= op(a) @ op(b) and *s (+)= its column sums of op(b); an undefined *c
+// or *s is allocated and written.  Returns false (and does nothing) where the
+// device has no such form or the dtypes are not float32.
+bool matmul_colsum(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b, Tensor* c,
+                   Tensor* s);
 Tensor transpose(const Tensor& a);
 Tensor reshape(const Tensor& a, std::vector<size_t> shape);
 Tensor squeeze(const Tensor& a, size_t dim);

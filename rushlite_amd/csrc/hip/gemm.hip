@@ -81,6 +81,8 @@ struct GemmArgs {
   const float* bias;   // per-column bias added to the final output (or null)
   int vec_out;         // C (and the bias) take 128-bit stores: n, ldc % 4 == 0, 16-byte aligned
   int relu;            // with a bias: ReLU after it (Linear followed by ReLU)
+  float* colsum;       // tiny kernel only: column sums of op(B) (+)= into it (or null)
+  int colsum_acc;
 };
 
 // Linear's epilogue: v + b, then, when asked, ReLU as the clamp functor
@@ -619,12 +621,36 @@ __global__ __launch_bounds__(256) void gemm_tiny(GemmArgs g) {
     if (j0 + c < j1)
 #pragma unroll
       for (int s = 0; s < 4; ++s) acc = M::step(a[c][s], b[c][s], acc);
+  // Column sums of op(B) (a Linear's bias gradient beside its weight
+  // gradient): the first row of blocks adds the B values its lanes already
+  // hold -- each lane its k values in order, then the lane parts and the
+  // waves in order through LDS.  Sums start from +0, so -0.0 never appears.
+  const bool colsum = g.colsum != nullptr && blockIdx.x == 0;
+  __shared__ float red_cs[4 * 64];
+  if (colsum) {
+    float cs = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kGroups; ++c)
+      if (j0 + c < j1)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) cs += b[c][s];
+    red_cs[wave * 64 + lane] = cs;  // [wave][part q][column li]
+  }
   // Blocks of the four waves summed in wave order: [wave][r][lane].
   constexpr int R = M::kRegs;
   __shared__ float red[4 * R * 64];
 #pragma unroll
   for (int r = 0; r < R; ++r) red[(wave * R + r) * 64 + lane] = acc[r];
   __syncthreads();
+  if (colsum && int(threadIdx.x) < BS) {
+    const int col = n0 + int(threadIdx.x);
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+      for (int qq = 0; qq < 64 / BS; ++qq) v += red_cs[w * 64 + qq * BS + int(threadIdx.x)];
+    if (col < g.n) g.colsum[col] = g.colsum_acc ? g.colsum[col] + v : v;
+  }
 #pragma unroll
   for (int u = 0; u < R / 4; ++u) {
     const int p = int(threadIdx.x) + 256 * u;  // (r, lane) pair
@@ -1233,6 +1259,59 @@ extern "C" int lmp_k_linear_f32(int trans_a, int trans_b, size_t m, size_t n,
                                 float* c, size_t ldc) {
   if (!bias) return fail(LMP_ERR_INVALID, "linear: null bias");
   return gemm_f32_entry(trans_a, trans_b, m, n, k, a, lda, b, ldb, bias, c, ldc, 0);
+}
+
+extern "C" int lmp_k_gemm_colsum_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
+                                     const float* a, size_t lda, const float* b, size_t ldb,
+                                     float* c, size_t ldc, int accumulate, float* colsum,
+                                     int colsum_accumulate) {
+  if (!colsum) return fail(LMP_ERR_INVALID, "gemm_colsum: null column-sum output");
+  if (m == 0 || n == 0 || k == 0 || !a || !b || !c)
+    return fail(LMP_ERR_UNSUPPORTED, "gemm_colsum: empty or null operand");
+  const size_t lim = 0x7fffffff;
+  if (m > lim || n > lim || k > lim || lda > lim || ldb > lim || ldc > lim)
+    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension above 2^31");
+  if ((trans_a ? lda < m : lda < k) || (trans_b ? ldb < k : ldb < n) || ldc < n)
+    return fail(LMP_ERR_INVALID, "gemm: leading dimension too small");
+  GemmArgs g{};
+  g.a = a;
+  g.b = b;
+  g.c = c;
+  g.m = int(m);
+  g.n = int(n);
+  g.k = int(k);
+  g.lda = int(lda);
+  g.ldb = int(ldb);
+  g.ldc = int(ldc);
+  g.accumulate = accumulate ? 1 : 0;
+  g.colsum = colsum;
+  g.colsum_acc = colsum_accumulate ? 1 : 0;
+  if (tiny_ok(g)) {
+    LMP_RUNTIME_OR_FAIL(rt);
+    return trans_a ? (trans_b ? launch_tiny<true, true>(rt, g) : launch_tiny<true, false>(rt, g))
+                   : (trans_b ? launch_tiny<false, true>(rt, g)
+                              : launch_tiny<false, false>(rt, g));
+  }
+  // Larger products: the GEMM, then the column sums of op(B) by the
+  // reduction kernels (contiguous B only), accumulated through a scratch
+  // buffer when asked.
+  if (ldb != (trans_b ? k : n))
+    return fail(LMP_ERR_UNSUPPORTED, "gemm_colsum: strided B on the two-launch path");
+  int rc = gemm_f32_entry(trans_a, trans_b, m, n, k, a, lda, b, ldb, nullptr, c, ldc,
+                          accumulate);
+  if (rc != LMP_OK) return rc;
+  // sum over k of op(B)[k][j]: B [k, n] reduces over its rows, B^T (stored
+  // [n, k]) over its columns.
+  const size_t outer = trans_b ? n : 1, len = k, inner = trans_b ? 1 : n;
+  float* dst = colsum;
+  if (colsum_accumulate) {
+    dst = static_cast<float*>(scratch_alloc(n * sizeof(float)));
+    if (!dst) return LMP_ERR_OOM;
+  }
+  rc = lmp_k_reduce(LMP_RED_SUM, LMP_FLOAT32, dst, b, outer, len, inner);
+  if (rc == LMP_OK && colsum_accumulate) rc = lmp_k_add_inplace(LMP_FLOAT32, colsum, dst, n);
+  if (colsum_accumulate) scratch_free(dst);
+  return rc;
 }
 
 extern "C" int lmp_k_linear_relu_f32(int trans_a, int trans_b, size_t m, size_t n,

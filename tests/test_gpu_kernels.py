@@ -277,6 +277,40 @@ def test_errors_are_reported(hip):
     assert L.lmp_rt_free(C.c_void_p(0xdead00)) == hip.ERR_INVALID
 
 
+# lmp_k_gemm_colsum_f32: a Linear's weight gradient and bias gradient (the
+# column sums of op(B)) together.  C must equal the plain GEMM bit for bit
+# (same kernel), the column sums the float64 sums to the reductions' bar, and
+# accumulation must add the same values in place.  Small products take one
+# launch (the tiny kernel, 16- and 32-wide blocks); (300, 500, 600) runs the
+# GEMM and then the dim-0 reduction.
+@pytest.mark.parametrize("m,n,k", [(256, 64, 32), (64, 10, 32), (40, 33, 7), (512, 300, 12),
+                                   (300, 500, 600)], ids=str)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_colsum(hip, m, n, k, ta, tb):
+    rng = np.random.default_rng(m * 5 + n + k + ta + 2 * tb)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    da = up(hip, a.T.copy() if ta else a)
+    db = up(hip, b.T.copy() if tb else b)
+    plain = hip.gemm(da, db, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    L = hip.lib()
+    c = hip.DeviceBuffer((m, n), np.float32)
+    cs = hip.DeviceBuffer((n,), np.float32)
+    hip.check(L.lmp_k_gemm_colsum_f32(ta, tb, m, n, k, da.ptr, da.shape[1], db.ptr, db.shape[1],
+                                      c.ptr, n, 0, cs.ptr, 0))
+    assert np.array_equal(c.numpy(), plain)
+    sums = cs.numpy()
+    truth = b.astype(np.float64).sum(0)
+    assert np.max(np.abs(sums - truth)) <= 1e-5 * max(1.0, np.max(np.abs(truth)))
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    s0 = rng.standard_normal(n).astype(np.float32)
+    dc, dcs = up(hip, c0), up(hip, s0)
+    hip.check(L.lmp_k_gemm_colsum_f32(ta, tb, m, n, k, da.ptr, da.shape[1], db.ptr, db.shape[1],
+                                      dc.ptr, n, 1, dcs.ptr, 1))
+    assert np.array_equal(dc.numpy(), c0 + plain)
+    assert np.array_equal(dcs.numpy(), s0 + sums)
+
+
 # Short-K products with a large C (write-bound, like config 3's skinny weight
 # gradient): ragged M and N, odd K, K = 1.
 @pytest.mark.parametrize("m,n,k", [(4100, 1030, 31), (2048, 2048, 32), (3000, 1500, 1),
