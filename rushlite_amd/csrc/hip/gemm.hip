@@ -307,6 +307,53 @@ __global__ __launch_bounds__(256) void fold_splits(float* __restrict__ c,
   else *p = bias ? lin_epi(acc, bias[col], relu) : acc;
 }
 
+// The same fold, four adjacent columns per lane (n and ldc multiples of four,
+// C and the bias 16-byte aligned), the split loads issued four at a time; the
+// adds keep split order, so the result equals fold_splits bit for bit.
+__global__ __launch_bounds__(256) void fold_splits4(float* __restrict__ c,
+                                                    const float* __restrict__ part,
+                                                    int m, int n, int ldc,
+                                                    int splits, int accumulate,
+                                                    const float* __restrict__ bias, int relu) {
+  const int64_t i4 = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t mn4 = int64_t(m) * n / 4;
+  if (i4 >= mn4) return;
+  const int64_t i = 4 * i4;
+  const int row = int(i / n), col = int(i - int64_t(row) * n);
+  const v4f* src = reinterpret_cast<const v4f*>(part) + i4;
+  v4f acc = src[0];
+  int s = 1;
+  for (; s + 4 <= splits; s += 4) {
+    v4f x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = src[int64_t(s + u) * mn4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc = acc + x[u];
+  }
+  for (; s < splits; ++s) acc = acc + src[int64_t(s) * mn4];
+  v4f* p = reinterpret_cast<v4f*>(c + int64_t(row) * ldc + col);
+  if (accumulate) *p = *p + acc;
+  else *p = bias ? lin_epi4(acc, *reinterpret_cast<const v4f*>(bias + col), relu) : acc;
+}
+
+bool aligned16(const void* p);
+
+// Adds the split-K partials into C (with the epilogue of the final output).
+int launch_fold(Runtime* rt, float* c, const float* part, int m, int n, int ldc, int splits,
+                int accumulate, const float* bias, int relu) {
+  const int64_t mn = int64_t(m) * n;
+  if (n % 4 == 0 && ldc % 4 == 0 && aligned16(c) && aligned16(part) &&
+      (!bias || aligned16(bias))) {
+    hipLaunchKernelGGL(fold_splits4, dim3(uint32_t((mn / 4 + 255) / 256)), dim3(256), 0,
+                       rt->stream, c, part, m, n, ldc, splits, accumulate, bias, relu);
+  } else {
+    hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
+                       rt->stream, c, part, m, n, ldc, splits, accumulate, bias, relu);
+  }
+  LMP_LAUNCH_CHECK("fold_splits");
+  return LMP_OK;
+}
+
 // ------------------------------------------------------------------ direct
 //
 // Register-direct MFMA kernel for M <= 32 (a Linear layer at a small batch:
@@ -1042,12 +1089,10 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
                        rt->stream, g);
   LMP_LAUNCH_CHECK("gemm_f32_mfma");
   if (splits > 1) {
-    const int64_t mn = int64_t(g.m) * g.n;
-    hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
-                       rt->stream, final_c, part, g.m, g.n, g.ldc, splits,
-                       g.accumulate, g.bias, g.relu);
-    LMP_LAUNCH_CHECK("fold_splits");
-    scratch_free(part);
+    const int frc = launch_fold(rt, final_c, part, g.m, g.n, g.ldc, splits, g.accumulate,
+                                g.bias, g.relu);
+    scratch_free(part);  // stream-ordered: the fold reads it first
+    if (frc != LMP_OK) return frc;
   }
   return LMP_OK;
 }
@@ -1076,12 +1121,10 @@ int launch_lds(Runtime* rt, GemmArgs g) {
                      rt->stream, g);
   LMP_LAUNCH_CHECK("gemm_f32_lds");
   if (splits > 1) {
-    const int64_t mn = int64_t(g.m) * g.n;
-    hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
-                       rt->stream, final_c, part, g.m, g.n, g.ldc, splits,
-                       g.accumulate, g.bias, g.relu);
-    LMP_LAUNCH_CHECK("fold_splits");
-    scratch_free(part);
+    const int frc = launch_fold(rt, final_c, part, g.m, g.n, g.ldc, splits, g.accumulate,
+                                g.bias, g.relu);
+    scratch_free(part);  // stream-ordered: the fold reads it first
+    if (frc != LMP_OK) return frc;
   }
   return LMP_OK;
 }
@@ -1123,12 +1166,10 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
                      d);
   LMP_LAUNCH_CHECK("gemm_direct");
   if (splits > 1) {
-    const int64_t mn = int64_t(g0.m) * g0.n;
-    hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
-                       rt->stream, g0.c, part, g0.m, g0.n, g0.ldc, splits, g0.accumulate,
-                       g0.bias, g0.relu);
-    LMP_LAUNCH_CHECK("fold_splits");
-    scratch_free(part);
+    const int frc = launch_fold(rt, g0.c, part, g0.m, g0.n, g0.ldc, splits, g0.accumulate,
+                                g0.bias, g0.relu);
+    scratch_free(part);  // stream-ordered: the fold reads it first
+    if (frc != LMP_OK) return frc;
   }
   return LMP_OK;
 }
