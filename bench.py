@@ -294,6 +294,10 @@ def mlp_bench(rsl, abi, dims, batch, steps, onehot, graph=False, fused_update=Fa
         with rsl.capture_on(fused_update):
             for name, p in list(model.named_parameters()):
                 model.params[name] = rsl.Variable(p.data - 1e-3 * p.grad, requires_grad=True)
+        if fused_update and not graph:
+            # the pending updates together (one kernel for the independent
+            # ones); a graph capture does this for the carried parameters
+            rsl.realize_all(p for _, p in model.named_parameters())
         loss.realize()
         return loss
 

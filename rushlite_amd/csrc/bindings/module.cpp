@@ -426,6 +426,55 @@ PYBIND11_MODULE(_C, m) {
     dst.copy(src);
     return false;
   });
+  // Realises every pending tensor of `items` (Variables or tensors) together:
+  // on the HIP device their elementwise regions (an optimizer's per-parameter
+  // updates) run as one kernel where they are independent.
+  m.def("realize_all", [](const py::iterable& items) {
+    std::vector<Tensor> keep;
+    std::vector<lmp::tensor::TensorImpl*> roots;
+    for (const py::handle& h : items) {
+      Tensor t = py::isinstance<Variable>(h) ? h.cast<Variable>().data() : h.cast<Tensor>();
+      auto impl = lmp::tensor::detail::UnsafeTensorAccessor::getImpl(t);
+      if (!impl->is_deferred()) continue;
+      roots.push_back(impl.get());
+      keep.push_back(t);
+    }
+    lmp::tensor::lazy::realize_many(roots, {});
+  });
+  // _realize_into for many pairs at once (one grouped kernel for the pending
+  // elementwise sources that can be computed in place); returns, per pair,
+  // whether src now shares dst's buffer.
+  m.def("_realize_into_many", [](std::vector<Tensor> dsts, std::vector<Tensor> srcs) {
+    LMP_CHECK(dsts.size() == srcs.size()) << "realize_into: one source per destination";
+    std::vector<lmp::tensor::TensorImpl*> roots;
+    std::vector<lmp::tensor::Storage> stores;
+    stores.reserve(dsts.size());
+    for (size_t i = 0; i < dsts.size(); ++i) {
+      auto di = lmp::tensor::detail::UnsafeTensorAccessor::getImpl(dsts[i]);
+      auto si = lmp::tensor::detail::UnsafeTensorAccessor::getImpl(srcs[i]);
+      LMP_CHECK(di->numel() == si->numel() && di->type() == si->type() &&
+                di->device() == si->device())
+          << "realize_into: tensors differ in size, dtype or device";
+      dsts[i].realize();
+      stores.push_back(di->storage());
+    }
+    std::vector<const lmp::tensor::Storage*> targets;
+    for (size_t i = 0; i < srcs.size(); ++i) {
+      auto si = lmp::tensor::detail::UnsafeTensorAccessor::getImpl(srcs[i]);
+      if (!si->is_deferred() || si->device() != DeviceType::HIP) continue;
+      roots.push_back(si.get());
+      targets.push_back(&stores[i]);
+    }
+    if (!roots.empty()) lmp::tensor::lazy::realize_many(roots, targets);
+    std::vector<bool> shared;
+    for (size_t i = 0; i < srcs.size(); ++i) {
+      auto si = lmp::tensor::detail::UnsafeTensorAccessor::getImpl(srcs[i]);
+      const bool same = si->raw() == stores[i].data();
+      if (!same) dsts[i].copy(srcs[i]);
+      shared.push_back(same);
+    }
+    return shared;
+  });
   m.def("_storage_ptr", [](const Tensor& t) {
     return reinterpret_cast<uintptr_t>(
         lmp::tensor::detail::UnsafeTensorAccessor::getImpl(t)->raw());

@@ -26,6 +26,7 @@
 // device synchronisation (the reference synchronises every launch,
 // nvrtc_backend.cpp:135-141).
 #include <cstdio>
+#include <functional>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -476,15 +477,76 @@ __device__ __forceinline__ double lmp_clamp(double x, double lo, double hi) {
 }
 )";
 
-// Kernel signature: the root's output, the interior outputs xo0.., the leaves.
+// Parameter names of one region in a kernel: its root output, the prefix of
+// its interior outputs (xo0, ..) and of its leaves (in0, ..).  A kernel that
+// runs several regions gives each its own names.
+struct Names {
+  std::string out, xo, in;
+};
+const Names kSingle{"out", "xo", "in"};
+Names region_names(size_t i) {
+  const std::string t = std::to_string(i);
+  return {"out_" + t, "xo_" + t + "_", "in_" + t + "_"};
+}
+
+// One region's parameters: the root's output, the interior outputs, the leaves.
+void emit_region_params(std::ostringstream& os, const Region& r, const char* T,
+                        const Names& nm, bool first) {
+  os << (first ? "" : ", ") << T << "* __restrict__ " << nm.out;
+  for (size_t k = 0; k < r.outputs.size(); ++k) os << ", " << T << "* __restrict__ " << nm.xo << k;
+  for (size_t l = 0; l < r.leaves.size(); ++l)
+    os << ", const " << T << "* __restrict__ " << nm.in << l;
+}
+
 void emit_params(std::ostringstream& os, const Region& r, const std::string& name,
                  const char* T) {
-  os << "extern \"C\" __global__ __launch_bounds__(" << kBlock << ") void " << name
-     << "(" << T << "* __restrict__ out";
-  for (size_t k = 0; k < r.outputs.size(); ++k) os << ", " << T << "* __restrict__ xo" << k;
-  for (size_t l = 0; l < r.leaves.size(); ++l)
-    os << ", const " << T << "* __restrict__ in" << l;
+  os << "extern \"C\" __global__ __launch_bounds__(" << kBlock << ") void " << name << "(";
+  emit_region_params(os, r, T, kSingle, true);
   os << ") {\n";
+}
+
+// The body of a float4 (vec) region: block `block` owns output float4s
+// [256 * block, 256 * block + 256) (one-shot).
+void emit_vec_body(std::ostringstream& os, const Region& r, const Plan& p, const Names& nm,
+                   const std::string& block) {
+  const size_t nl = r.leaves.size();
+  const bool rows = p.groups.size() == 2;
+  os << "  {\n  const unsigned v = " << block << " * " << kBlock << "u + threadIdx.x;\n";
+  os << "  if (v < " << p.nvec << "u) {\n";
+  if (rows) {
+    os << "  const unsigned r = v / " << p.cols4 << "u;\n";
+    os << "  const unsigned c = (v - r * " << p.cols4 << "u) * 4u;\n";
+  } else {
+    os << "  const unsigned r = 0u;\n  const unsigned c = v * 4u;\n";
+  }
+  for (size_t l = 0; l < nl; ++l) {
+    const bool contig = !p.groups.empty() && p.groups[0].stride[l] == 1;
+    const int64_t rs = rows ? p.groups[1].stride[l] : 0;
+    if (contig)
+      os << "  const lmp_v4 s" << l << " = *reinterpret_cast<const lmp_v4*>(" << nm.in << l
+         << " + (unsigned long)r * " << rs << "ul + c);\n";
+    else
+      os << "  const float s" << l << " = " << nm.in << l << "[(unsigned long)r * " << rs
+         << "ul];\n";
+  }
+  os << "  lmp_v4 o;\n";
+  for (size_t k = 0; k < r.outputs.size(); ++k) os << "  lmp_v4 x" << k << ";\n";
+  const char* comp[4] = {"x", "y", "z", "w"};
+  for (int c = 0; c < 4; ++c) {
+    os << "  {\n";
+    emit_chain(os, r, "    ", std::string("o.") + comp[c], "float", [&](int l) {
+      const bool contig = !p.groups.empty() && p.groups[0].stride[l] == 1;
+      return "s" + std::to_string(l) + (contig ? std::string(".") + comp[c] : "");
+    });
+    for (size_t k = 0; k < r.outputs.size(); ++k)
+      os << "    x" << k << "." << comp[c] << " = t" << r.node_of.at(r.outputs[k]) << ";\n";
+    os << "  }\n";
+  }
+  for (size_t k = 0; k < r.outputs.size(); ++k)
+    os << "  __builtin_nontemporal_store(x" << k << ", reinterpret_cast<lmp_v4*>(" << nm.xo << k
+       << ") + v);\n";
+  os << "  __builtin_nontemporal_store(o, reinterpret_cast<lmp_v4*>(" << nm.out << ") + v);\n";
+  os << "  }\n  }\n";
 }
 
 std::string codegen(const Region& r, const Plan& p, const std::string& name, bool f64) {
@@ -494,43 +556,8 @@ std::string codegen(const Region& r, const Plan& p, const std::string& name, boo
   emit_params(os, r, name, T);
   const size_t nl = r.leaves.size();
   if (p.vec) {
-    // One-shot: workgroup b owns output float4s [256b, 256b + 256).
-    const bool rows = p.groups.size() == 2;
-    os << "  const unsigned v = blockIdx.x * " << kBlock << "u + threadIdx.x;\n";
-    os << "  if (v >= " << p.nvec << "u) return;\n";
-    if (rows) {
-      os << "  const unsigned r = v / " << p.cols4 << "u;\n";
-      os << "  const unsigned c = (v - r * " << p.cols4 << "u) * 4u;\n";
-    } else {
-      os << "  const unsigned r = 0u;\n  const unsigned c = v * 4u;\n";
-    }
-    for (size_t l = 0; l < nl; ++l) {
-      const bool contig = !p.groups.empty() && p.groups[0].stride[l] == 1;
-      const int64_t rs = rows ? p.groups[1].stride[l] : 0;
-      if (contig)
-        os << "  const lmp_v4 s" << l << " = *reinterpret_cast<const lmp_v4*>(in" << l
-           << " + (unsigned long)r * " << rs << "ul + c);\n";
-      else
-        os << "  const float s" << l << " = in" << l << "[(unsigned long)r * " << rs
-           << "ul];\n";
-    }
-    os << "  lmp_v4 o;\n";
-    for (size_t k = 0; k < r.outputs.size(); ++k) os << "  lmp_v4 x" << k << ";\n";
-    const char* comp[4] = {"x", "y", "z", "w"};
-    for (int c = 0; c < 4; ++c) {
-      os << "  {\n";
-      emit_chain(os, r, "    ", std::string("o.") + comp[c], T, [&](int l) {
-        const bool contig = !p.groups.empty() && p.groups[0].stride[l] == 1;
-        return "s" + std::to_string(l) + (contig ? std::string(".") + comp[c] : "");
-      });
-      for (size_t k = 0; k < r.outputs.size(); ++k)
-        os << "    x" << k << "." << comp[c] << " = t" << r.node_of.at(r.outputs[k]) << ";\n";
-      os << "  }\n";
-    }
-    for (size_t k = 0; k < r.outputs.size(); ++k)
-      os << "  __builtin_nontemporal_store(x" << k << ", reinterpret_cast<lmp_v4*>(xo" << k
-         << ") + v);\n";
-    os << "  __builtin_nontemporal_store(o, reinterpret_cast<lmp_v4*>(out) + v);\n}\n";
+    emit_vec_body(os, r, p, kSingle, "blockIdx.x");
+    os << "}\n";
   } else {
     os << "  const unsigned long n = " << p.n << "ul;\n";
     os << "  for (unsigned long i = (unsigned long)blockIdx.x * " << kBlock
@@ -554,6 +581,59 @@ std::string codegen(const Region& r, const Plan& p, const std::string& name, boo
       os << "      xo" << k << "[i] = t" << r.node_of.at(r.outputs[k]) << ";\n";
     os << "    }\n    out[i] = res;\n  }\n}\n";
   }
+  return os.str();
+}
+
+// The body of an indexed region run one-shot: block `block` owns elements
+// [256 * block, 256 * block + 256), each decomposed into leaf offsets with
+// compile-time extents and strides.
+void emit_indexed_body(std::ostringstream& os, const Region& r, const Plan& p, const char* T,
+                       const Names& nm, const std::string& block) {
+  const size_t nl = r.leaves.size();
+  os << "  {\n  const unsigned long i = (unsigned long)" << block << " * " << kBlock
+     << "u + threadIdx.x;\n";
+  os << "  if (i < " << p.n << "ul) {\n";
+  os << "    unsigned long rest = i;\n";
+  for (size_t l = 0; l < nl; ++l) os << "    unsigned long o" << l << " = 0;\n";
+  for (size_t g = 0; g < p.groups.size(); ++g) {
+    os << "    {\n      const unsigned long q = rest / " << p.groups[g].extent
+       << "ul;\n      const unsigned long c = rest - q * " << p.groups[g].extent
+       << "ul;\n      rest = q;\n";
+    for (size_t l = 0; l < nl; ++l)
+      if (p.groups[g].stride[l])
+        os << "      o" << l << " += c * " << p.groups[g].stride[l] << "ul;\n";
+    os << "    }\n";
+  }
+  os << "    " << T << " res;\n    {\n";
+  emit_chain(os, r, "      ", "res", T, [&](int l) {
+    return nm.in + std::to_string(l) + "[o" + std::to_string(l) + "]";
+  });
+  for (size_t k = 0; k < r.outputs.size(); ++k)
+    os << "      " << nm.xo << k << "[i] = t" << r.node_of.at(r.outputs[k]) << ";\n";
+  os << "    }\n    " << nm.out << "[i] = res;\n  }\n  }\n";
+}
+
+// One kernel for several independent elementwise regions (realize_all):
+// region i owns workgroups [off_i, off_i + blocks_i), float4 lanes for a vec
+// plan, one element per lane otherwise.
+std::string codegen_multi(const std::vector<const Region*>& rs, const std::vector<const Plan*>& ps,
+                          const std::vector<bool>& f64, const std::vector<uint64_t>& blocks,
+                          const std::string& name) {
+  std::ostringstream os;
+  os << kPrelude;
+  os << "extern \"C\" __global__ __launch_bounds__(" << kBlock << ") void " << name << "(";
+  for (size_t i = 0; i < rs.size(); ++i)
+    emit_region_params(os, *rs[i], f64[i] ? "double" : "float", region_names(i), i == 0);
+  os << ") {\n";
+  uint64_t off = 0;
+  for (size_t i = 0; i < rs.size(); ++i) {
+    os << (i ? "  else " : "  ") << "if (blockIdx.x < " << off + blocks[i] << "u)\n";
+    const std::string block = "(blockIdx.x - " + std::to_string(off) + "u)";
+    if (ps[i]->vec) emit_vec_body(os, *rs[i], *ps[i], region_names(i), block);
+    else emit_indexed_body(os, *rs[i], *ps[i], f64[i] ? "double" : "float", region_names(i), block);
+    off += blocks[i];
+  }
+  os << "}\n";
   return os.str();
 }
 
@@ -724,74 +804,188 @@ struct Compiled {
 // by the root's realize() before any leaf is realised.
 thread_local const Storage* t_target = nullptr;
 
+// A region ready to launch: settled (leaves realised), outputs allocated.
+struct Job {
+  TensorImpl* root = nullptr;
+  Region r;
+  RowPlan rp;
+  Plan p;
+  bool f64 = false;
+  std::vector<size_t> shape;
+  Storage out{0, DeviceType::HIP};  // empty until prepare() allocates or takes a target
+  std::vector<Storage> extra;
+  // One lane per float4 (vec, one-shot), per row wave, or per element
+  // (grid-stride loop, one-shot up to 2^30 workgroups).
+  uint64_t blocks() const {
+    const uint64_t work = rp.ok ? uint64_t(rp.R) * 64 : p.vec ? p.nvec : p.n;
+    const uint64_t grid = (work + kBlock - 1) / kBlock;
+    return std::max<uint64_t>(1, std::min<uint64_t>(grid, uint64_t(1) << 30));
+  }
+  // Workgroups when run inside a group (one-shot for the indexed plan too).
+  uint64_t group_blocks() const {
+    const uint64_t work = p.vec ? p.nvec : p.n;
+    return std::max<uint64_t>(1, (work + kBlock - 1) / kBlock);
+  }
+  void push_args(std::vector<void*>& ptrs) const {
+    ptrs.push_back(out.data());
+    for (const Storage& x : extra) ptrs.push_back(x.data());
+    for (TensorImpl* leaf : r.leaves) ptrs.push_back(leaf->raw());
+  }
+  void finish() {
+    for (size_t k = 0; k < r.outputs.size(); ++k) r.outputs[k]->set_realized(extra[k]);
+    root->set_realized(out);
+  }
+};
+
+void run_eager_root(TensorImpl* root) {
+  for (const auto& in : root->lazy_op()->inputs) in->data();
+  root->lazy_op()->run_eager(*root);
+}
+
 class HipFusionBackend : public lazy::LazyBackend {
  public:
   void realize(TensorImpl* root) override {
-    // Host time of outermost realisations only (nested ones are inside).
-    thread_local int depth = 0;
-    struct Depth {
-      int& d;
-      ~Depth() { --d; }
-    } guard{++depth};
-    HostTimer timer(depth == 1 ? &backend_stats().fused_host_ns : nullptr);
-    realize_region(root);
+    HostScope scope;
+    const Storage* target = t_target;
+    t_target = nullptr;
+    Job job;
+    if (prepare(root, target, job)) launch_single(job);
+  }
+
+  // Several roots at once: the elementwise regions among them (an optimizer's
+  // per-parameter updates) run as one kernel when their regions are
+  // disjoint; row kernels, or all of them when regions overlap, are realised
+  // one by one.  targets[i], when not null, is root i's realize_into buffer.
+  void realize_many(const std::vector<TensorImpl*>& roots,
+                    const std::vector<const Storage*>& targets) override {
+    HostScope scope;
+    std::vector<Job> jobs;
+    jobs.reserve(roots.size());
+    std::vector<size_t> job_root;
+    for (size_t i = 0; i < roots.size(); ++i) {
+      Job job;
+      if (prepare(roots[i], targets[i], job)) {
+        jobs.push_back(std::move(job));
+        job_root.push_back(i);
+      }
+    }
+    // Groupable when every region's nodes are still pending, pairwise
+    // disjoint, and hold no other job's root.
+    std::unordered_set<TensorImpl*> seen;
+    bool ok = true;
+    for (const Job& j : jobs) {
+      for (TensorImpl* n : j.r.nodes) {
+        ok &= n->is_deferred() && seen.insert(n).second;
+      }
+    }
+    if (!ok) {
+      // Overlapping regions: realise each on its own, from scratch.
+      jobs.clear();
+      for (size_t i = 0; i < roots.size(); ++i) {
+        if (!roots[i]->is_deferred()) continue;
+        t_target = targets[i];
+        realize_region_outer(roots[i]);
+      }
+      return;
+    }
+    std::vector<Job*> group;
+    size_t params = 0;
+    const auto flush = [&] {
+      if (group.size() == 1) launch_single(*group[0]);
+      else if (!group.empty()) launch_group(group);
+      group.clear();
+      params = 0;
+    };
+    for (Job& j : jobs) {
+      const size_t np = 1 + j.r.outputs.size() + j.r.leaves.size();
+      // Row kernels, and regions large enough to fill the chip on their own
+      // (2^20 workgroups is far past that), launch alone.
+      if (j.rp.ok || j.group_blocks() > (uint64_t(1) << 20)) {
+        launch_single(j);
+        continue;
+      }
+      if (group.size() == kMaxGroup || params + np > kMaxGroupParams) flush();
+      group.push_back(&j);
+      params += np;
+    }
+    flush();
   }
 
  private:
-  void realize_region(TensorImpl* root) {
-    const Storage* target = t_target;
-    t_target = nullptr;
-    if (!root->is_deferred()) return;
-    if (!fusible_node(root)) {
-      for (const auto& in : root->lazy_op()->inputs) in->data();
-      root->lazy_op()->run_eager(*root);
-      return;
+  static constexpr size_t kMaxGroup = 16;
+  static constexpr size_t kMaxGroupParams = 96;
+
+  // Host time of outermost realisations only (nested ones are inside).
+  struct HostScope {
+    static int& depth() {
+      thread_local int d = 0;
+      return d;
     }
-    const Region r = settle_region(root);
+    HostTimer timer;
+    HostScope() : timer(++depth() == 1 ? &backend_stats().fused_host_ns : nullptr) {}
+    ~HostScope() { --depth(); }
+  };
+
+  void realize_region_outer(TensorImpl* root) { realize(root); }
+
+  // Settles root's region and allocates its outputs (true), or realises root
+  // without a fused kernel (false): not pending, not fusible, constants only,
+  // a reduction no row kernel takes, or an empty output.
+  bool prepare(TensorImpl* root, const Storage* target, Job& job) {
+    if (!root->is_deferred()) return false;
+    if (!fusible_node(root)) {
+      run_eager_root(root);
+      return false;
+    }
+    job.root = root;
+    job.r = settle_region(root);
+    const Region& r = job.r;
     if (r.leaves.empty()) {
       if (fusion_log())
-        std::fprintf(stderr, "[lmp fusion] eager constants root %s\n", shape_text(root->shape()).c_str());
+        std::fprintf(stderr, "[lmp fusion] eager constants root %s\n",
+                     shape_text(root->shape()).c_str());
       // Constants only (a fill, or arithmetic on fills): eager.
-      for (const auto& in : root->lazy_op()->inputs) in->data();
-      root->lazy_op()->run_eager(*root);
-      return;
+      run_eager_root(root);
+      return false;
     }
-    const bool f64 = root->type() == DataType::Float64;
-    const RowPlan rp = row_plan(r);
-    if (is_reduce(root) && !rp.ok) {
+    job.f64 = root->type() == DataType::Float64;
+    job.rp = row_plan(r);
+    if (is_reduce(root) && !job.rp.ok) {
       if (fusion_log())
-        std::fprintf(stderr, "[lmp fusion] eager reduce root %s\n", shape_text(root->shape()).c_str());
+        std::fprintf(stderr, "[lmp fusion] eager reduce root %s\n",
+                     shape_text(root->shape()).c_str());
       // A reduction no row kernel can take (long rows, other layouts): eager.
-      for (const auto& in : root->lazy_op()->inputs) in->data();
-      root->lazy_op()->run_eager(*root);
-      return;
+      run_eager_root(root);
+      return false;
     }
-    const std::vector<size_t> shape = root->shape();
-    const size_t n = shape_numel(shape);
+    job.shape = root->shape();
+    const size_t n = shape_numel(job.shape);
     // Writing into the target is safe when every leaf stored there is read at
     // the output's own index: same shape, elementwise region.
-    bool in_place = target && target->byte_size() == n * dtype_size(root->type()) && !rp.ok;
+    bool in_place =
+        target && target->byte_size() == n * dtype_size(root->type()) && !job.rp.ok;
     if (in_place) {
       for (TensorImpl* leaf : r.leaves)
-        if (leaf->raw() == target->data() && leaf->shape() != shape) in_place = false;
+        if (leaf->raw() == target->data() && leaf->shape() != job.shape) in_place = false;
     }
-    Storage out = in_place ? *target : Storage(n * dtype_size(root->type()), DeviceType::HIP);
-    std::vector<Storage> extra;
-    extra.reserve(r.outputs.size());
+    job.out = in_place ? *target : Storage(n * dtype_size(root->type()), DeviceType::HIP);
+    job.extra.reserve(r.outputs.size());
     for (TensorImpl* x : r.outputs)
-      extra.emplace_back(shape_numel(x->shape()) * dtype_size(x->type()), DeviceType::HIP);
+      job.extra.emplace_back(shape_numel(x->shape()) * dtype_size(x->type()), DeviceType::HIP);
     if (n == 0) {
-      for (size_t k = 0; k < r.outputs.size(); ++k) r.outputs[k]->set_realized(extra[k]);
-      root->set_realized(out);
-      return;
+      job.finish();
+      return false;
     }
-    const Plan p = make_plan(r, shape, f64);
-    std::vector<int64_t> sig = signature(r, shape, p, f64, rp);
+    job.p = make_plan(r, job.shape, job.f64);
+    return true;
+  }
+
+  void* compiled(std::vector<int64_t> sig, const std::function<std::string()>& source) {
     const uint64_t key = sig_hash(sig);
     void* handle = lookup(key, sig);
     if (!handle) {
       const std::string name = "lmp_fused";
-      const std::string src = rp.ok ? codegen_rows(r, rp, name, f64) : codegen(r, p, name, f64);
+      const std::string src = source();
       hip_ok(lmp_jit_compile(key, src.c_str(), name.c_str(), &handle), "lmp_jit_compile");
       std::lock_guard<std::mutex> lock(mu_);
       cache_[key] = Compiled{handle, std::move(sig)};
@@ -799,28 +993,65 @@ class HipFusionBackend : public lazy::LazyBackend {
     } else {
       ++backend_stats().jit_cache_hits;
     }
-    // Launch: one lane per float4 (vec, one-shot) or per element (grid-stride
-    // loop, one-shot up to 2^30 workgroups).
-    const uint64_t work = rp.ok ? uint64_t(rp.R) * 64 : p.vec ? p.nvec : p.n;
-    uint64_t grid = (work + kBlock - 1) / kBlock;
-    grid = std::max<uint64_t>(1, std::min<uint64_t>(grid, uint64_t(1) << 30));
-    std::vector<void*> ptrs;
-    ptrs.reserve(r.leaves.size() + r.outputs.size() + 1);
-    ptrs.push_back(out.data());
-    for (const Storage& x : extra) ptrs.push_back(x.data());
-    for (TensorImpl* leaf : r.leaves) ptrs.push_back(leaf->raw());
+    return handle;
+  }
+
+  void launch(void* handle, uint64_t grid, std::vector<void*>& ptrs) {
     std::vector<void*> args(ptrs.size());
     for (size_t i = 0; i < ptrs.size(); ++i) args[i] = &ptrs[i];
     hip_ok(lmp_jit_launch(handle, static_cast<uint32_t>(grid), kBlock, args.data()),
            "lmp_jit_launch");
     ++backend_stats().fused_launches;
+  }
+
+  void launch_single(Job& job) {
+    const Region& r = job.r;
+    void* handle = compiled(signature(r, job.shape, job.p, job.f64, job.rp), [&] {
+      return job.rp.ok ? codegen_rows(r, job.rp, "lmp_fused", job.f64)
+                       : codegen(r, job.p, "lmp_fused", job.f64);
+    });
+    std::vector<void*> ptrs;
+    ptrs.reserve(r.leaves.size() + r.outputs.size() + 1);
+    job.push_args(ptrs);
+    launch(handle, job.blocks(), ptrs);
     backend_stats().fused_nodes += r.nodes.size();
     if (fusion_log())
       std::fprintf(stderr, "[lmp fusion] %s root %s nodes %zu leaves %zu outputs %zu\n",
-                   rp.ok ? "rows" : p.vec ? "vec" : "indexed", shape_text(shape).c_str(),
-                   r.nodes.size(), r.leaves.size(), r.outputs.size());
-    for (size_t k = 0; k < r.outputs.size(); ++k) r.outputs[k]->set_realized(extra[k]);
-    root->set_realized(out);
+                   job.rp.ok ? "rows" : job.p.vec ? "vec" : "indexed",
+                   shape_text(job.shape).c_str(), r.nodes.size(), r.leaves.size(),
+                   r.outputs.size());
+    job.finish();
+  }
+
+  void launch_group(const std::vector<Job*>& group) {
+    std::vector<int64_t> sig{0x4c4d504d, static_cast<int64_t>(group.size())};
+    std::vector<const Region*> rs;
+    std::vector<const Plan*> ps;
+    std::vector<bool> f64;
+    std::vector<uint64_t> blocks;
+    uint64_t grid = 0;
+    size_t nodes = 0;
+    for (const Job* j : group) {
+      const std::vector<int64_t> one = signature(j->r, j->shape, j->p, j->f64, j->rp);
+      sig.push_back(static_cast<int64_t>(one.size()));
+      sig.insert(sig.end(), one.begin(), one.end());
+      rs.push_back(&j->r);
+      ps.push_back(&j->p);
+      f64.push_back(j->f64);
+      blocks.push_back(j->group_blocks());
+      grid += j->group_blocks();
+      nodes += j->r.nodes.size();
+    }
+    void* handle = compiled(std::move(sig),
+                            [&] { return codegen_multi(rs, ps, f64, blocks, "lmp_fused"); });
+    std::vector<void*> ptrs;
+    for (const Job* j : group) j->push_args(ptrs);
+    launch(handle, grid, ptrs);
+    backend_stats().fused_nodes += nodes;
+    if (fusion_log())
+      std::fprintf(stderr, "[lmp fusion] group of %zu regions, %zu nodes\n", group.size(),
+                   nodes);
+    for (Job* j : group) j->finish();
   }
 
  private:

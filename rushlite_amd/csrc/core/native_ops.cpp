@@ -486,6 +486,25 @@ void realize(TensorImpl* t) {
   b->realize(t);
 }
 
+void realize_many(const std::vector<TensorImpl*>& roots,
+                  const std::vector<const Storage*>& targets) {
+  LMP_CHECK(targets.empty() || targets.size() == roots.size())
+      << "realize_many: one target per root";
+  std::vector<TensorImpl*> pending;
+  std::vector<const Storage*> tg;
+  for (size_t i = 0; i < roots.size(); ++i) {
+    if (!roots[i]->is_deferred()) continue;
+    LMP_CHECK(roots[i]->device() == roots.front()->device())
+        << "realize_many: tensors on different devices";
+    pending.push_back(roots[i]);
+    tg.push_back(targets.empty() ? nullptr : targets[i]);
+  }
+  if (pending.empty()) return;
+  LazyBackend* b = backend(pending.front()->device());
+  LMP_CHECK(b != nullptr) << "no lazy backend registered for device";
+  b->realize_many(pending, tg);
+}
+
 std::shared_ptr<LazyFunction> make_binary(int code, std::shared_ptr<TensorImpl> a,
                                           std::shared_ptr<TensorImpl> b, Scalar p0,
                                           Scalar p1) {

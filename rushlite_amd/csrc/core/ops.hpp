@@ -204,12 +204,25 @@ struct LazyFunction {
 struct LazyBackend {  // lazy_backend.hpp:15-35
   virtual ~LazyBackend() = default;
   virtual void realize(TensorImpl* t) = 0;
+  // Several pending tensors at once (e.g. an optimizer's parameter updates);
+  // targets[i], when not null, is a buffer root i may be computed straight
+  // into (as realize_into).  The default realises them one by one.
+  virtual void realize_many(const std::vector<TensorImpl*>& roots,
+                            const std::vector<const Storage*>& targets) {
+    (void)targets;
+    for (TensorImpl* t : roots)
+      if (t->is_deferred()) realize(t);
+  }
 };
 LazyBackend* backend(DeviceType dev);
 void register_backend(DeviceType dev, LazyBackend* b);
 
 std::shared_ptr<TensorImpl> record(std::shared_ptr<LazyFunction> fn);
 void realize(TensorImpl* t);
+// Realises every pending tensor of `roots` (all on one device) through its
+// backend's realize_many; `targets` is empty or one entry (or null) per root.
+void realize_many(const std::vector<TensorImpl*>& roots,
+                  const std::vector<const Storage*>& targets);
 
 // p0/p1 are clamp backward's bounds (LMP_BIN_CLAMP_BACKWARD).
 std::shared_ptr<LazyFunction> make_binary(int code,

@@ -77,16 +77,20 @@ class Graph:
         try:
             yield self
             after = _snapshot(carry)
+            dsts, srcs = [], []
             for name, old in before.items():
                 new = after.get(name)
                 if new is None or new is old:
                     continue
                 src, dst = new.data, old.data
                 if _C._storage_ptr(src) != _C._storage_ptr(dst):
-                    # A pending fused update (made under capture_on) is
-                    # computed straight into the old buffer; anything else is
-                    # copied there.
-                    _C._realize_into(dst, src)
+                    dsts.append(dst)
+                    srcs.append(src)
+            if dsts:
+                # Pending fused updates (made under capture_on) are computed
+                # straight into the old buffers, together in one kernel where
+                # they are independent; anything else is copied there.
+                _C._realize_into_many(dsts, srcs)
             self._g.end()
         except BaseException:
             self._g.abort()

@@ -732,6 +732,59 @@ def test_long_held_chain_splits_into_few_regions(rsl):
         assert np.array_equal(t.numpy().view(np.uint32), w.view(np.uint32)), i
 
 
+def test_realize_all_groups_independent_updates(rsl):
+    """realize_all runs the pending elementwise updates of several tensors
+    (different shapes, float4 and indexed plans, float32 and float64, as an
+    optimizer's per-parameter p - lr * g) as one kernel, each equal to
+    realising it alone; a row reduction among them runs on its own, and
+    updates sharing a pending subexpression fall back to one by one."""
+    rng = np.random.default_rng(23)
+    shapes = [(256, 64), (64,), (64, 10), (10,), (33, 7)]
+    ps = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
+    gs = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
+
+    def updates(dt=np.float32):
+        out = []
+        rdt = rsl.dtype.float64 if dt == np.float64 else rsl.dtype.float32
+        for p_np, g_np in zip(ps, gs):
+            p, g = rsl.Variable(p_np.astype(dt), dtype=rdt), rsl.Variable(g_np.astype(dt), dtype=rdt)
+            with rsl.capture_on():
+                out.append(p - 1e-3 * g)
+        return out
+
+    want = [u.numpy() for u in updates()]
+    want64 = [u.numpy() for u in updates(np.float64)]
+    got = updates()
+    s0 = rsl._stats()["fused_launches"]
+    rsl.realize_all(got)
+    assert rsl._stats()["fused_launches"] - s0 == 1
+    for g, w in zip(got, want):
+        assert not rsl._is_deferred(g)
+        assert np.array_equal(g.numpy().view(np.uint32), w.view(np.uint32))
+    # float64 updates join the group; a row reduction runs on its own
+    mixed = updates() + updates(np.float64)
+    x = rsl.Variable(rng.standard_normal((8, 30)).astype(np.float32))
+    with rsl.capture_on():
+        row = rsl.sum(x * 2.0, 1)
+    want_row = rsl.sum(x * 2.0, 1).numpy()
+    s0 = rsl._stats()["fused_launches"]
+    rsl.realize_all(mixed + [row])
+    assert rsl._stats()["fused_launches"] - s0 == 2
+    for g, w in zip(mixed[:len(shapes)], want):
+        assert np.array_equal(g.numpy().view(np.uint32), w.view(np.uint32))
+    for g, w in zip(mixed[len(shapes):], want64):
+        assert np.array_equal(g.numpy().view(np.uint64), w.view(np.uint64))
+    assert np.array_equal(row.numpy(), want_row)
+    # two roots sharing a pending value: realised one by one, still correct
+    a = rsl.Variable(ps[0])
+    with rsl.capture_on():
+        t = a * 3.0
+        r1, r2 = t + 1.0, t - 1.0
+    rsl.realize_all([r1, r2])
+    assert np.array_equal(r1.numpy(), (ps[0] * np.float32(3)) + np.float32(1))
+    assert np.array_equal(r2.numpy(), (ps[0] * np.float32(3)) - np.float32(1))
+
+
 def test_leaf_region_storing_a_shared_node(rsl):
     """Rows of 4096 are too long for a row kernel, so the row sum L below is a
     leaf of c's region, and realising it first reaches n, which c's region
