@@ -62,6 +62,16 @@ void Variable::zero_grad() {
 }
 
 namespace {
+// A pending constant (a fill node, float32 or float64): its value as the
+// tensor holds it.
+bool pending_fill(const Tensor& t, Scalar* value) {
+  const auto& ti = tensor::detail::UnsafeTensorAccessor::getImpl(t);
+  if (!ti->is_deferred() || ti->lazy_op()->kind() != tensor::lazy::OpKind::Fill) return false;
+  const Scalar v = ti->lazy_op()->param0();
+  *value = t.type() == DataType::Float32 ? Scalar(float(v)) : v;
+  return true;
+}
+
 // Per-(device, dtype) [1] zero used to start a deferred gradient as 0 + g.
 const Tensor& zero_scalar(DeviceType dev, DataType dt) {
   static std::vector<Tensor> cache(static_cast<size_t>(DeviceType::Count) * 6);
@@ -76,6 +86,13 @@ void Variable::incr_grad(const Tensor& g) {
   if (!impl_->grad.defined()) {
     LMP_INTERNAL_ASSERT(g.shape() == impl_->data.shape())
         << "There should be no broadcasting in incr_grad";
+    Scalar v;
+    if (pending_fill(g, &v)) {
+      // 0 + a constant is that constant (with -0.0 -> +0.0): the gradient
+      // stays a constant node, which later reductions can fold.
+      impl_->grad = tensor::full_like(g, 0.0 + v);
+      return;
+    }
     impl_->grad = tops::add(zero_scalar(g.device(), g.type()), g);
     return;
   }
@@ -86,7 +103,35 @@ void Variable::incr_grad(const Tensor& g) {
   // pass holds its storage yet: the sum can stay pending too and fuse with the
   // pending terms, in the same order as the in-place add.
   if (tensor::detail::UnsafeTensorAccessor::getImpl(impl_->grad)->is_deferred()) {
+    Scalar a, b;
+    if (g.type() == impl_->grad.type() && pending_fill(impl_->grad, &a) && pending_fill(g, &b)) {
+      // Two constants add to a constant, rounded as the add kernel rounds;
+      // the gradient tensor is updated in place, so a handle taken from
+      // .grad sees the sum (as add_inplace would give it).
+      const Scalar sum = g.type() == DataType::Float32 ? Scalar(float(a) + float(b)) : a + b;
+      tensor::detail::UnsafeTensorAccessor::getImpl(impl_->grad)
+          ->replace_pending_constant(tensor::lazy::make_fill(g.shape(), g.device(), g.type(), sum));
+      return;
+    }
     impl_->grad = tops::add(impl_->grad, g);
+    return;
+  }
+  // A realised gradient receiving a pending term (the backward formulas run
+  // captured): grad + g is one fused kernel computed straight into the
+  // gradient's buffer, so the buffer keeps its identity and g is never
+  // materialised.  Same values as realising g and adding it in place.
+  const auto& gi = tensor::detail::UnsafeTensorAccessor::getImpl(g);
+  if (gi->is_deferred() && g.type() == impl_->grad.type() &&
+      tensor::lazy::backend(g.device()) != nullptr) {
+    Tensor sum;
+    {
+      tensor::lazy::CaptureGuard capture(true);
+      sum = tops::add(impl_->grad, g);
+    }
+    const auto& gradi = tensor::detail::UnsafeTensorAccessor::getImpl(impl_->grad);
+    if (!tensor::lazy::realize_into(tensor::detail::UnsafeTensorAccessor::getImpl(sum).get(),
+                                    gradi->storage()))
+      impl_->grad.copy(sum);
     return;
   }
   tops::add_inplace(impl_->grad, g);  // variable.cpp:30-35
@@ -176,9 +221,14 @@ void Variable::backward() {
   // tensors a pending gradient reads must not change it.  Deepest first: the
   // region of an input's gradient reaches back to the seed and stores the
   // gradients held on the way as extra outputs, so a chain of pending
-  // gradients is one kernel rather than one per gradient.
+  // gradients is one kernel rather than one per gradient.  A constant
+  // gradient (a pending fill: the seed, or a gradient that is the seed
+  // passed through additions) reads nothing, so it may stay pending until it
+  // is read.
+  Scalar v;
   for (auto it = topo.rbegin(); it != topo.rend(); ++it)
-    if (it->impl_->grad.defined()) it->impl_->grad.realize();
+    if (it->impl_->grad.defined() && !pending_fill(it->impl_->grad, &v))
+      it->impl_->grad.realize();
 }
 
 // ------------------------------------------------------------ op recording

@@ -256,9 +256,12 @@ Region build_region(TensorImpl* root) {
     for (TensorImpl* n : r.nodes)
       for (const auto& in : n->lazy_op()->inputs)
         if (r.node_of.count(in.get())) ++refs[in.get()];
+    // A constant (fill node) that others hold is a literal here and stays
+    // pending for them: nothing to store.
     std::vector<TensorImpl*> shared;
     for (TensorImpl* n : r.nodes)
-      if (n != root && r.owners.at(n) > refs[n]) shared.push_back(n);
+      if (n != root && r.owners.at(n) > refs[n] && n->lazy_op()->kind() != lazy::OpKind::Fill)
+        shared.push_back(n);
     bool has_reduce = false;
     for (TensorImpl* n : r.nodes) has_reduce |= is_reduce(n);
     const RowPlan rp = has_reduce ? row_plan(r) : RowPlan{};
@@ -844,6 +847,14 @@ void run_eager_root(TensorImpl* root) {
 
 class HipFusionBackend : public lazy::LazyBackend {
  public:
+  bool realize_into(TensorImpl* root, const Storage& target) override {
+    if (!root->is_deferred()) return false;
+    t_target = &target;
+    realize(root);
+    t_target = nullptr;
+    return root->raw() == target.data();
+  }
+
   void realize(TensorImpl* root) override {
     HostScope scope;
     const Storage* target = t_target;

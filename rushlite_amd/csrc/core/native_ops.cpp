@@ -1,6 +1,7 @@
 // Op frontends, the capture flag, lazy nodes, record and realize.
 // Lamp3 counterparts: native/*.cpp, lazy/*.cpp, lazy/functions/*.cpp.
 #include <array>
+#include <cmath>
 #include <cstring>
 #include <iomanip>
 #include <limits>
@@ -127,9 +128,57 @@ bool capture_reduction(const Tensor& a, size_t axis) {
 }
 }  // namespace
 
+namespace {
+// A reduction of a pending constant (a fill node: backward's ones seed, a
+// SummationBackward ones) needs no pass over memory when its result is the
+// same in every summation order: max and min are the value combined once
+// with the identity (cpu/kernels.hpp:155-174), and a sum
+// of n copies of an integer-valued v with |v| * n <= 2^24 (float32) or 2^53
+// (float64) has only exact partial sums (a +-0 fill sums to +0 from the +0
+// identity).  The result is then a constant of the keep-dims shape: pending
+// under capture, filled otherwise.  Returns false where that does not hold.
+bool fold_constant_reduction(const Tensor& a, size_t axis, int code, Tensor* out) {
+  const auto& ai = Acc::getImpl(a);
+  if (!ai->is_deferred() || ai->lazy_op()->kind() != lazy::OpKind::Fill) return false;
+  const DataType t = a.type();
+  if (t != DataType::Float32 && t != DataType::Float64) return false;
+  if (axis >= a.shape().size() || a.shape()[axis] == 0) return false;
+  const double n = static_cast<double>(a.shape()[axis]);
+  const double v = t == DataType::Float32 ? double(float(ai->lazy_op()->param0()))
+                                          : double(ai->lazy_op()->param0());
+  if (std::isnan(v)) return false;
+  double r;
+  const bool f32 = t == DataType::Float32;
+  const double big = f32 ? double(std::numeric_limits<float>::max())
+                         : std::numeric_limits<double>::max();
+  if (code == LMP_RED_MAX) {
+    r = -big < v ? v : -big;  // combine(lowest(), v): -inf folds to lowest()
+  } else if (code == LMP_RED_MIN) {
+    r = v < big ? v : big;  // combine(max(), v): +inf folds to max()
+  } else if (code == LMP_RED_SUM) {
+    const double lim = t == DataType::Float32 ? 16777216.0 : 9007199254740992.0;
+    if (v != std::trunc(v) || std::fabs(v) * n > lim) return false;
+    r = v == 0.0 ? 0.0 : v * n;
+  } else {
+    return false;
+  }
+  std::vector<size_t> shape = a.shape();
+  shape[axis] = 1;
+  if (lazy::should_capture(a.device())) {
+    *out = Acc::fromImpl(lazy::record(lazy::make_fill(shape, a.device(), t, r)));
+  } else {
+    *out = empty(shape, a.device(), t);
+    out->fill(r);
+  }
+  return true;
+}
+}  // namespace
+
 #define LMP_DEF_REDUCT(name, CODE)                                              \
   Tensor name(const Tensor& a, size_t axis) {                                   \
     const auto& ai = Acc::getImpl(a);                                           \
+    Tensor folded;                                                              \
+    if (fold_constant_reduction(a, axis, CODE, &folded)) return folded;         \
     if (capture_reduction(a, axis))                                             \
       return Acc::fromImpl(lazy::record(lazy::make_reduce(CODE, ai, axis)));    \
     return wrap(name##_stub()(a.device(), *ai, axis));                          \
@@ -484,6 +533,13 @@ void realize(TensorImpl* t) {
   LazyBackend* b = backend(t->device());
   LMP_CHECK(b != nullptr) << "no lazy backend registered for device";
   b->realize(t);
+}
+
+bool realize_into(TensorImpl* root, const Storage& target) {
+  if (!root->is_deferred()) return false;
+  LazyBackend* b = backend(root->device());
+  LMP_CHECK(b != nullptr) << "no lazy backend registered for device";
+  return b->realize_into(root, target);
 }
 
 void realize_many(const std::vector<TensorImpl*>& roots,

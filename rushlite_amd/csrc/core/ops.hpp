@@ -213,6 +213,14 @@ struct LazyBackend {  // lazy_backend.hpp:15-35
     for (TensorImpl* t : roots)
       if (t->is_deferred()) realize(t);
   }
+  // Realises pending `root` straight into `target` (a buffer of its size that
+  // its own region reads at most at the output's index) and then shares it;
+  // false when the backend cannot (root is then realised elsewhere).
+  virtual bool realize_into(TensorImpl* root, const Storage& target) {
+    (void)target;
+    realize(root);
+    return false;
+  }
 };
 LazyBackend* backend(DeviceType dev);
 void register_backend(DeviceType dev, LazyBackend* b);
@@ -223,6 +231,8 @@ void realize(TensorImpl* t);
 // backend's realize_many; `targets` is empty or one entry (or null) per root.
 void realize_many(const std::vector<TensorImpl*>& roots,
                   const std::vector<const Storage*>& targets);
+// LazyBackend::realize_into of root's device.
+bool realize_into(TensorImpl* root, const Storage& target);
 
 // p0/p1 are clamp backward's bounds (LMP_BIN_CLAMP_BACKWARD).
 std::shared_ptr<LazyFunction> make_binary(int code,

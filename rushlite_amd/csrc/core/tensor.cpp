@@ -156,6 +156,12 @@ void TensorImpl::set_deferred(std::shared_ptr<lazy::LazyFunction> op) {
   lazy_ = std::move(op);
 }
 
+void TensorImpl::replace_pending_constant(std::shared_ptr<lazy::LazyFunction> op) {
+  LMP_CHECK(is_deferred() && lazy_->inputs.empty())
+      << "replace_pending_constant: tensor is not a pending constant";
+  lazy_ = std::move(op);
+}
+
 // Views share storage.  A pending graph is realised first so that the view
 // and its base read the same buffer instead of each re-running the graph.
 TensorImpl TensorImpl::reshape(std::vector<size_t> new_shape) {

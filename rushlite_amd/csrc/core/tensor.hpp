@@ -131,6 +131,10 @@ class TensorImpl {
   const std::shared_ptr<lazy::LazyFunction>& lazy_op() const noexcept { return lazy_; }
   void set_realized(Storage storage);
   void set_deferred(std::shared_ptr<lazy::LazyFunction> op);
+  // Replaces a pending constant (a node without inputs) by another pending op
+  // of the same shape and dtype, keeping this tensor's identity (a gradient
+  // accumulated while still a constant).
+  void replace_pending_constant(std::shared_ptr<lazy::LazyFunction> op);
   Storage storage() const noexcept { return storage_; }
   // Raw pointer without realisation; only valid for realised tensors.
   void* raw() const noexcept { return storage_.data(); }

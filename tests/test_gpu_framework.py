@@ -732,6 +732,44 @@ def test_long_held_chain_splits_into_few_regions(rsl):
         assert np.array_equal(t.numpy().view(np.uint32), w.view(np.uint32)), i
 
 
+def test_broadcast_add_backward_folds_and_accumulates_in_place(rsl):
+    """The backward of A + B + C (B [1, N], C [M, 1]) reduces the ones seed
+    over each broadcast axis: a sum of ones is exact in any order, so it is
+    folded to a constant instead of a pass over the seed, and the gradients
+    stay constants until read.  Accumulation keeps the gradient tensors'
+    identity throughout -- the in-place accumulation Lamp3 tests in
+    autograd_tests.cpp:487-514."""
+    m, n = 300, 257
+    rng = np.random.default_rng(27)
+    A = rsl.Variable(rng.standard_normal((m, n)).astype(np.float32), requires_grad=True)
+    B = rsl.Variable(rng.standard_normal((1, n)).astype(np.float32), requires_grad=True)
+    C = rsl.Variable(rng.standard_normal((m, 1)).astype(np.float32), requires_grad=True)
+    (A + B + C).backward()
+    held = [v.grad for v in (A, B, C)]  # handles taken before any read
+    s0 = rsl._stats()
+    y = A + B + C
+    y.backward()
+    s1 = rsl._stats()
+    # The gradients are constants until read: the second backward launches
+    # nothing (the forward's two adds are eager), and the held handles see the
+    # accumulated values.
+    assert s1["eager_launches"] - s0["eager_launches"] == 2
+    assert s1["fused_launches"] - s0["fused_launches"] == 0
+    assert np.all(held[0].numpy() == 2.0)
+    assert np.all(held[1].numpy() == 2.0 * m) and np.all(held[2].numpy() == 2.0 * n)
+    assert np.all(y.grad.numpy() == 1.0)
+    # Read (materialised) gradients accumulate in place: one fused kernel each
+    # computes g + the pending term into the existing buffer.
+    ptrs = [rsl._storage_ptr(v.grad) for v in (A, B, C)]
+    s0 = rsl._stats()
+    (A + B + C).backward()
+    s1 = rsl._stats()
+    assert [rsl._storage_ptr(v.grad) for v in (A, B, C)] == ptrs
+    assert s1["fused_launches"] - s0["fused_launches"] == 3
+    assert np.all(held[0].numpy() == 3.0)
+    assert np.all(B.grad.numpy() == 3.0 * m) and np.all(C.grad.numpy() == 3.0 * n)
+
+
 def test_realize_all_groups_independent_updates(rsl):
     """realize_all runs the pending elementwise updates of several tensors
     (different shapes, float4 and indexed plans, float32 and float64, as an
