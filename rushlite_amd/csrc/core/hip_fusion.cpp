@@ -881,12 +881,15 @@ class HipFusionBackend : public lazy::LazyBackend {
       }
     }
     // Groupable when every region's nodes are still pending, pairwise
-    // disjoint, and hold no other job's root.
+    // disjoint (constants excepted: each region inlines them as literals),
+    // and hold no other job's root.
     std::unordered_set<TensorImpl*> seen;
     bool ok = true;
     for (const Job& j : jobs) {
       for (TensorImpl* n : j.r.nodes) {
-        ok &= n->is_deferred() && seen.insert(n).second;
+        ok &= n->is_deferred();
+        if (ok && (n == j.root || n->lazy_op()->kind() != lazy::OpKind::Fill))
+          ok &= seen.insert(n).second;
       }
     }
     if (!ok) {
