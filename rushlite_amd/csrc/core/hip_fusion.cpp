@@ -1106,4 +1106,31 @@ std::string fused_source_for(TensorImpl* root) {
   return codegen(r, make_plan(r, root->shape(), f64), "lmp_fused", f64);
 }
 
+// Source of the one kernel realize_all would run for these elementwise roots
+// (each region's plan, one-shot workgroup ranges); for tests and inspection.
+std::string fused_group_source_for(const std::vector<TensorImpl*>& roots) {
+  std::vector<Region> rs;
+  std::vector<Plan> ps;
+  std::vector<bool> f64;
+  std::vector<uint64_t> blocks;
+  rs.reserve(roots.size());
+  ps.reserve(roots.size());
+  for (TensorImpl* root : roots) {
+    LMP_CHECK(root->is_deferred()) << "tensor has no pending graph";
+    rs.push_back(settle_region(root));
+    f64.push_back(root->type() == DataType::Float64);
+    ps.push_back(make_plan(rs.back(), root->shape(), f64.back()));
+    LMP_CHECK(!row_plan(rs.back()).ok) << "row regions are not grouped";
+    const uint64_t work = ps.back().vec ? ps.back().nvec : ps.back().n;
+    blocks.push_back(std::max<uint64_t>(1, (work + kBlock - 1) / kBlock));
+  }
+  std::vector<const Region*> rp;
+  std::vector<const Plan*> pp;
+  for (size_t i = 0; i < rs.size(); ++i) {
+    rp.push_back(&rs[i]);
+    pp.push_back(&ps[i]);
+  }
+  return codegen_multi(rp, pp, f64, blocks, "lmp_fused");
+}
+
 }  // namespace lmp::tensor::hip

@@ -14,6 +14,7 @@
 
 namespace lmp::tensor::hip {
 std::string fused_source_for(TensorImpl* root);
+std::string fused_group_source_for(const std::vector<TensorImpl*>& roots);
 }
 
 using namespace lmp::tensor;
@@ -35,8 +36,7 @@ P red(int op, const P& a) {
   return lazy::record(lazy::make_reduce(op, a, a->shape().size() - 1));
 }
 
-void check(const char* what, const P& root, const char* must_contain) {
-  const std::string src = hip::fused_source_for(root.get());
+void check_source(const char* what, const std::string& src, const char* must_contain) {
   if (src.find(must_contain) == std::string::npos) {
     std::printf("FAIL %s: source lacks \"%s\"\n", what, must_contain);
     ++failures;
@@ -57,6 +57,14 @@ void check(const char* what, const P& root, const char* must_contain) {
     std::printf("ok   %s (%zu bytes)\n", what, src.size());
   }
   hiprtcDestroyProgram(&prog);
+}
+
+void check(const char* what, const P& root, const char* must_contain) {
+  check_source(what, hip::fused_source_for(root.get()), must_contain);
+}
+
+P fill(std::vector<size_t> shape, double v) {
+  return lazy::record(lazy::make_fill(shape, DeviceType::HIP, DataType::Float32, v));
 }
 
 P softmax(P x) {
@@ -106,6 +114,44 @@ int main() {
     const P r = red(LMP_RED_SUM, bin(LMP_BIN_MUL, un(LMP_UN_NEG, y),
                                      un(LMP_UN_LOG, bin(LMP_BIN_ADD, p, k))));
     check("loss row", r, "logf(");
+  }
+  {
+    // Interior values something else holds become extra outputs of the
+    // region's kernel (xo0, ..) instead of separate realisations.
+    P a = leaf({64, 128}), b = leaf({64, 128});
+    const P t = bin(LMP_BIN_MUL, a, b);  // held below: stored by the kernel
+    const P r = bin(LMP_BIN_SUB, bin(LMP_BIN_ADD, t, a), b);
+    check("held interior value as extra output (float4)", r, "xo0");
+    P c = leaf({64, 100});
+    const P e = un(LMP_UN_EXP, c);  // held
+    const P s = red(LMP_RED_SUM, e);
+    check("held interior value in a row kernel", s, "xo0");
+  }
+  {
+    // A row region taking a [1, 1] constant (the loss seed) and the backward
+    // functors of abs and clamp.
+    P x = leaf({32, 10}), g = leaf({32, 10});
+    const P seed = fill({1, 1}, 1.0);
+    const P r = red(LMP_RED_SUM,
+                    bin(LMP_BIN_MUL, seed,
+                        lazy::record(lazy::make_binary(LMP_BIN_CLAMP_BACKWARD, x, g, 0.0, 1e300))));
+    check("row region with a [1,1] fill and clamp backward", r, "__uint_as_float(0x3f800000u)");
+    const P ab = lazy::record(lazy::make_binary(LMP_BIN_ABS_BACKWARD, x, g));
+    check("abs backward", ab, "(-");
+  }
+  {
+    // realize_all's grouped kernel: float4, indexed and float64 regions, each
+    // in its own workgroup range.
+    P p1 = leaf({256, 64}), g1 = leaf({256, 64}), lr = leaf({1});
+    P p2 = leaf({10}), g2 = leaf({10});
+    P p3 = leaf({33, 7}, DataType::Float64), g3 = leaf({33, 7}, DataType::Float64),
+      lr64 = leaf({1}, DataType::Float64);
+    const P u1 = bin(LMP_BIN_SUB, p1, bin(LMP_BIN_MUL, lr, g1));
+    const P u2 = bin(LMP_BIN_SUB, p2, bin(LMP_BIN_MUL, lr, g2));
+    const P u3 = bin(LMP_BIN_SUB, p3, bin(LMP_BIN_MUL, lr64, g3));
+    check_source("grouped updates (float4, indexed, float64)",
+                 hip::fused_group_source_for({u1.get(), u2.get(), u3.get()}),
+                 "else if (blockIdx.x <");
   }
   if (failures) {
     std::printf("%d codegen failures\n", failures);
