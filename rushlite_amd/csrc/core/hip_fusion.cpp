@@ -470,6 +470,7 @@ void emit_chain(std::ostringstream& os, const Region& r, const std::string& inde
   os << indent << dst << " = t" << (r.nodes.size() - 1) << ";\n";
 }
 
+#define LMP_WAVE_SWAP_SRC(...) #__VA_ARGS__
 const char* kPrelude = R"(
 typedef float lmp_v4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float lmp_clamp(float x, float lo, float hi) {
@@ -478,7 +479,11 @@ __device__ __forceinline__ float lmp_clamp(float x, float lo, float hi) {
 __device__ __forceinline__ double lmp_clamp(double x, double lo, double hi) {
   return x < lo ? lo : (x > hi ? hi : x);
 }
-)";
+)"
+// The eager reductions' lane exchanges, the same text.
+#include "../hip/wave_swap.inc"
+    "\n";
+#undef LMP_WAVE_SWAP_SRC
 
 // Parameter names of one region in a kernel: its root output, the prefix of
 // its interior outputs (xo0, ..) and of its leaves (in0, ..).  A kernel that
@@ -762,8 +767,8 @@ std::string codegen_rows(const Region& r, const RowPlan& rp, const std::string& 
     } else {
       os << b[0] << ";\n";
     }
-    for (int off = 32; off >= 1; off >>= 1)
-      os << "    { const " << T << " o = __shfl_xor(" << P << "v, " << off << ", 64); " << P
+    for (int off = 1; off <= 32; off <<= 1)
+      os << "    { const " << T << " o = lmp_swap<" << off << ">(" << P << "v); " << P
          << "v = " << comb(P + "v", "o") << "; }\n";
     os << "    v" << m << " = " << P << "v;\n  }\n";
   }

@@ -5,7 +5,7 @@
 // Row case (inner == 1, e.g. sum/max over dim 1 of [16384,16384]):
 //   long fp32 rows  -> one 256-thread workgroup per row segment, 128-bit
 //                      loads, 16 independent accumulators per lane, wave64
-//                      butterfly (__shfl_xor) then LDS across the 4 waves;
+//                      butterfly (DPP lane swaps) then LDS across the 4 waves;
 //                      a row is split over several workgroups only when
 //                      there are too few rows to fill 256 CUs, and the
 //                      partials are folded by a second pass in fixed order.
@@ -41,11 +41,21 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
 
+#define LMP_WAVE_SWAP_SRC(...) __VA_ARGS__
+#include "wave_swap.inc"
+#undef LMP_WAVE_SWAP_SRC
+
+// Butterfly over the 64 lanes in the order 1, 2, 4, 8, 16, 32; lane 0 holds
+// the result.
 template <int OP, typename T>
 __device__ __forceinline__ T wave_reduce(T v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1)
-    v = Reducer<OP, T>::combine(v, __shfl_xor(v, off, 64));
+  using R = Reducer<OP, T>;
+  v = R::combine(v, lmp_swap<1>(v));
+  v = R::combine(v, lmp_swap<2>(v));
+  v = R::combine(v, lmp_swap<4>(v));
+  v = R::combine(v, lmp_swap<8>(v));
+  v = R::combine(v, lmp_swap<16>(v));
+  v = R::combine(v, lmp_swap<32>(v));
   return v;
 }
 

@@ -96,18 +96,18 @@ int main() {
   }
   {
     const P r1 = softmax(leaf({512, 1000}));
-    check("softmax 512x1000 (float4 order)", r1, "__shfl_xor");
+    check("softmax 512x1000 (float4 order)", r1, "lmp_swap<32>");
     const P r2 = softmax(leaf({32, 10}));
-    check("softmax 32x10 (scalar order)", r2, "__shfl_xor");
+    check("softmax 32x10 (scalar order)", r2, "lmp_swap<32>");
     const P r3 = softmax(leaf({7, 333}));
-    check("softmax 7x333", r3, "__shfl_xor");
+    check("softmax 7x333", r3, "lmp_swap<32>");
     const P r4 = softmax(leaf({64, 100}, DataType::Float64));
     check("softmax float64", r4, "double");
   }
   for (int op : {LMP_RED_SUM, LMP_RED_MAX, LMP_RED_MIN, LMP_RED_PROD}) {
     P a = leaf({5, 3, 12}), w = leaf({12}), c = leaf({1});
     const P r = red(op, bin(LMP_BIN_ADD, bin(LMP_BIN_MUL, a, w), c));
-    check("reduce of a*w+c, 3-d rows", r, "__shfl_xor");
+    check("reduce of a*w+c, 3-d rows", r, "lmp_swap<32>");
   }
   {
     P p = leaf({32, 10}), y = leaf({32, 10}), k = leaf({1});
