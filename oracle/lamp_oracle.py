@@ -33,11 +33,29 @@ UN = dict(neg=0, exp=1, log=2, sqrt=3, abs=4, sin=5, cos=6, tan=7, clamp=8)
 RED = dict(sum=0, max=1, min=2, prod=3)
 
 _libs: dict[str, C.CDLL] = {}
+_fast_default = False
 
 
-def load(fast: bool = False) -> C.CDLL:
+class fast_build:
+    """Within this block the wrappers (and so OVar, mlp_step, mlp_train) run on
+    liblamp_cpu_fast.so, the reference's -O3 -ffast-math build, unless a call
+    passes fast= itself.  bench.py's CPU baseline times the MLPs this way."""
+
+    def __enter__(self):
+        global _fast_default
+        self._prev, _fast_default = _fast_default, True
+        return self
+
+    def __exit__(self, *exc):
+        global _fast_default
+        _fast_default = self._prev
+
+
+def load(fast: bool | None = None) -> C.CDLL:
     """liblamp_cpu.so (strict IEEE, for parity) or liblamp_cpu_fast.so
     (the reference's -ffast-math flags, for the timed CPU baseline)."""
+    if fast is None:
+        fast = _fast_default
     name = "liblamp_cpu_fast.so" if fast else "liblamp_cpu.so"
     if name not in _libs:
         path = HERE / name
@@ -97,7 +115,7 @@ def padded_strides(in_shape, nd):
     return out
 
 
-def binary(op: str, a, b, p0: float = 0.0, p1: float = 0.0, fast: bool = False):
+def binary(op: str, a, b, p0: float = 0.0, p1: float = 0.0, fast: bool | None = None):
     a, b = _f32(a), _f32(b)
     same = a.shape == b.shape
     out_shape = a.shape if same else broadcast_shape(a.shape, b.shape)
@@ -112,7 +130,7 @@ def binary(op: str, a, b, p0: float = 0.0, p1: float = 0.0, fast: bool = False):
     return out
 
 
-def unary(op: str, a, p0: float = 0.0, p1: float = 0.0, fast: bool = False):
+def unary(op: str, a, p0: float = 0.0, p1: float = 0.0, fast: bool | None = None):
     a = _f32(a)
     out = np.empty_like(a)
     load(fast).lcpu_unary_f32(UN[op], out.ctypes.data, a.ctypes.data, a.size,
@@ -120,7 +138,7 @@ def unary(op: str, a, p0: float = 0.0, p1: float = 0.0, fast: bool = False):
     return out
 
 
-def reduce(op: str, a, axis: int, fast: bool = False):
+def reduce(op: str, a, axis: int, fast: bool | None = None):
     a = _f32(a)
     oshape = list(a.shape)
     oshape[axis] = 1
@@ -131,7 +149,7 @@ def reduce(op: str, a, axis: int, fast: bool = False):
     return out
 
 
-def matmul(a, b, fast: bool = False):
+def matmul(a, b, fast: bool | None = None):
     a, b = _f32(a), _f32(b)
     if a.ndim != 2 or b.ndim != 2 or a.shape[1] != b.shape[0]:
         raise ValueError("matmul: incompatible shapes")
@@ -141,7 +159,7 @@ def matmul(a, b, fast: bool = False):
     return out
 
 
-def transpose(a, fast: bool = False):
+def transpose(a, fast: bool | None = None):
     a = _f32(a)
     out = np.empty((a.shape[1], a.shape[0]), np.float32)
     load(fast).lcpu_transpose_f32(out.ctypes.data, a.ctypes.data, a.shape[0],
@@ -149,19 +167,19 @@ def transpose(a, fast: bool = False):
     return out
 
 
-def fill(shape, value: float, fast: bool = False):
+def fill(shape, value: float, fast: bool | None = None):
     out = np.empty(shape, np.float32)
     load(fast).lcpu_fill_f32(out.ctypes.data, out.size, value)
     return out
 
 
-def add_inplace(dst: np.ndarray, src, fast: bool = False) -> None:
+def add_inplace(dst: np.ndarray, src, fast: bool | None = None) -> None:
     src = _f32(src)
     assert dst.dtype == np.float32 and dst.flags.c_contiguous and dst.shape == src.shape
     load(fast).lcpu_add_inplace_f32(dst.ctypes.data, src.ctypes.data, dst.size)
 
 
-def num_threads(fast: bool = False) -> int:
+def num_threads(fast: bool | None = None) -> int:
     return load(fast).lcpu_num_threads()
 
 
@@ -351,6 +369,19 @@ def relu(a):
     return clamp(a, 0.0, DBL_MAX)
 
 
+def relu_with_mask(a, mask):
+    """ReLU whose backward passes the gradient where `mask` is true instead of
+    where 0 < x < DBL_MAX.  A test hands in the masks of the implementation
+    under test: a pre-activation within rounding of zero may land on either
+    side in another valid GEMM summation order, and one such unit moves a
+    whole weight-gradient column.  Forward values are clamp's."""
+    mask = np.asarray(mask, bool)
+    if mask.shape != a.data.shape:
+        raise ValueError("relu_with_mask: mask shape differs from the input's")
+    keep = mask.astype(np.float32)
+    return _unary_var("clamp", a, lambda n, a: binary("mul", n.grad, keep), 0.0, DBL_MAX)
+
+
 def _reduct_var(op, a: OVar, axis: int, grad):
     out = reduce(op, a.data, axis)
 
@@ -425,17 +456,18 @@ def softmax(x: OVar, dim: int) -> OVar:
 # ------------------------------------------------------------------- MLP
 
 
-def mlp_step(weights, biases, x, y, f64_gemm: bool = False):
+def mlp_step(weights, biases, x, y, f64_gemm: bool = False, relu_masks=None):
     """One forward + backward of the README MLP from the given parameters.
     Returns (loss, weight grads, bias grads).  f64_gemm swaps the GEMMs for
-    float64-accumulated ones (see matmul_f64)."""
+    float64-accumulated ones (see matmul_f64); relu_masks (one boolean array
+    per hidden layer) replaces each ReLU's backward mask (see relu_with_mask)."""
     W = [OVar(w, True) for w in weights]
     B = [OVar(b, True) for b in biases]
     h = OVar(x)
     for i in range(len(W)):
         h = matmul_v(h, W[i], f64_gemm) + B[i]
         if i < len(W) - 1:
-            h = relu(h)
+            h = relu(h) if relu_masks is None else relu_with_mask(h, relu_masks[i])
     p = softmax(h, -1)
     loss = sum_(sum_((-OVar(y)) * log(p + 1e-3), 1), 0)
     loss.backward()

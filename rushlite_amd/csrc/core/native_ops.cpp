@@ -224,6 +224,9 @@ bool matmul_colsum(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b,
   if (c->defined() && (!f32(*c) || c->device() != dev)) return false;
   if (s->defined() && (!f32(*s) || s->device() != dev)) return false;
   const size_t m = a.shape()[trans_a ? 1 : 0], n = b.shape()[trans_b ? 0 : 1];
+  // An empty inner dimension (a batch of zero rows) takes the unfused path:
+  // a zero product and the identity of an empty sum.
+  if (a.shape()[trans_a ? 0 : 1] == 0) return false;
   const bool acc_c = c->defined(), acc_s = s->defined();
   if (!acc_c)
     *c = wrap(TensorImpl(Storage(m * n * sizeof(float), dev), {m, n}, DataType::Float32));

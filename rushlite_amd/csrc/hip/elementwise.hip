@@ -111,7 +111,8 @@ __global__ __launch_bounds__(kBlock) void bin2d_f32(
 
 struct NdDesc {
   int nd;                      // innermost first
-  FastDiv div[LMP_MAX_DIMS];   // extents (as 32-bit magic dividers)
+  FastDiv div[LMP_MAX_DIMS];   // extents below 2^32 (as 32-bit magic dividers)
+  uint64_t ext[LMP_MAX_DIMS];  // every extent (the divisor when it is 2^32 or more)
   int64_t sa[LMP_MAX_DIMS];
   int64_t sb[LMP_MAX_DIMS];
 };
@@ -125,16 +126,16 @@ __global__ __launch_bounds__(kBlock) void bin_nd(T* __restrict__ out,
   const uint64_t stride = uint64_t(gridDim.x) * kBlock;
   for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n;
        i += stride) {
-    // Each extent is < 2^32 and every per-dim remainder fits 32 bits; the
-    // running quotient may not, so peel the innermost dims with 64-bit math
-    // only when the flat index itself exceeds 32 bits.
+    // The magic divider serves while both the running quotient and the
+    // extent fit 32 bits; otherwise the dim is peeled with 64-bit division.
     uint64_t rest = i;
     int64_t oa = 0, ob = 0;
     for (int k = 0; k < d.nd; ++k) {
+      const uint64_t e = d.ext[k];
       uint64_t q;
-      if (rest <= 0xffffffffull) q = d.div[k].div(uint32_t(rest));
-      else q = rest / d.div[k].d;
-      const uint64_t coord = rest - q * d.div[k].d;
+      if (rest <= 0xffffffffull && e <= 0xffffffffull) q = d.div[k].div(uint32_t(rest));
+      else q = rest / e;
+      const uint64_t coord = rest - q * e;
       oa += int64_t(coord) * d.sa[k];
       ob += int64_t(coord) * d.sb[k];
       rest = q;
@@ -151,9 +152,8 @@ int launch_bin_nd(T* out, const T* a, const T* b, const Coalesced& c,
   d.nd = c.nd;
   uint64_t n = 1;
   for (int k = 0; k < c.nd; ++k) {
-    if (c.shape[k] > 0xffffffffll)
-      return fail(LMP_ERR_UNSUPPORTED, "binary: extent above 2^32");
-    d.div[k] = FastDiv(uint32_t(c.shape[k]));
+    d.ext[k] = uint64_t(c.shape[k]);
+    d.div[k] = FastDiv(c.shape[k] <= 0xffffffffll ? uint32_t(c.shape[k]) : 1u);
     d.sa[k] = c.sa[k];
     d.sb[k] = c.sb[k];
     n *= uint64_t(c.shape[k]);

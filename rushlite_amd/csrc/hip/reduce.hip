@@ -319,6 +319,36 @@ __global__ __launch_bounds__(kBlock) void col_reduce_scalar(
   dst[(o * S + s) * inner + c] = acc;
 }
 
+// Column reduction with one lane per output element (o, c) of [outer, inner],
+// grid-striding over them: the axis is folded sequentially from the identity
+// (eight loads in flight, combined in row order).  Used when outer exceeds
+// the grid's z extent, where the kernels above would need one z slice per
+// outer index (reduct.cu:166-182 grid-strides over any output count too).
+template <int OP, typename T>
+__global__ __launch_bounds__(kBlock) void col_reduce_flat(T* __restrict__ out,
+                                                          const T* __restrict__ in,
+                                                          uint64_t outer, uint64_t len,
+                                                          uint64_t inner) {
+  using R = Reducer<OP, T>;
+  const uint64_t n = outer * inner;
+  const uint64_t stride = uint64_t(gridDim.x) * kBlock;
+  for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+    const uint64_t o = i / inner, c = i - o * inner;
+    const T* src = in + o * len * inner + c;
+    T acc = R::identity();
+    uint64_t r = 0;
+    for (; r + 8 <= len; r += 8, src += 8 * inner) {
+      T x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = src[u * inner];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = R::combine(acc, x[u]);
+    }
+    for (; r < len; ++r, src += inner) acc = R::combine(acc, *src);
+    out[i] = acc;
+  }
+}
+
 // Fold S chunk partials [outer, S, inner] -> [outer, inner] in chunk order.
 template <int OP, typename T>
 __global__ __launch_bounds__(kBlock) void fold_chunks(T* __restrict__ out,
@@ -405,8 +435,17 @@ int reduce_cols(Runtime* rt, T* out, const T* in, uint64_t outer, uint64_t len,
   const uint64_t lanes = vec ? inner / 4 : inner;
   const uint64_t per_wg = vec ? 64 : kBlock;
   const uint64_t gx = (lanes + per_wg - 1) / per_wg;
-  if (gx > 0x7fffffffull || outer > 65535)
-    return fail(LMP_ERR_UNSUPPORTED, "reduce: grid too large");
+  if (gx > 0x7fffffffull || outer > 65535) {
+    // More outer slices than the grid's z extent (or columns than its x
+    // extent): one lane per output element, grid-striding.
+    const uint64_t n = outer * inner;
+    const uint64_t cap = uint64_t(rt->cu_count) * 64;
+    const uint64_t blocks = std::min<uint64_t>((n + kBlock - 1) / kBlock, cap);
+    hipLaunchKernelGGL((col_reduce_flat<OP, T>), dim3(uint32_t(blocks)), dim3(kBlock), 0,
+                       rt->stream, out, in, outer, len, inner);
+    LMP_LAUNCH_CHECK("col_reduce_flat");
+    return LMP_OK;
+  }
   // Chunk the reduced axis until the grid reaches ~4 workgroups per CU
   // (measured best for [16384,16384]: 176 us at 4/CU vs 196 us at 8/CU),
   // keeping at least 64 rows per chunk.

@@ -96,6 +96,100 @@ def test_transcendentals_within_2ulp(hip, oracle, op):
     assert d.max() <= 2, (op, int(d.max()))
 
 
+def _correctly_rounded(op, x, y=None):
+    """float64 evaluation rounded once to float32: the correctly rounded value
+    except where the float64 result lies within one float64 ulp of a float32
+    rounding boundary (a 2^-29-relative band, covered by the 2-ulp bar)."""
+    d = x.astype(np.float64)
+    with np.errstate(all="ignore"):
+        if op == "pow":
+            return np.power(d, y.astype(np.float64)).astype(np.float32)
+        return getattr(np, op)(d).astype(np.float32)
+
+
+def _transcendental_inputs(op, rng):
+    n = 1 << 16
+    if op == "exp":
+        x = rng.uniform(-103.0, 88.7, n)  # through the subnormal results to the overflow edge
+        special = [0.0, -0.0, 1.0, -1.0, 88.72, 88.73, -87.3, -103.9, np.inf, -np.inf, np.nan]
+    elif op == "log":
+        x = 10.0 ** rng.uniform(-44.0, 38.5, n)  # subnormal inputs to near FLT_MAX
+        special = [1.0, 2.0, 0.5, 0.0, -1.0, np.inf, np.nan, 1e-45, 3.4e38]
+    else:
+        x = np.concatenate([rng.uniform(-100.0, 100.0, n - 64),
+                            rng.uniform(-1e4, 1e4, 64)])
+        special = [0.0, -0.0, np.pi / 2, np.pi, 1e-30, np.inf, np.nan]
+    return np.concatenate([x, special]).astype(np.float32)
+
+
+@pytest.mark.parametrize("op", ["exp", "log", "sin", "cos", "tan"])
+def test_transcendentals_vs_correctly_rounded(hip, op):
+    """The GPU's exp/log/sin/cos/tan (ocml, reached from the functors of
+    cpu/kernels.hpp:74-113) within 2 ulp of the correctly rounded float32
+    result, independently of the glibc oracle; NaN where it is NaN."""
+    x = _transcendental_inputs(op, np.random.default_rng(29))
+    got = hip.unary(op, up(hip, x)).numpy()
+    want = _correctly_rounded(op, x)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan), op
+    d = ulp_dist(got[~nan], want[~nan])
+    assert d.max() <= 2, (op, int(d.max()), float(x[~nan][d.argmax()]))
+
+
+def test_pow_vs_correctly_rounded(hip):
+    rng = np.random.default_rng(31)
+    a = np.concatenate([rng.uniform(0.01, 10, 1 << 15), 10.0 ** rng.uniform(-10, 10, 1 << 15)])
+    b = np.concatenate([rng.uniform(-4, 4, 1 << 15), rng.uniform(-3, 3, 1 << 15)])
+    a, b = a.astype(np.float32), b.astype(np.float32)
+    got = hip.binary("pow", up(hip, a), up(hip, b)).numpy()
+    want = _correctly_rounded("pow", a, b)
+    assert ulp_dist(got, want).max() <= 2
+
+
+@pytest.mark.parametrize("shape", [(70000, 5, 4), (65536, 9, 3), (66000, 2, 7),
+                                   (70000, 1, 2)], ids=str)
+def test_reduce_outer_beyond_grid_z(hip, oracle, shape):
+    """More outer slices than a grid's z extent (65535), which the reference
+    grid-strides over (reduct.cu:166-182, 253-257): one lane per output folds
+    the axis in row order, so every op equals the oracle's sequential fold
+    (cpu/reduct.cpp:15-19) bit for bit."""
+    rng = np.random.default_rng(zlib.crc32(repr(shape).encode()))
+    a = rng.standard_normal(shape, dtype=np.float32)
+    for op in ("sum", "max", "min", "prod"):
+        src = (1.0 + 0.01 * a).astype(np.float32) if op == "prod" else a
+        got = hip.reduce(op, up(hip, src), 1).numpy()
+        want = oracle.reduce(op, src, 1)
+        assert got.shape == want.shape
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), op
+
+
+def test_binary_extent_beyond_32_bits(hip):
+    """A broadcast add [2^32 + 3, 1] + [1, 2] (8.6e9 outputs, 51 GB): after
+    coalescing, the outer extent is above 2^32, so the generic kernel peels
+    that dim with 64-bit division.  Values planted in a around index 2^32
+    must land in the right output rows."""
+    L = hip.lib()
+    n = (1 << 32) + 3
+    a = hip.DeviceBuffer((n, 1), np.float32)
+    b = up(hip, np.array([[0.25, 0.5]], np.float32))
+    hip.check(L.lmp_k_fill(hip.FLOAT32, a.ptr, n, 1.0))
+    marks = [0, 1, (1 << 31) + 7, (1 << 32) - 1, 1 << 32, (1 << 32) + 1, n - 1]
+    for i in marks:
+        v = np.array([100.0 + (i % 1000)], np.float32)
+        hip.check(L.lmp_rt_memcpy_h2d(C.c_void_p(a.ptr + 4 * i), v.ctypes.data_as(C.c_void_p), 4))
+    out = hip.binary("add", a, b)
+    assert tuple(out.shape) == (n, 2)
+    a.free()
+    probe = marks + [12345, (1 << 32) - 2, n - 2]
+    for i in probe:
+        row = np.empty(2, np.float32)
+        hip.check(L.lmp_rt_memcpy_d2h(row.ctypes.data_as(C.c_void_p), C.c_void_p(out.ptr + 8 * i), 8))
+        base = np.float32(100.0 + (i % 1000)) if i in marks else np.float32(1.0)
+        assert row[0] == base + np.float32(0.25) and row[1] == base + np.float32(0.5), (i, row)
+    out.free()
+    hip.check(L.lmp_rt_empty_cache())
+
+
 def test_fill_cast_add_inplace(hip):
     L = hip.lib()
     buf = hip.DeviceBuffer((1001,), np.float32)
@@ -123,7 +217,9 @@ REDUCE_CASES = [((300, 257), 0), ((300, 257), 1), ((4, 37, 5), 0), ((4, 37, 5), 
                 # one-pass column strips (axis of at most 4096 rows): ragged
                 # strip, several outer slices, the length limit and one past it
                 ((512, 1000), 0), ((6, 700, 16), 1), ((4096, 64), 0), ((4097, 64), 0),
-                ((100, 4), 0)]
+                ((100, 4), 0),
+                # more outer slices than a grid's z extent
+                ((70000, 5, 4), 1)]
 
 
 @pytest.mark.parametrize("shape,axis", REDUCE_CASES, ids=str)

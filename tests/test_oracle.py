@@ -376,6 +376,47 @@ def test_mlp_step_gemm_orders_vs_torch(oracle):
             assert np.max(np.abs(g - w)) / np.max(np.abs(w)) < 1e-5
 
 
+def test_mlp_step_with_relu_masks_vs_torch(oracle):
+    """relu_masks replaces the ReLU's backward mask and nothing else: with
+    the natural mask (0 < t) the step equals the plain step exactly, and with
+    two units flipped (one passing unit blocked, one blocked unit passed) it
+    matches a torch float64 step whose ReLU has that gradient mask and
+    clamp's values."""
+    rng = np.random.default_rng(6)
+    x = rng.random((32, 256), dtype=np.float32)
+    y = rng.random((32, 10), dtype=np.float32)
+    ws = [(rng.standard_normal((256, 64)) * 0.1).astype(np.float32),
+          (rng.standard_normal((64, 10)) * 0.1).astype(np.float32)]
+    bs = [(rng.standard_normal(64) * 0.1).astype(np.float32),
+          (rng.standard_normal(10) * 0.1).astype(np.float32)]
+    t = oracle.binary("add", oracle.matmul(x, ws[0]), bs[0])
+    natural = t > 0
+    plain = oracle.mlp_step(ws, bs, x, y)
+    same = oracle.mlp_step(ws, bs, x, y, relu_masks=[natural])
+    assert same[0] == plain[0]
+    for g, w in zip(same[1] + same[2], plain[1] + plain[2]):
+        assert np.array_equal(g, w)
+    mask = natural.copy()
+    pos, neg = np.argwhere(natural)[3], np.argwhere(~natural)[5]
+    mask[tuple(pos)], mask[tuple(neg)] = False, True
+    tw = [torch.tensor(w, dtype=torch.float64, requires_grad=True) for w in ws]
+    tb = [torch.tensor(b, dtype=torch.float64, requires_grad=True) for b in bs]
+    tx, ty = torch.tensor(x, dtype=torch.float64), torch.tensor(y, dtype=torch.float64)
+    th = tx @ tw[0] + tb[0]
+    tm = torch.tensor(mask, dtype=torch.float64)
+    h = torch.clamp(th, min=0.0).detach() + (th - th.detach()) * tm
+    p = _torch_softmax_lamp(h @ tw[1] + tb[1], -1)
+    tl = (-ty * torch.log(p + 1e-3)).sum(1, keepdim=True).sum(0, keepdim=True)
+    tl.backward()
+    want = [t_.grad.numpy() for t_ in (tw[0], tb[0], tw[1], tb[1])]
+    loss, gw, gb = oracle.mlp_step(ws, bs, x, y, f64_gemm=True, relu_masks=[mask])
+    assert abs(loss - float(tl)) <= 1e-5 * abs(float(tl))
+    for g, w in zip([gw[0], gb[0], gw[1], gb[1]], want):
+        assert np.max(np.abs(g - w)) / np.max(np.abs(w)) < 1e-5
+    # the flips are visible: the first layer's gradients move
+    assert np.max(np.abs(gw[0] - plain[1][0])) > 1e-3 * np.max(np.abs(plain[1][0]))
+
+
 # ------------------------------------------------ typed (non-fp32) oracle
 
 from oracle import lamp_typed as T  # noqa: E402
