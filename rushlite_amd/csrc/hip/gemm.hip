@@ -1048,6 +1048,175 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
   }
 }
 
+// ------------------------------------------------------------------ rows
+//
+// M <= 32 with B transposed and enough columns to give every CU a block of
+// 32 (Linear's input gradient dY * W^T at a small batch: C[m, n] =
+// sum_k A[m, k] * Bs[n, k] with the weight stored as Bs [n, k]).  Column j of
+// C needs row j of Bs in full, so a workgroup that owns 32 columns reads 32
+// whole rows of Bs -- one contiguous span of memory -- over all of K: no
+// split of K, no partials, no fold.  (The split-K direct kernel instead reads
+// 4 KiB pieces of 128 rows 16 KiB apart.)  Its four waves take consecutive
+// quarters of K and add their 32x32 blocks through LDS in wave order.
+//
+// Operands move through wave-private LDS rings: per group of 32 k values a
+// 32 x 32 tile of A and one of Bs (4 KiB each), each filled by four
+// global_load_lds_dwordx4 instructions whose lanes cover 8 rows x 128 bytes,
+// so every instruction reads whole lines (loading straight into MFMA layout
+// would spread each instruction over 32 rows).  In LDS a tile row is 128
+// bytes and its 16-byte chunk c sits in slot c ^ (row & 7), which the DMA
+// arranges by choosing the chunk each lane fetches; fragment reads of a
+// wave's 32 rows then spread over the banks.  Lane l holds row l % 32 and,
+// in half h = l / 32, k0 + 16 h .. k0 + 16 h + 15 (four 128-bit LDS reads per
+// operand); MFMA step s pairs k0 + s with k0 + 16 + s.  STAGES tiles of each
+// wave are in flight; rows outside the matrix and k past the wave's range
+// read the zero page.
+//
+// Each workgroup walks its waves' tiles starting at tile (13 * block) mod
+// count and wrapping around.  With every workgroup starting at k = 0 the
+// whole chip would request the same column offsets of rows 16 KiB apart at
+// once, which crowds a few HBM channels (32.6 us for config 3's dX on
+// MI355X); staggered starts spread the requests (27.0 us).  The order of the
+// k terms then depends on the column block, and is the same on every run.
+struct RowsArgs {
+  const float* a;
+  const float* b;  // stored [n, k]
+  float* c;
+  int m, n, k;
+  int lda, ldb, ldc;
+  int accumulate;
+  const float* bias;  // per-column bias added to the output (or null)
+  int relu;           // with a bias: ReLU after it
+  int vec_out;        // C and the bias take 128-bit accesses
+};
+
+constexpr int kRowsWaves = 4;
+constexpr int kRowsStages = 3;
+constexpr int kRowsTile = 32 * 32;  // floats of one operand tile
+
+// Wait until at most N of this wave's vector-memory operations are
+// outstanding (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14, expcnt
+// and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int STAGES>
+__global__ __launch_bounds__(64 * kRowsWaves, 1) void gemm_thin_rows(RowsArgs g) {
+  constexpr int STAGE = 2 * kRowsTile;  // A tile, then B tile
+  __shared__ __attribute__((aligned(1024))) float smem[kRowsWaves * STAGES * STAGE];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int li = lane & 31, lh = lane >> 5;
+  const int n0 = int(blockIdx.x) * 32;
+  const int part = ((g.k + kRowsWaves - 1) / kRowsWaves + 31) / 32 * 32;
+  const int kb = wave * part;
+  const int ke = min(g.k, kb + part);
+  const int ntiles = kb < ke ? (ke - kb + 31) / 32 : 0;
+  const int rot = ntiles ? int((blockIdx.x * 13u) % uint32_t(ntiles)) : 0;
+  float* ring = smem + wave * STAGES * STAGE;
+  // The zero page's address, materialised once outside the loop.
+  uint64_t zero_bits = reinterpret_cast<uint64_t>(g_direct_zeros);
+  asm volatile("" : "+s"(zero_bits));
+  const float* zero = reinterpret_cast<const float*>(zero_bits);
+
+  // DMA roles: instruction q of a tile covers rows 8q .. 8q + 7; lane L fills
+  // slot (row 8q + L / 8, L % 8), i.e. fetches chunk (L % 8) ^ (row & 7).
+  const float* asrc[4];
+  const float* bsrc[4];
+  int dk[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int row = 8 * q + (lane >> 3);
+    const int c = (lane & 7) ^ (row & 7);
+    dk[q] = 4 * c;
+    asrc[q] = row < g.m ? g.a + int64_t(row) * g.lda + 4 * c : nullptr;
+    bsrc[q] = n0 + row < g.n ? g.b + int64_t(n0 + row) * g.ldb + 4 * c : nullptr;
+  }
+  auto issue = [&](int t) {
+    const int tt = t + rot < ntiles ? t + rot : t + rot - ntiles;
+    const int k0 = kb + 32 * tt;
+    float* st = ring + (t % STAGES) * STAGE;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      lds_dma16(asrc[q] && k0 + dk[q] < ke ? asrc[q] + k0 : zero, st + q * 256);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      lds_dma16(bsrc[q] && k0 + dk[q] < ke ? bsrc[q] + k0 : zero, st + kRowsTile + q * 256);
+  };
+
+  v16f acc = v16f(0.0f);
+#pragma unroll
+  for (int t = 0; t < STAGES - 1; ++t)
+    if (t < ntiles) issue(t);
+  for (int t = 0; t < ntiles; ++t) {
+    // The slot refilled here was read in the previous iteration, whose LDS
+    // reads completed before its MFMAs.
+    if (t + STAGES - 1 < ntiles) {
+      issue(t + STAGES - 1);
+      wait_vm<(STAGES - 1) * 8>();  // tile t has landed
+    } else {
+      wait_vm<0>();
+    }
+    const float* sa = ring + (t % STAGES) * STAGE;
+    const float* sb = sa + kRowsTile;
+    v4f fa[4], fb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int slot = li * 32 + (((4 * lh + i) ^ (li & 7)) << 2);
+      fa[i] = *reinterpret_cast<const v4f*>(sa + slot);
+      fb[i] = *reinterpret_cast<const v4f*>(sb + slot);
+    }
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[s / 4][s % 4], fb[s / 4][s % 4], acc, 0, 0, 0);
+  }
+
+  // Waves' blocks [wave][r][lane] in LDS (over the rings, once every wave is
+  // done with them), summed in wave order.  Thread t owns row t / 8 of the
+  // block and its columns 4 (t % 8) .. 4 (t % 8) + 3; accumulator register r
+  // of lane l holds row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+  __syncthreads();
+  float* red = smem;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
+  __syncthreads();
+  const int t = int(threadIdx.x);
+  const int row = t >> 3, c4 = (t & 7) * 4;
+  const int r = ((row >> 3) << 2) | (row & 3), lhr = (row >> 2) & 1;
+  v4f v;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int ln = c4 + q + 32 * lhr;
+    float s = red[r * 64 + ln];
+#pragma unroll
+    for (int w = 1; w < kRowsWaves; ++w) s += red[(w * 16 + r) * 64 + ln];
+    v[q] = s;
+  }
+  if (row >= g.m) return;
+  float* out = g.c + int64_t(row) * g.ldc;
+  const int col = n0 + c4;
+  if (g.vec_out) {
+    if (col < g.n) {
+      v4f* o = reinterpret_cast<v4f*>(out + col);
+      if (g.accumulate) *o = *o + v;
+      else if (g.bias) *o = lin_epi4(v, *reinterpret_cast<const v4f*>(g.bias + col), g.relu);
+      else *o = v;
+    }
+    return;
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (col + q < g.n) {
+      float* o = out + col + q;
+      if (g.accumulate) *o = *o + v[q];
+      else *o = g.bias ? lin_epi(v[q], g.bias[col + q], g.relu) : v[q];
+    }
+  }
+}
+
 // Default split of K: none once there is a tile for every CU; otherwise
 // enough splits to give each CU two workgroups, keeping at least four K tiles
 // per split.
@@ -1174,6 +1343,29 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
   return LMP_OK;
 }
 
+// M <= 32 with B transposed on the whole-rows kernel: one workgroup per 32
+// columns, no split of K.
+int launch_rows(Runtime* rt, const GemmArgs& g0) {
+  RowsArgs r{};
+  r.a = g0.a;
+  r.b = g0.b;
+  r.c = g0.c;
+  r.m = g0.m;
+  r.n = g0.n;
+  r.k = g0.k;
+  r.lda = g0.lda;
+  r.ldb = g0.ldb;
+  r.ldc = g0.ldc;
+  r.accumulate = g0.accumulate;
+  r.bias = g0.bias;
+  r.relu = g0.relu;
+  r.vec_out = g0.vec_out;
+  const dim3 grid{uint32_t((g0.n + 31) / 32), 1u, 1u};
+  hipLaunchKernelGGL(gemm_thin_rows<kRowsStages>, grid, dim3(64 * kRowsWaves), 0, rt->stream, r);
+  LMP_LAUNCH_CHECK("gemm_thin_rows");
+  return LMP_OK;
+}
+
 // Tile choice (measured on MI355X, fp32): the tiny kernel for small
 // latency-bound products (K <= 512, at most 2^21 multiply-adds); 128x128 whenever its tiles cover
 // the CUs; with a short K (<= 2048) and too few 128x128 tiles, 64x64 tiles
@@ -1183,9 +1375,13 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
 template <bool TA, bool TB>
 int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok) {
   if (tiny_ok(g)) return launch_tiny<TA, TB>(rt, g);
+  // M <= 32 with B transposed and a 32-column block for every CU: whole rows
+  // of B per workgroup, no split (config 3's dX: 46 -> 31-35 us cold).
+  if constexpr (!TA && TB) {
+    if (direct_ok && g.m <= 32 && (g.n + 31) / 32 >= rt->cu_count) return launch_rows(rt, g);
+  }
   // With B transposed a wave's loads touch more cache lines per byte, so
-  // three fragments in flight instead of two (32x8192x4096: 33.5 us against
-  // 36-37 us on MI355X; four measured no better).
+  // three fragments in flight instead of two.
   if (direct_ok && g.m <= 32) return launch_direct<TA, TB, TB ? 3 : 2>(rt, g);
   if (g.m <= 64) return launch_gemm_cfg<CfgSkinny, TA, TB>(rt, g, vec);
   if (vec) {

@@ -329,6 +329,36 @@ def test_gemm_wide_tiles(hip, m, n, k, ta, tb):
     assert rel_err(dc.numpy()[rows], c0[rows].astype(np.float64) + want) <= 1e-4
 
 
+# M <= 32 with B transposed and at least one 32-column block per CU takes the
+# whole-rows kernel (no split of K): config 3's dX, a short batch with a
+# ragged column block and K not a multiple of the 32-value groups, and a
+# very short K.
+@pytest.mark.parametrize("m,n,k", [(32, 8192, 4096), (7, 8200, 1000), (32, 8256, 36)], ids=str)
+def test_gemm_thin_rows(hip, m, n, k):
+    rng = np.random.default_rng(m * 7 + n + k)
+    a = (rng.standard_normal((m, k)) * 0.1).astype(np.float32)
+    bs = (rng.standard_normal((n, k)) * 0.1).astype(np.float32)  # stored [n, k]
+    da, db = up(hip, a), up(hip, bs)
+    want = a.astype(np.float64) @ bs.astype(np.float64).T
+    got = hip.gemm(da, db, trans_b=True).numpy()
+    assert rel_err(got, want) <= 1e-4
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    dc = up(hip, c0)
+    hip.gemm(da, db, trans_b=True, out=dc, accumulate=True)
+    assert rel_err(dc.numpy(), c0.astype(np.float64) + want) <= 1e-4
+    # the Linear epilogue (bias, then ReLU) on this path
+    bias = rng.standard_normal(n).astype(np.float32)
+    dbias = up(hip, bias)
+    L = hip.lib()
+    for entry, relu in ((L.lmp_k_linear_f32, False), (L.lmp_k_linear_relu_f32, True)):
+        out = hip.DeviceBuffer((m, n), np.float32)
+        hip.check(entry(0, 1, m, n, k, da.ptr, k, db.ptr, k, dbias.ptr, out.ptr, n))
+        lin = got + bias  # the product rounded to fp32, then the bias added once
+        if relu:
+            lin = np.where(lin < 0, np.float32(0), lin)
+        assert np.array_equal(out.numpy(), lin), relu
+
+
 def test_transpose(hip):
     for shape in ((3, 2), (64, 64), (130, 70), (1, 9)):
         a = np.random.default_rng(0).standard_normal(shape).astype(np.float32)
