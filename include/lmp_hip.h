@@ -31,8 +31,10 @@
 extern "C" {
 #endif
 
-#define LMP_HIP_ABI_VERSION 6
+#define LMP_HIP_ABI_VERSION 7
 #define LMP_MAX_DIMS 16 /* align_utils.hpp:7 */
+/* Size of the fixed per-device workspace of lmp_k_gemm_f32_noalloc. */
+#define LMP_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 
 typedef enum {
   LMP_OK = 0,
@@ -237,6 +239,25 @@ int lmp_k_reduce(int op, int dtype, void* out, const void* in, size_t outer,
 int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
                    const float* a, size_t lda, const float* b, size_t ldb,
                    float* c, size_t ldc, int accumulate);
+
+/* lmp_k_gemm_f32 without allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory -- code under HIP graph
+ * capture on streams of their own, tight serving loops, harnesses that forbid
+ * hipMalloc.  Same arguments, kernels and results (bit for bit) as
+ * lmp_k_gemm_f32; the split-K partials of products that split K go to a
+ * fixed workspace of LMP_NOALLOC_SCRATCH_BYTES (a device array, one copy per
+ * device, reserved when the library's code object loads there and held until
+ * the process ends) instead of the pool.  A product whose partials would not
+ * fit fails with LMP_ERR_UNSUPPORTED (lmp_k_gemm_f32 serves it); config 4's
+ * largest split (512 x 4096, K split four ways) uses exactly 32 MiB.  Calls
+ * allocate nothing and free nothing, and need nothing cleared between them
+ * (every partial is written before it is read).  All calls on one GPU share
+ * its workspace: calls whose kernels overlap on that GPU (graphs holding
+ * them replayed concurrently on different streams) race.  The first call of
+ * any entry point before lmp_rt_init performs the library's set-up. */
+int lmp_k_gemm_f32_noalloc(int trans_a, int trans_b, size_t m, size_t n, size_t k,
+                           const float* a, size_t lda, const float* b, size_t ldb,
+                           float* c, size_t ldc, int accumulate);
 
 /* C = op(A) * op(B) + bias, bias a row vector of n values added to every row
  * of the finished fp32 product (after any split-K fold): one pass instead of

@@ -94,6 +94,8 @@ SIGNATURES = {
     "lmp_k_reduce": (_i, [_i, _i, _vp, _vp, _sz, _sz, _sz]),
     "lmp_k_gemm_f32": (_i, [_i, _i, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp,
                             _sz, _i]),
+    "lmp_k_gemm_f32_noalloc": (_i, [_i, _i, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp,
+                                    _sz, _i]),
     "lmp_k_gemm": (_i, [_i, _i, _i, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _i]),
     "lmp_k_linear_f32": (_i, [_i, _i, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _vp, _sz]),
     "lmp_k_linear_relu_f32": (_i, [_i, _i, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _vp, _sz]),

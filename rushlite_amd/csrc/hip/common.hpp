@@ -23,6 +23,11 @@ struct Runtime {
   int cu_count = 0;
   int max_threads_per_cu = 2048;
   size_t lds_per_cu = 0;
+  // Device address of the bound device's copy of the no-allocation
+  // workspace (LMP_NOALLOC_SCRATCH_BYTES), looked up once at set-up; null
+  // with the reason in noalloc_error when the lookup failed.
+  void* noalloc_scratch = nullptr;
+  std::string noalloc_error;
 };
 
 // Initialise lazily on device 0 when a kernel entry runs before lmp_rt_init.

@@ -336,6 +336,31 @@ __global__ __launch_bounds__(256) void fold_splits4(float* __restrict__ c,
   else *p = bias ? lin_epi4(acc, *reinterpret_cast<const v4f*>(bias + col), relu) : acc;
 }
 
+// Where split-K partials live: the pool (taken per call and returned once
+// the fold is enqueued; stream order makes the reuse safe) or, for the
+// no-allocation entry point, the device's fixed workspace.
+struct Workspace {
+  float* fixed = nullptr;  // device address of the fixed workspace, or null
+  size_t fixed_bytes = 0;
+
+  int take(size_t bytes, float** out) const {
+    if (fixed) {
+      if (bytes > fixed_bytes)
+        return fail(LMP_ERR_UNSUPPORTED,
+                    "gemm_noalloc: the split-K partials need " + std::to_string(bytes) +
+                        " bytes, above the " + std::to_string(fixed_bytes) +
+                        "-byte no-allocation workspace (lmp_k_gemm_f32 serves this product)");
+      *out = fixed;
+      return LMP_OK;
+    }
+    *out = static_cast<float*>(scratch_alloc(bytes));
+    return *out ? LMP_OK : LMP_ERR_OOM;
+  }
+  void give(float* p) const {
+    if (!fixed) scratch_free(p);
+  }
+};
+
 bool aligned16(const void* p);
 
 // Adds the split-K partials into C (with the epilogue of the final output).
@@ -1228,7 +1253,7 @@ int default_splits(Runtime* rt, int tiles, int k_tiles) {
 }
 
 template <class C, bool TA, bool TB>
-int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
+int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, const Workspace& ws, int splits = 0) {
   g.tiles_m = (g.m + C::BM - 1) / C::BM;
   g.tiles_n = (g.n + C::BN - 1) / C::BN;
   const int tiles = g.tiles_m * g.tiles_n;
@@ -1241,9 +1266,8 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
   float* final_c = g.c;
   float* part = nullptr;
   if (splits > 1) {
-    part = static_cast<float*>(
-        scratch_alloc(size_t(splits) * size_t(g.m) * size_t(g.n) * sizeof(float)));
-    if (!part) return LMP_ERR_OOM;
+    const int wrc = ws.take(size_t(splits) * size_t(g.m) * size_t(g.n) * sizeof(float), &part);
+    if (wrc != LMP_OK) return wrc;
     g.c = part;
   }
   const dim3 grid{uint32_t(tiles), 1u, uint32_t(splits)};
@@ -1260,7 +1284,7 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
   if (splits > 1) {
     const int frc = launch_fold(rt, final_c, part, g.m, g.n, g.ldc, splits, g.accumulate,
                                 g.bias, g.relu);
-    scratch_free(part);  // stream-ordered: the fold reads it first
+    ws.give(part);  // stream-ordered: the fold reads it first
     if (frc != LMP_OK) return frc;
   }
   return LMP_OK;
@@ -1269,7 +1293,7 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, int splits = 0) {
 // One of the one-workgroup-per-CU LDS configurations: K split so the tiles
 // cover the CUs once, keeping at least eight K tiles per split.
 template <class L, bool TA, bool TB>
-int launch_lds(Runtime* rt, GemmArgs g) {
+int launch_lds(Runtime* rt, GemmArgs g, const Workspace& ws) {
   g.tiles_m = (g.m + L::BM - 1) / L::BM;
   g.tiles_n = (g.n + L::BN - 1) / L::BN;
   const int tiles = g.tiles_m * g.tiles_n;
@@ -1280,9 +1304,8 @@ int launch_lds(Runtime* rt, GemmArgs g) {
   float* final_c = g.c;
   float* part = nullptr;
   if (splits > 1) {
-    part = static_cast<float*>(
-        scratch_alloc(size_t(splits) * size_t(g.m) * size_t(g.n) * sizeof(float)));
-    if (!part) return LMP_ERR_OOM;
+    const int wrc = ws.take(size_t(splits) * size_t(g.m) * size_t(g.n) * sizeof(float), &part);
+    if (wrc != LMP_OK) return wrc;
     g.c = part;
   }
   const dim3 grid{uint32_t(tiles), 1u, uint32_t(splits)};
@@ -1292,7 +1315,7 @@ int launch_lds(Runtime* rt, GemmArgs g) {
   if (splits > 1) {
     const int frc = launch_fold(rt, final_c, part, g.m, g.n, g.ldc, splits, g.accumulate,
                                 g.bias, g.relu);
-    scratch_free(part);  // stream-ordered: the fold reads it first
+    ws.give(part);  // stream-ordered: the fold reads it first
     if (frc != LMP_OK) return frc;
   }
   return LMP_OK;
@@ -1302,7 +1325,7 @@ int launch_lds(Runtime* rt, GemmArgs g) {
 // values of k per wave; the split count aims at one workgroup per CU (more
 // only adds partial traffic: measured on MI355X); `splits` > 0 overrides it.
 template <bool TA, bool TB, int STAGES = 2>
-int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
+int launch_direct(Runtime* rt, const GemmArgs& g0, const Workspace& ws, int splits = 0) {
   DirectArgs d{};
   d.a = g0.a;
   d.b = g0.b;
@@ -1325,9 +1348,8 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
   splits = (g0.k + d.k_per_wg - 1) / d.k_per_wg;
   float* part = nullptr;
   if (splits > 1) {
-    part = static_cast<float*>(
-        scratch_alloc(size_t(splits) * size_t(g0.m) * size_t(g0.n) * sizeof(float)));
-    if (!part) return LMP_ERR_OOM;
+    const int wrc = ws.take(size_t(splits) * size_t(g0.m) * size_t(g0.n) * sizeof(float), &part);
+    if (wrc != LMP_OK) return wrc;
     d.c = part;
   }
   const dim3 grid{uint32_t(d.n_blocks), uint32_t(splits), 1u};
@@ -1337,7 +1359,7 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, int splits = 0) {
   if (splits > 1) {
     const int frc = launch_fold(rt, g0.c, part, g0.m, g0.n, g0.ldc, splits, g0.accumulate,
                                 g0.bias, g0.relu);
-    scratch_free(part);  // stream-ordered: the fold reads it first
+    ws.give(part);  // stream-ordered: the fold reads it first
     if (frc != LMP_OK) return frc;
   }
   return LMP_OK;
@@ -1373,7 +1395,7 @@ int launch_rows(Runtime* rt, const GemmArgs& g0) {
 // K.  M <= 64 uses 32x256 tiles, and M <= 32 the register-direct kernel when
 // its alignment requirements hold.
 template <bool TA, bool TB>
-int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok) {
+int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok, const Workspace& ws) {
   if (tiny_ok(g)) return launch_tiny<TA, TB>(rt, g);
   // M <= 32 with B transposed and a 32-column block for every CU: whole rows
   // of B per workgroup, no split (config 3's dX: 46 -> 31-35 us cold).
@@ -1382,23 +1404,23 @@ int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok) {
   }
   // With B transposed a wave's loads touch more cache lines per byte, so
   // three fragments in flight instead of two.
-  if (direct_ok && g.m <= 32) return launch_direct<TA, TB, TB ? 3 : 2>(rt, g);
-  if (g.m <= 64) return launch_gemm_cfg<CfgSkinny, TA, TB>(rt, g, vec);
+  if (direct_ok && g.m <= 32) return launch_direct<TA, TB, TB ? 3 : 2>(rt, g, ws);
+  if (g.m <= 64) return launch_gemm_cfg<CfgSkinny, TA, TB>(rt, g, vec, ws);
   if (vec) {
     const int64_t big_tiles = int64_t((g.m + LdsBig::BM - 1) / LdsBig::BM) *
                               ((g.n + LdsBig::BN - 1) / LdsBig::BN);
     // (K of a few tiles leaves the kernel bound by writing C: more, smaller
     // tiles do better there.)
-    if (big_tiles >= rt->cu_count && g.k >= 256) return launch_lds<LdsBig, TA, TB>(rt, g);
-    if (g.m >= 512 && g.n >= 2048 && g.k >= 2048) return launch_lds<LdsWide, TA, TB>(rt, g);
+    if (big_tiles >= rt->cu_count && g.k >= 256) return launch_lds<LdsBig, TA, TB>(rt, g, ws);
+    if (g.m >= 512 && g.n >= 2048 && g.k >= 2048) return launch_lds<LdsWide, TA, TB>(rt, g, ws);
   }
   const int64_t large_tiles = int64_t((g.m + CfgLarge::BM - 1) / CfgLarge::BM) *
                               ((g.n + CfgLarge::BN - 1) / CfgLarge::BN);
   const int64_t small_tiles = int64_t((g.m + CfgSmall::BM - 1) / CfgSmall::BM) *
                               ((g.n + CfgSmall::BN - 1) / CfgSmall::BN);
   if (large_tiles < rt->cu_count && g.k <= 2048 && small_tiles >= rt->cu_count)
-    return launch_gemm_cfg<CfgSmall, TA, TB>(rt, g, vec, 1);
-  return launch_gemm_cfg<CfgLarge, TA, TB>(rt, g, vec);
+    return launch_gemm_cfg<CfgSmall, TA, TB>(rt, g, vec, ws, 1);
+  return launch_gemm_cfg<CfgLarge, TA, TB>(rt, g, vec, ws);
 }
 
 bool aligned16(const void* p) {
@@ -1436,7 +1458,8 @@ namespace {
 
 int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
                    const float* a, size_t lda, const float* b, size_t ldb,
-                   const float* bias, float* c, size_t ldc, int accumulate, int relu = 0) {
+                   const float* bias, float* c, size_t ldc, int accumulate, int relu = 0,
+                   const Workspace& ws = Workspace{}) {
   if (m == 0 || n == 0) return LMP_OK;
   if (!c) return fail(LMP_ERR_INVALID, "gemm: null output");
   if (k == 0 && bias)
@@ -1477,10 +1500,10 @@ int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
   // (and a float4 bias read when there is a bias).
   const bool direct_ok =
       vec && (trans_b || (ldc % 4 == 0 && aligned16(c) && (!bias || aligned16(bias))));
-  if (!trans_a && !trans_b) return launch_gemm<false, false>(rt, g, vec, direct_ok);
-  if (!trans_a && trans_b) return launch_gemm<false, true>(rt, g, vec, direct_ok);
-  if (trans_a && !trans_b) return launch_gemm<true, false>(rt, g, vec, direct_ok);
-  return launch_gemm<true, true>(rt, g, vec, direct_ok);
+  if (!trans_a && !trans_b) return launch_gemm<false, false>(rt, g, vec, direct_ok, ws);
+  if (!trans_a && trans_b) return launch_gemm<false, true>(rt, g, vec, direct_ok, ws);
+  if (trans_a && !trans_b) return launch_gemm<true, false>(rt, g, vec, direct_ok, ws);
+  return launch_gemm<true, true>(rt, g, vec, direct_ok, ws);
 }
 
 }  // namespace
@@ -1491,6 +1514,19 @@ extern "C" int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n,
                               int accumulate) {
   return gemm_f32_entry(trans_a, trans_b, m, n, k, a, lda, b, ldb, nullptr, c, ldc,
                         accumulate);
+}
+
+extern "C" int lmp_k_gemm_f32_noalloc(int trans_a, int trans_b, size_t m, size_t n,
+                                      size_t k, const float* a, size_t lda,
+                                      const float* b, size_t ldb, float* c, size_t ldc,
+                                      int accumulate) {
+  LMP_RUNTIME_OR_FAIL(rt);
+  if (!rt->noalloc_scratch)
+    return fail(LMP_ERR_RUNTIME, "gemm_noalloc: no workspace on this device (" +
+                                     rt->noalloc_error + ")");
+  const Workspace ws{static_cast<float*>(rt->noalloc_scratch), LMP_NOALLOC_SCRATCH_BYTES};
+  return gemm_f32_entry(trans_a, trans_b, m, n, k, a, lda, b, ldb, nullptr, c, ldc, accumulate,
+                        0, ws);
 }
 
 extern "C" int lmp_k_linear_f32(int trans_a, int trans_b, size_t m, size_t n,

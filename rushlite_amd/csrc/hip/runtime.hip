@@ -13,6 +13,13 @@
 #include "arena.hpp"
 #include "common.hpp"
 
+// Workspace of the no-allocation entry point (lmp_k_gemm_f32_noalloc): a
+// fixed device array, one copy on each device the library's code object is
+// loaded on, held until the process ends.  Host code never passes `scratch`
+// itself to a kernel (on the host the name is only a stand-in): set-up looks
+// up the device's copy with hipGetSymbolAddress and keeps that address.
+static __device__ __align__(256) float scratch[LMP_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
 namespace lmp_hip {
 
 namespace {
@@ -85,6 +92,18 @@ int init_locked(int device) {
   g_rt.cu_count = prop.multiProcessorCount;
   g_rt.max_threads_per_cu = prop.maxThreadsPerMultiProcessor;
   g_rt.lds_per_cu = prop.maxSharedMemoryPerMultiProcessor;
+  // The bound device's copy of the no-allocation workspace (this device is
+  // current).  A failed lookup leaves only that entry point unusable: it
+  // reports the reason; every other entry point works as before.
+  void* ws = nullptr;
+  const hipError_t we = hipGetSymbolAddress(&ws, HIP_SYMBOL(scratch));
+  if (we == hipSuccess && ws) {
+    g_rt.noalloc_scratch = ws;
+  } else {
+    g_rt.noalloc_error = std::string("hipGetSymbolAddress(scratch): ") +
+                         (we == hipSuccess ? "null address" : hipGetErrorString(we));
+    (void)hipGetLastError();
+  }
   g_ready = true;
   return LMP_OK;
 }
