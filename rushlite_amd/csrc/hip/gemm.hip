@@ -81,7 +81,8 @@ struct GemmArgs {
   const float* bias;   // per-column bias added to the final output (or null)
   int vec_out;         // C (and the bias) take 128-bit stores: n, ldc % 4 == 0, 16-byte aligned
   int relu;            // with a bias: ReLU after it (Linear followed by ReLU)
-  float* colsum;       // tiny kernel only: column sums of op(B) (+)= into it (or null)
+  float* colsum;       // column sums of op(B) (+)= into it (or null): tiny kernel and LDS
+                       // tiles with B untransposed and K unsplit
   int colsum_acc;
 };
 
@@ -824,6 +825,7 @@ using LdsSmall = LdsCfg<2, 2, 2, 2, 2, 2>;
 using LdsWide = LdsCfg<4, 2, 2, 2, 3, 1>;
 using LdsBig = LdsCfg<2, 4, 4, 2, 2, 1>;
 
+
 __device__ __forceinline__ int kswz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
 // One 16-byte global load per lane into LDS.  Kept out of the templates: a
@@ -833,12 +835,17 @@ __device__ __forceinline__ void lds_dma16(const float* src, float* lds) {
   __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
 }
 
-// Wait until at most N of this wave's vector-memory loads are outstanding.
+// Wait until at most N of this wave's vector-memory operations are
+// outstanding (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14, expcnt
+// and lgkmcnt left at their maxima).  The empty asm statements with a memory
+// clobber keep the compiler from moving LDS accesses across the wait: the
+// LDS a DMA load fills is not visible to its alias analysis.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-  else static_assert(N < 0, "add the count used by a new configuration");
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+  asm volatile("" ::: "memory");
 }
 
 template <int NT, int MINB, class C, bool TA, bool TB>
@@ -867,6 +874,18 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
   const int k_tiles = (g.k + kBK - 1) / kBK;
   const int kt0 = split * g.k_tiles_per_split;
   const int kt1 = min(k_tiles, kt0 + g.k_tiles_per_split);
+
+  // Column sums of op(B) beside the product (a Linear's bias gradient beside
+  // its weight gradient; the host passes colsum only with B untransposed and
+  // K unsplit): the workgroups of the first tile row add up the B panels they
+  // stage anyway.  Thread t owns column t % BN of the tile and rows
+  // (t / BN) * CS_ROWS .. + CS_ROWS - 1 of every K tile, in K order; the parts
+  // are added in part order at the end.
+  constexpr int CS_PARTS = NT / BN, CS_ROWS = kBK / CS_PARTS;
+  static_assert(TB || (NT % BN == 0 && kBK % CS_PARTS == 0), "column-sum layout");
+  const bool do_cs = !TB && g.colsum != nullptr && tile_m == 0;  // uniform per workgroup
+  const int cs_col = int(threadIdx.x) % BN, cs_part = int(threadIdx.x) / BN;
+  float cs = 0.0f;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1007,7 +1026,35 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
       else mma(fa1, fb1);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (!TB) {
+      if (do_cs) {
+        const float* sb = smem + stage * C::STAGE + C::A_PANEL;
+#pragma unroll
+        for (int r = 0; r < CS_ROWS; ++r) {
+          const int kr = cs_part * CS_ROWS + r;
+          cs += sb[kr * BN + (cs_col ^ ((kr >> 4) << 5))];
+        }
+      }
+    }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+
+  if constexpr (!TB) {
+    if (do_cs) {
+      // The parts of each column in part order, once every wave is done with
+      // the stages.
+      asm volatile("s_barrier" ::: "memory");
+      smem[threadIdx.x] = cs;
+      __syncthreads();
+      if (int(threadIdx.x) < BN) {
+        float t = smem[threadIdx.x];
+#pragma unroll
+        for (int q = 1; q < CS_PARTS; ++q) t += smem[q * BN + threadIdx.x];
+        const int col = n0 + int(threadIdx.x);
+        if (col < g.n) g.colsum[col] = g.colsum_acc ? g.colsum[col] + t : t;
+      }
+      __syncthreads();
+    }
   }
 
   const bool partial = gridDim.z > 1;
@@ -1119,15 +1166,6 @@ constexpr int kRowsWaves = 4;
 constexpr int kRowsStages = 3;
 constexpr int kRowsTile = 32 * 32;  // floats of one operand tile
 
-// Wait until at most N of this wave's vector-memory operations are
-// outstanding (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14, expcnt
-// and lgkmcnt left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
 template <int STAGES>
 __global__ __launch_bounds__(64 * kRowsWaves, 1) void gemm_thin_rows(RowsArgs g) {
   constexpr int STAGE = 2 * kRowsTile;  // A tile, then B tile
@@ -1181,9 +1219,9 @@ __global__ __launch_bounds__(64 * kRowsWaves, 1) void gemm_thin_rows(RowsArgs g)
     // reads completed before its MFMAs.
     if (t + STAGES - 1 < ntiles) {
       issue(t + STAGES - 1);
-      wait_vm<(STAGES - 1) * 8>();  // tile t has landed
+      wait_vmcnt<(STAGES - 1) * 8>();  // tile t has landed
     } else {
-      wait_vm<0>();
+      wait_vmcnt<0>();
     }
     const float* sa = ring + (t % STAGES) * STAGE;
     const float* sb = sa + kRowsTile;
@@ -1253,7 +1291,8 @@ int default_splits(Runtime* rt, int tiles, int k_tiles) {
 }
 
 template <class C, bool TA, bool TB>
-int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, const Workspace& ws, int splits = 0) {
+int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, const Workspace& ws, int splits = 0,
+                    bool* colsum_done = nullptr) {
   g.tiles_m = (g.m + C::BM - 1) / C::BM;
   g.tiles_n = (g.n + C::BN - 1) / C::BN;
   const int tiles = g.tiles_m * g.tiles_n;
@@ -1263,6 +1302,9 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, const Workspace& ws, int 
   g.k_tiles_per_split = (k_tiles + splits - 1) / splits;
   splits = std::max(1, (k_tiles + g.k_tiles_per_split - 1) / g.k_tiles_per_split);
 
+  // Column sums ride only on the LDS tiles with B untransposed and no split.
+  if (g.colsum && (!(vec && std::is_same_v<C, CfgLarge>) || splits > 1 || TB)) g.colsum = nullptr;
+  if (g.colsum && colsum_done) *colsum_done = true;
   float* final_c = g.c;
   float* part = nullptr;
   if (splits > 1) {
@@ -1293,7 +1335,7 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, const Workspace& ws, int 
 // One of the one-workgroup-per-CU LDS configurations: K split so the tiles
 // cover the CUs once, keeping at least eight K tiles per split.
 template <class L, bool TA, bool TB>
-int launch_lds(Runtime* rt, GemmArgs g, const Workspace& ws) {
+int launch_lds(Runtime* rt, GemmArgs g, const Workspace& ws, bool* colsum_done = nullptr) {
   g.tiles_m = (g.m + L::BM - 1) / L::BM;
   g.tiles_n = (g.n + L::BN - 1) / L::BN;
   const int tiles = g.tiles_m * g.tiles_n;
@@ -1301,6 +1343,9 @@ int launch_lds(Runtime* rt, GemmArgs g, const Workspace& ws) {
   int splits = std::max(1, std::min(rt->cu_count / tiles, k_tiles / 8));
   g.k_tiles_per_split = (k_tiles + splits - 1) / splits;
   splits = std::max(1, (k_tiles + g.k_tiles_per_split - 1) / g.k_tiles_per_split);
+  // Column sums ride only with B untransposed and no split.
+  if (g.colsum && (splits > 1 || TB)) g.colsum = nullptr;
+  if (g.colsum && colsum_done) *colsum_done = true;
   float* final_c = g.c;
   float* part = nullptr;
   if (splits > 1) {
@@ -1395,8 +1440,12 @@ int launch_rows(Runtime* rt, const GemmArgs& g0) {
 // K.  M <= 64 uses 32x256 tiles, and M <= 32 the register-direct kernel when
 // its alignment requirements hold.
 template <bool TA, bool TB>
-int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok, const Workspace& ws) {
-  if (tiny_ok(g)) return launch_tiny<TA, TB>(rt, g);
+int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok, const Workspace& ws,
+                bool* colsum_done = nullptr) {
+  if (tiny_ok(g)) {
+    if (g.colsum && colsum_done) *colsum_done = true;
+    return launch_tiny<TA, TB>(rt, g);
+  }
   // M <= 32 with B transposed and a 32-column block for every CU: whole rows
   // of B per workgroup, no split (config 3's dX: 46 -> 31-35 us cold).
   if constexpr (!TA && TB) {
@@ -1411,8 +1460,8 @@ int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok, const 
                               ((g.n + LdsBig::BN - 1) / LdsBig::BN);
     // (K of a few tiles leaves the kernel bound by writing C: more, smaller
     // tiles do better there.)
-    if (big_tiles >= rt->cu_count && g.k >= 256) return launch_lds<LdsBig, TA, TB>(rt, g, ws);
-    if (g.m >= 512 && g.n >= 2048 && g.k >= 2048) return launch_lds<LdsWide, TA, TB>(rt, g, ws);
+    if (big_tiles >= rt->cu_count && g.k >= 256) return launch_lds<LdsBig, TA, TB>(rt, g, ws, colsum_done);
+    if (g.m >= 512 && g.n >= 2048 && g.k >= 2048) return launch_lds<LdsWide, TA, TB>(rt, g, ws, colsum_done);
   }
   const int64_t large_tiles = int64_t((g.m + CfgLarge::BM - 1) / CfgLarge::BM) *
                               ((g.n + CfgLarge::BN - 1) / CfgLarge::BN);
@@ -1420,7 +1469,7 @@ int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok, const 
                               ((g.n + CfgSmall::BN - 1) / CfgSmall::BN);
   if (large_tiles < rt->cu_count && g.k <= 2048 && small_tiles >= rt->cu_count)
     return launch_gemm_cfg<CfgSmall, TA, TB>(rt, g, vec, ws, 1);
-  return launch_gemm_cfg<CfgLarge, TA, TB>(rt, g, vec, ws);
+  return launch_gemm_cfg<CfgLarge, TA, TB>(rt, g, vec, ws, 0, colsum_done);
 }
 
 bool aligned16(const void* p) {
@@ -1459,7 +1508,8 @@ namespace {
 int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
                    const float* a, size_t lda, const float* b, size_t ldb,
                    const float* bias, float* c, size_t ldc, int accumulate, int relu = 0,
-                   const Workspace& ws = Workspace{}) {
+                   const Workspace& ws = Workspace{}, float* colsum = nullptr,
+                   int colsum_acc = 0, bool* colsum_done = nullptr) {
   if (m == 0 || n == 0) return LMP_OK;
   if (!c) return fail(LMP_ERR_INVALID, "gemm: null output");
   if (k == 0 && bias)
@@ -1489,6 +1539,8 @@ int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
   g.accumulate = accumulate ? 1 : 0;
   g.bias = bias;
   g.relu = bias && relu ? 1 : 0;
+  g.colsum = colsum;
+  g.colsum_acc = colsum_acc ? 1 : 0;
   g.vec_out = n % 4 == 0 && ldc % 4 == 0 && aligned16(c) && (!bias || aligned16(bias));
   // 128-bit panel loads need 16-byte rows and a contiguous extent that is a
   // multiple of four.
@@ -1500,10 +1552,11 @@ int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
   // (and a float4 bias read when there is a bias).
   const bool direct_ok =
       vec && (trans_b || (ldc % 4 == 0 && aligned16(c) && (!bias || aligned16(bias))));
-  if (!trans_a && !trans_b) return launch_gemm<false, false>(rt, g, vec, direct_ok, ws);
-  if (!trans_a && trans_b) return launch_gemm<false, true>(rt, g, vec, direct_ok, ws);
-  if (trans_a && !trans_b) return launch_gemm<true, false>(rt, g, vec, direct_ok, ws);
-  return launch_gemm<true, true>(rt, g, vec, direct_ok, ws);
+  bool* cd = colsum_done;
+  if (!trans_a && !trans_b) return launch_gemm<false, false>(rt, g, vec, direct_ok, ws, cd);
+  if (!trans_a && trans_b) return launch_gemm<false, true>(rt, g, vec, direct_ok, ws, cd);
+  if (trans_a && !trans_b) return launch_gemm<true, false>(rt, g, vec, direct_ok, ws, cd);
+  return launch_gemm<true, true>(rt, g, vec, direct_ok, ws, cd);
 }
 
 }  // namespace
@@ -1568,14 +1621,17 @@ extern "C" int lmp_k_gemm_colsum_f32(int trans_a, int trans_b, size_t m, size_t 
                    : (trans_b ? launch_tiny<false, true>(rt, g)
                               : launch_tiny<false, false>(rt, g));
   }
-  // Larger products: the GEMM, then the column sums of op(B) by the
+  // Larger products: the column sums ride in the GEMM when it runs on LDS
+  // tiles with B untransposed and K unsplit (the first tile row adds up the B
+  // panels); otherwise the GEMM, then the column sums of op(B) by the
   // reduction kernels (contiguous B only), accumulated through a scratch
   // buffer when asked.
   if (ldb != (trans_b ? k : n))
     return fail(LMP_ERR_UNSUPPORTED, "gemm_colsum: strided B on the two-launch path");
+  bool fused = false;
   int rc = gemm_f32_entry(trans_a, trans_b, m, n, k, a, lda, b, ldb, nullptr, c, ldc,
-                          accumulate);
-  if (rc != LMP_OK) return rc;
+                          accumulate, 0, Workspace{}, colsum, colsum_accumulate, &fused);
+  if (rc != LMP_OK || fused) return rc;
   // sum over k of op(B)[k][j]: B [k, n] reduces over its rows, B^T (stored
   // [n, k]) over its columns.
   const size_t outer = trans_b ? n : 1, len = k, inner = trans_b ? 1 : n;

@@ -407,10 +407,14 @@ def test_errors_are_reported(hip):
 # column sums of op(B)) together.  C must equal the plain GEMM bit for bit
 # (same kernel), the column sums the float64 sums to the reductions' bar, and
 # accumulation must add the same values in place.  Small products take one
-# launch (the tiny kernel, 16- and 32-wide blocks); (300, 500, 600) runs the
-# GEMM and then the dim-0 reduction.
+# launch (the tiny kernel, 16- and 32-wide blocks); (300, 500, 600) splits K,
+# so it runs the GEMM and then the dim-0 reduction; config 4's weight
+# gradients (4096, 4096, 512) and (4096, 1000, 512) and the ragged
+# (4100, 1000, 500) run on LDS tiles without a split, where the first tile row
+# also sums B (when B is not transposed).
 @pytest.mark.parametrize("m,n,k", [(256, 64, 32), (64, 10, 32), (40, 33, 7), (512, 300, 12),
-                                   (300, 500, 600)], ids=str)
+                                   (300, 500, 600), (4096, 4096, 512), (4096, 1000, 512),
+                                   (4100, 1000, 500)], ids=str)
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_gemm_colsum(hip, m, n, k, ta, tb):
     rng = np.random.default_rng(m * 5 + n + k + ta + 2 * tb)
