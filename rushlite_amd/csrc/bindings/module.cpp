@@ -28,28 +28,28 @@ bool realize_into(TensorImpl* root, const Storage& target);
 
 namespace {
 
-// Nested Python sequences -> flat values + shape (bindings/variable.hpp:21-48).
-void flatten(const py::handle& node, std::vector<Scalar>& data,
-             std::vector<size_t>& shape, size_t depth) {
-  if (py::isinstance<py::sequence>(node) && !py::isinstance<py::str>(node) &&
-      !py::isinstance<py::bytes>(node)) {
-    auto seq = py::reinterpret_borrow<py::sequence>(node);
-    const size_t n = seq.size();
-    if (depth == shape.size()) {
-      if (!data.empty()) throw py::value_error("Rushlite: array must be uniform");
-      shape.push_back(n);
-    } else if (shape[depth] != n) {
-      throw py::value_error("Rushlite: array must be uniform");
-    }
-    for (const auto& item : seq) flatten(item, data, shape, depth + 1);
-  } else {
-    if (depth != shape.size()) throw py::value_error("Rushlite: array must be uniform");
-    try {
-      data.push_back(node.cast<Scalar>());
-    } catch (const py::cast_error&) {
-      throw py::value_error("Rushlite: invalid input type");
-    }
+// Values and shape of Python data that is not an ndarray (nested lists or
+// tuples of numbers, or one number), read through numpy.asarray: numpy works
+// out the shape and refuses ragged nesting, the dtype kind tells numbers from
+// anything else, and the values arrive as float64 -- Lamp3's Scalar -- for
+// the tensor constructor to convert to the target dtype.  The two error texts
+// are the ones Lamp3's Python users see (bindings/variable.hpp:21-48).
+void values_of(const py::handle& data, std::vector<Scalar>& flat, std::vector<size_t>& shape) {
+  py::array arr;
+  try {
+    arr = py::module_::import("numpy").attr("asarray")(data);
+  } catch (py::error_already_set& e) {
+    if (e.matches(PyExc_ValueError)) throw py::value_error("Rushlite: array must be uniform");
+    throw py::value_error("Rushlite: invalid input type");
   }
+  const char kind = arr.dtype().kind();
+  if (kind != 'b' && kind != 'i' && kind != 'u' && kind != 'f')
+    throw py::value_error("Rushlite: invalid input type");
+  const auto values = py::array_t<double, py::array::c_style | py::array::forcecast>::ensure(arr);
+  if (!values) throw py::value_error("Rushlite: invalid input type");
+  shape.assign(values.shape(), values.shape() + values.ndim());
+  if (shape.empty()) shape.push_back(1);  // one number: a [1] tensor, as for a 0-d ndarray
+  flat.assign(values.data(), values.data() + values.size());
 }
 
 DataType dtype_of_numpy(const py::dtype& dt) {
@@ -87,7 +87,7 @@ Tensor tensor_from(const py::object& data, DeviceType device, DataType dtype) {
   }
   std::vector<Scalar> flat;
   std::vector<size_t> shape;
-  flatten(data, flat, shape, 0);
+  values_of(data, flat, shape);
   return Tensor(flat, shape, device, dtype);
 }
 

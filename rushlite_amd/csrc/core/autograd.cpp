@@ -48,7 +48,10 @@ Variable Variable::op_result(const Tensor& data, bool requires_grad) {
 
 const Tensor& Variable::grad() const {
   LMP_CHECK(impl_->requires_grad) << "Cannot access grad() if requires_grad = false";
-  if (!impl_->grad.defined()) impl_->grad = tensor::zeros_like(impl_->data);
+  if (!impl_->grad.defined()) {
+    impl_->grad = tensor::zeros_like(impl_->data);
+    impl_->grad_pass = 0;  // made outside any backward pass
+  }
   return impl_->grad;
 }
 
@@ -72,6 +75,9 @@ bool pending_fill(const Tensor& t, Scalar* value) {
   return true;
 }
 
+// Backward passes run on this thread (VariableImpl::grad_pass).
+thread_local uint64_t t_backward_pass = 0;
+
 // Per-(device, dtype) [1] zero used to start a deferred gradient as 0 + g.
 const Tensor& zero_scalar(DeviceType dev, DataType dt) {
   static std::vector<Tensor> cache(static_cast<size_t>(DeviceType::Count) * 6);
@@ -86,6 +92,7 @@ void Variable::incr_grad(const Tensor& g) {
   if (!impl_->grad.defined()) {
     LMP_INTERNAL_ASSERT(g.shape() == impl_->data.shape())
         << "There should be no broadcasting in incr_grad";
+    impl_->grad_pass = t_backward_pass;
     Scalar v;
     if (pending_fill(g, &v)) {
       // 0 + a constant is that constant (with -0.0 -> +0.0): the gradient
@@ -98,10 +105,6 @@ void Variable::incr_grad(const Tensor& g) {
   }
   LMP_INTERNAL_ASSERT(g.shape() == impl_->grad.shape())
       << "There should be no broadcasting in incr_grad";
-  // A gradient still pending was started in this backward pass (every
-  // gradient is realised before backward() returns), so nothing outside the
-  // pass holds its storage yet: the sum can stay pending too and fuse with the
-  // pending terms, in the same order as the in-place add.
   if (tensor::detail::UnsafeTensorAccessor::getImpl(impl_->grad)->is_deferred()) {
     Scalar a, b;
     if (g.type() == impl_->grad.type() && pending_fill(impl_->grad, &a) && pending_fill(g, &b)) {
@@ -113,8 +116,18 @@ void Variable::incr_grad(const Tensor& g) {
           ->replace_pending_constant(tensor::lazy::make_fill(g.shape(), g.device(), g.type(), sum));
       return;
     }
-    impl_->grad = tops::add(impl_->grad, g);
-    return;
+    if (impl_->grad_pass == t_backward_pass) {
+      // Started in this pass (every other gradient is realised before
+      // backward() returns), so nothing outside the pass holds it: the sum
+      // stays pending and fuses with the pending terms, in the same order as
+      // the in-place add.
+      impl_->grad = tops::add(impl_->grad, g);
+      return;
+    }
+    // A constant left pending by an earlier pass, which a handle taken from
+    // .grad may share: written to its own buffer now (same tensor), then the
+    // term is added in place below, as add_inplace does (variable.cpp:30-35).
+    impl_->grad.realize();
   }
   // A realised gradient receiving a pending term (the backward formulas run
   // captured): grad + g is one fused kernel computed straight into the
@@ -143,6 +156,7 @@ void Variable::incr_grad_matmul(const Tensor& a, const Tensor& b, bool trans_a,
   if (!impl_->grad.defined()) {
     // A GEMM accumulates from +0, so its product equals 0 + product exactly.
     impl_->grad = tops::matmul_t(a, b, trans_a, trans_b);
+    impl_->grad_pass = t_backward_pass;
     LMP_INTERNAL_ASSERT(impl_->grad.shape() == impl_->data.shape())
         << "There should be no broadcasting in incr_grad";
     return;
@@ -166,9 +180,12 @@ bool Variable::incr_grad_linear(Variable& w, Variable& b, const Tensor& x, const
     LMP_INTERNAL_ASSERT(wg.shape() == w.impl_->data.shape())
         << "There should be no broadcasting in incr_grad";
     w.impl_->grad = wg;
+    w.impl_->grad_pass = t_backward_pass;
   }
-  if (!b.impl_->grad.defined())
+  if (!b.impl_->grad.defined()) {
     b.impl_->grad = bg.shape() == b.impl_->data.shape() ? bg : bg.reshape(b.impl_->data.shape());
+    b.impl_->grad_pass = t_backward_pass;
+  }
   return true;
 }
 
@@ -213,7 +230,9 @@ void Variable::backward() {
     // device with a lazy backend.  Values are those of the eager formulas
     // (fused kernels equal eager ones bit for bit).
     tensor::lazy::CaptureGuard capture(true);
+    ++t_backward_pass;
     impl_->grad = tensor::ones_like(impl_->data);
+    impl_->grad_pass = t_backward_pass;
     for (Variable& node : topo)
       if (node.impl_->grad_fn) node.impl_->grad_fn->apply({node});
   }

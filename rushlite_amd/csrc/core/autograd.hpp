@@ -41,6 +41,10 @@ struct VariableImpl {
   // zeros.  Once it exists the buffer stays put: later accumulations are in
   // place, so a pointer taken from .grad stays valid across backward passes.
   Tensor grad;
+  // The backward pass (a per-thread count) in which grad was started: a
+  // gradient still pending from an earlier pass is a constant that a handle
+  // taken from .grad may share, so a later term is added in place.
+  uint64_t grad_pass = 0;
   std::shared_ptr<Function> grad_fn;
   bool requires_grad = false;
 };

@@ -155,4 +155,48 @@ class Arena {
   std::set<std::pair<std::size_t, Addr>> free_;   // (size, addr) of free ones
 };
 
+// Result of asking the device for memory.
+enum class DeviceAlloc { kOk, kOutOfMemory, kError };
+
+// What happens when no free block of an arena can serve a request
+// (allocator.cu:101-125): ask the device for a new segment of
+// max(min_segment, the rounded request); if the device is out of memory and
+// `may_release` allows it (not while a graph is being captured), wait for the
+// queued work so no cached block is still in use, give every wholly free
+// segment of `cache` back to the device, and ask once more.  The new segment
+// joins `target` (the eager arena, or a graph's private one) and the request
+// is served from it.  Dev supplies the device side:
+//   DeviceAlloc malloc(std::size_t bytes, Arena::Addr* base);
+//   bool sync();                         // false: the wait itself failed
+//   bool free(Arena::Addr base);         // false: the release failed
+// Returns kOk with *out set, kOutOfMemory when the device refused even after
+// the release, or kError when a device call failed or the segment it returned
+// cannot be added (that segment goes back to the device); *segment gets the
+// size asked for.
+template <class Dev>
+DeviceAlloc grow_and_allocate(Arena& target, Arena& cache, std::size_t bytes,
+                              std::size_t min_segment, bool may_release, Dev& dev,
+                              Arena::Span* out, std::size_t* segment) {
+  const std::size_t need = target.round_up(bytes);
+  const std::size_t seg = need > min_segment ? need : min_segment;
+  *segment = seg;
+  Arena::Addr base = 0;
+  DeviceAlloc st = dev.malloc(seg, &base);
+  if (st == DeviceAlloc::kOutOfMemory && may_release) {
+    if (!dev.sync()) return DeviceAlloc::kError;
+    for (const Arena::Span& s : cache.take_free_segments())
+      if (!dev.free(s.addr)) return DeviceAlloc::kError;
+    st = dev.malloc(seg, &base);
+  }
+  if (st != DeviceAlloc::kOk) return st;
+  if (!target.add_segment(base, seg)) {
+    (void)dev.free(base);
+    return DeviceAlloc::kError;
+  }
+  auto span = target.allocate(bytes);
+  if (!span) return DeviceAlloc::kError;
+  *out = *span;
+  return DeviceAlloc::kOk;
+}
+
 }  // namespace lmp_hip

@@ -90,12 +90,19 @@ std::string cache_dir() {
   return "";
 }
 
-// Everything the code object depends on.
+// Everything the code object depends on: the source, the target, the
+// options, and the compiler's release down to its patch level (hipRTC
+// reports major.minor only; the HIP runtime and driver versions it ships with
+// carry the patch, so a point release of ROCm misses the cache).
 std::string jit_identity(const std::string& source, const std::string& arch) {
-  int major = 0, minor = 0;
+  int major = 0, minor = 0, runtime = 0, driver = 0;
   hiprtcVersion(&major, &minor);
-  std::string id = "lmp-jit-v1\n" + arch + "\nhiprtc " + std::to_string(major) + "." +
-                   std::to_string(minor) + "\n";
+  if (hipRuntimeGetVersion(&runtime) != hipSuccess) runtime = -1;
+  if (hipDriverGetVersion(&driver) != hipSuccess) driver = -1;
+  (void)hipGetLastError();
+  std::string id = "lmp-jit-v2\n" + arch + "\nhiprtc " + std::to_string(major) + "." +
+                   std::to_string(minor) + "\nhip runtime " + std::to_string(runtime) +
+                   "\nhip driver " + std::to_string(driver) + "\n";
   for (const auto& o : compile_options(arch)) id += o + "\n";
   id += source;
   return id;

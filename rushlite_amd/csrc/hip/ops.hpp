@@ -1,6 +1,6 @@
 // Per-element functors of the backend, one definition shared by the eager
 // kernels.  The hipRTC fusion kernels spell the same expressions in source
-// form (core/hip_lazy_backend.cpp), so eager and fused results agree bit for
+// form (core/hip_fusion.cpp), so eager and fused results agree bit for
 // bit.  Semantics follow Lamp3's CPU functors (cpu/kernels.hpp:22-174): the
 // arithmetic happens in the output dtype, comparisons yield 1 or 0 in the
 // output dtype, clamp returns NaN and -0.0 unchanged, and the clamp backward

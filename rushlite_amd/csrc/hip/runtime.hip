@@ -108,37 +108,51 @@ int init_locked(int device) {
   return LMP_OK;
 }
 
+// The device side of Arena's growth policy: hipMalloc, a stream wait and
+// hipFree, keeping the text of the first failure.
+struct HipSegments {
+  std::string error;
+  DeviceAlloc malloc(size_t bytes, Arena::Addr* base) {
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, bytes);
+    if (e == hipSuccess) {
+      *base = reinterpret_cast<Arena::Addr>(p);
+      return DeviceAlloc::kOk;
+    }
+    (void)hipGetLastError();
+    error = "hipMalloc of " + std::to_string(bytes) + " bytes failed: " + hipGetErrorString(e);
+    return e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation ? DeviceAlloc::kOutOfMemory
+                                                                     : DeviceAlloc::kError;
+  }
+  bool sync() {
+    const hipError_t e = hipStreamSynchronize(g_rt.stream);
+    if (e != hipSuccess) error = std::string("hipStreamSynchronize: ") + hipGetErrorString(e);
+    return e == hipSuccess;
+  }
+  bool free(Arena::Addr base) {
+    const hipError_t e = hipFree(reinterpret_cast<void*>(base));
+    if (e != hipSuccess) error = std::string("hipFree: ") + hipGetErrorString(e);
+    return e == hipSuccess;
+  }
+};
+
 int grow_and_allocate(Pool& p, Arena& arena, size_t bytes, void** out) {
-  const size_t need = arena.round_up(bytes);
-  const size_t seg = std::max(kMinSegment, need);
-  void* base = nullptr;
-  hipError_t e = hipMalloc(&base, seg);
+  HipSegments dev;
+  Arena::Span span;
+  size_t seg = 0;
   // The release-and-retry path synchronises the stream, which a capture forbids.
-  if ((e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) && !p.capturing) {
-    (void)hipGetLastError();
-    // Release cached segments once, then retry (allocator.cu:101-125).
-    hipError_t se = hipStreamSynchronize(g_rt.stream);
-    if (se != hipSuccess)
-      return fail(LMP_ERR_RUNTIME, std::string("hipStreamSynchronize: ") +
-                                       hipGetErrorString(se));
-    for (const Arena::Span& s : p.arena.take_free_segments())
-      (void)hipFree(reinterpret_cast<void*>(s.addr));
-    e = hipMalloc(&base, seg);
+  const DeviceAlloc st = lmp_hip::grow_and_allocate(arena, p.arena, bytes, kMinSegment,
+                                                    !p.capturing, dev, &span, &seg);
+  if (st == DeviceAlloc::kOk) {
+    ++p.device_mallocs;
+    *out = reinterpret_cast<void*>(span.addr);
+    return LMP_OK;
   }
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(LMP_ERR_OOM, "hipMalloc of " + std::to_string(seg) +
-                                 " bytes failed: " + hipGetErrorString(e));
-  }
-  ++p.device_mallocs;
-  if (!arena.add_segment(reinterpret_cast<Arena::Addr>(base), seg))
-    return fail(LMP_ERR_RUNTIME, "allocator: hipMalloc returned a misaligned "
-                                 "or overlapping segment");
-  auto span = arena.allocate(bytes);
-  if (!span)
-    return fail(LMP_ERR_RUNTIME, "allocator: new segment cannot serve request");
-  *out = reinterpret_cast<void*>(span->addr);
-  return LMP_OK;
+  if (st == DeviceAlloc::kOutOfMemory) return fail(LMP_ERR_OOM, dev.error);
+  return fail(LMP_ERR_RUNTIME,
+              dev.error.empty() ? std::string("allocator: the new segment of ") + std::to_string(seg) +
+                                      " bytes cannot serve the request"
+                                : dev.error);
 }
 
 // Hand the segments of destroyed graphs whose blocks are all freed back to

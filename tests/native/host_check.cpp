@@ -1,15 +1,20 @@
 // Host-only checks of the backend's CPU-side logic: the caching arena
-// (best fit, split, coalesce, segment release, unknown-address rejection)
-// and the magic-number divider.  Built and run by tests/test_host_native.py
-// with g++; no GPU involved.
+// (best fit, split, coalesce, segment release, unknown-address rejection),
+// its growth policy on an out-of-memory device (wait, release the cached free
+// segments, retry once; allocator.cu:101-125) against a synthetic device, and
+// the magic-number divider.  Built and run by tests/test_host_native.py with
+// g++; no GPU involved.
 #include <cassert>
 #include <cstdio>
 #include <random>
+#include <string>
+#include <vector>
 
 #include "arena.hpp"
 #include "fastdiv.hpp"
 
 using lmp_hip::Arena;
+using lmp_hip::DeviceAlloc;
 using lmp_hip::FastDiv;
 
 #define CHECK(c)                                                  \
@@ -68,6 +73,124 @@ int arena_checks() {
   return 0;
 }
 
+// A device with `capacity` bytes: hands out aligned, non-overlapping bases,
+// refuses a request that would exceed its capacity, and logs every call.
+struct FakeDevice {
+  std::size_t capacity, held = 0;
+  Arena::Addr next = 0x40000000;
+  std::vector<std::pair<Arena::Addr, std::size_t>> live;
+  std::vector<std::string> log;
+  bool fail_sync = false;
+  DeviceAlloc malloc(std::size_t bytes, Arena::Addr* base) {
+    log.push_back("malloc " + std::to_string(bytes));
+    if (held + bytes > capacity) return DeviceAlloc::kOutOfMemory;
+    *base = next;
+    next += bytes;
+    held += bytes;
+    live.push_back({*base, bytes});
+    return DeviceAlloc::kOk;
+  }
+  bool sync() {
+    log.push_back("sync");
+    return !fail_sync;
+  }
+  bool free(Arena::Addr base) {
+    log.push_back("free " + std::to_string(base));
+    for (auto it = live.begin(); it != live.end(); ++it)
+      if (it->first == base) {
+        held -= it->second;
+        live.erase(it);
+        return true;
+      }
+    return false;
+  }
+};
+
+int growth_policy_checks() {
+  constexpr std::size_t kMin = 1 << 20;  // minimum segment
+  using Log = std::vector<std::string>;
+  {
+    // Two cached segments: one wholly free (1 MiB), one holding a live block
+    // (2 MiB).  A 1.5 MiB request fits no free block, and the 3.5 MiB device
+    // has no room for a 1.5 MiB segment until the free one is given back: the
+    // policy must wait, hand back exactly that segment, and retry once.
+    FakeDevice dev{7 << 19};
+    Arena eager(256);
+    Arena::Addr a = 0, b = 0;
+    CHECK(dev.malloc(kMin, &a) == DeviceAlloc::kOk && eager.add_segment(a, kMin));
+    CHECK(dev.malloc(2 * kMin, &b) == DeviceAlloc::kOk && eager.add_segment(b, 2 * kMin));
+    auto keep = eager.allocate(3 * kMin / 2);  // lives in the 2 MiB segment
+    CHECK(keep && keep->addr == b);
+    dev.log.clear();
+    Arena::Span span;
+    std::size_t seg = 0;
+    auto st = lmp_hip::grow_and_allocate(eager, eager, 1536 << 10, kMin, true, dev, &span, &seg);
+    CHECK(st == DeviceAlloc::kOk && seg == std::size_t(1536) << 10);
+    CHECK((dev.log == Log{"malloc 1572864", "sync", "free " + std::to_string(a), "malloc 1572864"}));
+    CHECK(eager.segment_count() == 2 && span.size == std::size_t(1536) << 10);
+    CHECK(eager.release(span.addr) && eager.release(keep->addr));
+  }
+  {
+    // Still too little after the release: one retry, then out of memory,
+    // and nothing is added to the arena.
+    FakeDevice dev{kMin};
+    Arena eager(256);
+    Arena::Addr a = 0;
+    CHECK(dev.malloc(kMin, &a) == DeviceAlloc::kOk && eager.add_segment(a, kMin));
+    auto keep = eager.allocate(100);
+    dev.log.clear();
+    Arena::Span span;
+    std::size_t seg = 0;
+    auto st = lmp_hip::grow_and_allocate(eager, eager, 4096, kMin, true, dev, &span, &seg);
+    CHECK(st == DeviceAlloc::kOutOfMemory);
+    CHECK((dev.log == Log{"malloc 1048576", "sync", "malloc 1048576"}));  // no free segment to give
+    CHECK(eager.segment_count() == 1 && eager.release(keep->addr));
+  }
+  {
+    // During a graph capture (no release allowed): no wait, no release, one
+    // request only; a graph's private arena grows while releases would come
+    // from the eager arena.
+    FakeDevice dev{kMin};
+    Arena eager(256), graph(256);
+    Arena::Addr a = 0;
+    CHECK(dev.malloc(kMin, &a) == DeviceAlloc::kOk && eager.add_segment(a, kMin));
+    dev.log.clear();
+    Arena::Span span;
+    std::size_t seg = 0;
+    CHECK(lmp_hip::grow_and_allocate(graph, eager, 64, kMin, false, dev, &span, &seg) ==
+          DeviceAlloc::kOutOfMemory);
+    CHECK((dev.log == Log{"malloc 1048576"}) && eager.segment_count() == 1);
+    // with release allowed the eager arena's free segment goes back and the
+    // new segment joins the graph's arena
+    dev.log.clear();
+    CHECK(lmp_hip::grow_and_allocate(graph, eager, 64, kMin, true, dev, &span, &seg) ==
+          DeviceAlloc::kOk);
+    CHECK(eager.segment_count() == 0 && graph.segment_count() == 1 && span.size == 256);
+  }
+  {
+    // A failed wait is an error, and nothing is released after it.
+    FakeDevice dev{0};
+    dev.fail_sync = true;
+    Arena eager(256);
+    Arena::Span span;
+    std::size_t seg = 0;
+    CHECK(lmp_hip::grow_and_allocate(eager, eager, 64, kMin, true, dev, &span, &seg) ==
+          DeviceAlloc::kError);
+    CHECK((dev.log == std::vector<std::string>{"malloc 1048576", "sync"}));
+  }
+  {
+    // A request above the minimum segment gets a segment of its own size.
+    FakeDevice dev{64 << 20};
+    Arena eager(256);
+    Arena::Span span;
+    std::size_t seg = 0;
+    CHECK(lmp_hip::grow_and_allocate(eager, eager, (5 << 20) + 1, kMin, true, dev, &span, &seg) ==
+          DeviceAlloc::kOk);
+    CHECK(seg == (std::size_t(5) << 20) + 256 && dev.held == seg);
+  }
+  return 0;
+}
+
 int fastdiv_checks() {
   std::mt19937_64 rng(1);
   const uint32_t special[] = {1, 2, 3, 4, 5, 7, 10, 1000, 1024, 2048, 4096, 16383, 65535,
@@ -95,6 +218,7 @@ int fastdiv_checks() {
 
 int main() {
   if (arena_checks()) return 1;
+  if (growth_policy_checks()) return 1;
   if (fastdiv_checks()) return 1;
   std::printf("host checks ok\n");
   return 0;

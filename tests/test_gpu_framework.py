@@ -116,6 +116,28 @@ def test_repeated_backward_accumulates_in_place(rsl):
     close(a.grad.tolist(), GOLDEN["repeated_backward"]["grad_a"])
 
 
+def test_constant_gradient_then_a_term_accumulates_in_place(rsl):
+    """a + b backward leaves a.grad the seed passed through (a constant, kept
+    pending); a tensor handle taken from .grad then (a Variable made from it
+    shares the tensor), and the gradient after a second pass adds a
+    non-constant term (a * a: 2a), are the same tensor in the same buffer
+    holding 1 + 2a, as the reference's in-place accumulation gives
+    (variable.cpp:30-35, autograd_tests.cpp:487-514)."""
+    a = V(rsl, [[1.0, 2.0], [3.0, 4.0]], True)
+    b = V(rsl, [[5.0, 6.0], [7.0, 8.0]], True)
+    (a + b).backward()
+    held = rsl.Variable(a.grad)  # not read yet: still the pending constant
+    (a * a).backward()
+    want = [3.0, 5.0, 7.0, 9.0]
+    assert a.grad.tolist() == want
+    assert held.tolist() == want
+    assert rsl._storage_ptr(held.data) == rsl._storage_ptr(a.grad)
+    # a third pass keeps that buffer
+    (a * 2.0).backward()
+    assert held.tolist() == [5.0, 7.0, 9.0, 11.0]
+    assert rsl._storage_ptr(held.data) == rsl._storage_ptr(a.grad)
+
+
 def test_tensor_api(rsl):
     t = rsl._C._Tensor([1.0, 2.0, 3.0, 4.0, 5.0, 6.0], [3, 2], rsl.device.hip, rsl.dtype.float32)
     assert t.index([2, 1]) == 6.0 and t.index([1, 0]) == 3.0

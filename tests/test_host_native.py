@@ -87,3 +87,24 @@ def test_fusion_codegen_compiles_with_hiprtc(tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600)
     assert out.returncode == 0, out.stdout[-3000:] + out.stderr[-2000:]
     assert "fusion codegen ok" in out.stdout
+
+
+def test_sequence_constructor_shapes_and_errors():
+    """Variable(nested sequence) on the CPU device: the shape numpy derives,
+    numbers of any kind as their float64 values, one number as a [1] tensor,
+    and Lamp3's two error texts for ragged nesting and non-numeric items
+    (bindings/variable.hpp:21-48)."""
+    import rushlite_amd as rsl
+    cpu = rsl.device.cpu
+    for data, shape, values in (([[1, 2], [3, 4]], [2, 2], [1.0, 2.0, 3.0, 4.0]),
+                                (((1, 2), (3, 4)), [2, 2], [1.0, 2.0, 3.0, 4.0]),
+                                ([1.5, True, 3], [3], [1.5, 1.0, 3.0]),
+                                (2.5, [1], [2.5]), ([], [0], []), ([[]], [1, 0], [])):
+        v = rsl.Variable(data, device=cpu)
+        assert v.shape == shape and v.data.tolist() == values, data
+    for bad in ([[1, 2], [3]], [[1, 2], 3]):
+        with pytest.raises(ValueError, match="Rushlite: array must be uniform"):
+            rsl.Variable(bad, device=cpu)
+    for bad in ([1, "a"], [1, None], "abc", [1 + 2j]):
+        with pytest.raises(ValueError, match="Rushlite: invalid input type"):
+            rsl.Variable(bad, device=cpu)

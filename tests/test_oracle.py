@@ -8,8 +8,10 @@ folds in pure Python for the reduction / matmul order, float64 numpy for sums
 and products, and torch float64 autograd for the gradient formulas.
 """
 import json
-import zlib
 import math
+import subprocess
+import sys
+import zlib
 from pathlib import Path
 
 import numpy as np
@@ -30,6 +32,14 @@ def correctly_rounded(fn, *args):
 
 
 # ------------------------------------------------------------ golden vectors
+
+
+def test_known_answer_fixture_matches_its_transcription():
+    """tests/golden/lamp3_known_answers.json is exactly what the committed
+    transcription script writes."""
+    script = Path(__file__).parent / "golden" / "make_known_answers.py"
+    assert subprocess.run([sys.executable, str(script), "--check"]).returncode == 0
+
 
 @pytest.mark.parametrize("case", GOLDEN["tensor"], ids=lambda c: c["name"])
 def test_known_answers_binary(oracle, case):
