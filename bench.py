@@ -513,10 +513,10 @@ def cpu_baseline(seconds, gpu_extra, host):
     while True:
         O.binary("add", O.binary("mul", a, a, **fast), b, **fast)
         reps += 1
-        el = time.perf_counter() - t0
-        if (el >= seconds and reps >= 3) or reps >= 5000:
+        c1_el = time.perf_counter() - t0
+        if (c1_el >= seconds and reps >= 3) or reps >= 5000:
             break
-    c1_value = BYTES_C1 * reps / el / 1e9
+    c1_value = BYTES_C1 * reps / c1_el / 1e9
 
     # config 1b: the 6-op chain as six eager ops
     def chain6():
@@ -606,7 +606,7 @@ def cpu_baseline(seconds, gpu_extra, host):
             "cores": O.num_threads(fast=True), "kind": "port",
             "sample": f"full config-1 workload (c = a*a + b, a [8192,8192], b [8192,1]) "
                       f"x {reps} reps, eager mul then broadcast add as Lamp3's CPU path "
-                      f"runs it, liblamp_cpu_fast.so (-O3 -ffast-math, OpenMP), {el:.1f} s",
+                      f"runs it, liblamp_cpu_fast.so (-O3 -ffast-math, OpenMP), {c1_el:.1f} s",
             "host": host,
             "configs": configs}
 
