@@ -425,7 +425,9 @@ struct DirectFrag {
   v4f b[4];  // TB: b[q][s]; !TB: b[s][q]
 
   // Loads are unconditional: a lane whose element lies outside the matrix (or
-  // past ke) reads zeros from g_direct_zeros instead.  Guarded loads would
+  // past ke) reads zeros from g_direct_zeros instead.  B (the weight, read
+  // once) is loaded with the nontemporal hint so it does not push A out of
+  // the L2.  Guarded loads would
   // each sit behind a branch, and a select after the load would wait for it
   // at once; either way nothing would stay in flight while the MFMAs run.
   __device__ __forceinline__ void load(const DirectArgs& g, int row, int n0, int k0,
@@ -447,16 +449,16 @@ struct DirectFrag {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const bool ok = col < g.n && kq + s < ke;
-        b[s] = *reinterpret_cast<const v4f*>(ok ? g.b + int64_t(kq + s) * g.ldb + col
-                                                : g_direct_zeros);
+        b[s] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(
+            ok ? g.b + int64_t(kq + s) * g.ldb + col : g_direct_zeros));
       }
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int col = n0 + 32 * q + li;
         const bool ok = col < g.n && kq < ke;
-        b[q] = *reinterpret_cast<const v4f*>(ok ? g.b + int64_t(col) * g.ldb + kq
-                                                : g_direct_zeros);
+        b[q] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(
+            ok ? g.b + int64_t(col) * g.ldb + kq : g_direct_zeros));
       }
     }
   }
@@ -834,6 +836,11 @@ __device__ __forceinline__ int kswz(int row) { return (row & 7) ^ ((row >> 3) & 
 __device__ __forceinline__ void lds_dma16(const float* src, float* lds) {
   __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
 }
+// The same with the nontemporal hint (cache-policy bit 1, `nt`): for operand
+// lines read once, so they do not push reused lines out of the L2.
+__device__ __forceinline__ void lds_dma16_nt(const float* src, float* lds) {
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 2);
+}
 
 // Wait until at most N of this wave's vector-memory operations are
 // outstanding (gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14, expcnt
@@ -1207,7 +1214,7 @@ __global__ __launch_bounds__(64 * kRowsWaves, 1) void gemm_thin_rows(RowsArgs g)
       lds_dma16(asrc[q] && k0 + dk[q] < ke ? asrc[q] + k0 : zero, st + q * 256);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      lds_dma16(bsrc[q] && k0 + dk[q] < ke ? bsrc[q] + k0 : zero, st + kRowsTile + q * 256);
+      lds_dma16_nt(bsrc[q] && k0 + dk[q] < ke ? bsrc[q] + k0 : zero, st + kRowsTile + q * 256);
   };
 
   v16f acc = v16f(0.0f);
