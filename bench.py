@@ -498,10 +498,16 @@ def cpu_baseline(seconds, gpu_extra, host):
     """Every config on the oracle's fast build (-O3 -ffast-math, OpenMP), the
     way Lamp3's CPU backend runs it: eager ops, per-output sequential
     reductions, i-j-k GEMMs (cpu/binary.cpp, cpu/expand.cpp, cpu/reduct.cpp:7-19,
-    cpu/matrix.cpp:26-33).  Work is bounded to a few seconds per config; each
-    entry states its sample and repetitions."""
+    cpu/matrix.cpp:26-33), with flush-to-zero and denormals-are-zero on, the
+    mode a -ffast-math build's startup code sets.  Work is bounded to a few
+    seconds per config; each entry states its sample and repetitions."""
     from oracle import lamp_oracle as O
     O.load(fast=True)
+    with O.denormal_flush():
+        return _cpu_baseline(O, seconds, gpu_extra, host)
+
+
+def _cpu_baseline(O, seconds, gpu_extra, host):
     fast = dict(fast=True)
     configs = {}
 
@@ -603,10 +609,11 @@ def cpu_baseline(seconds, gpu_extra, host):
                   "full-batch estimate scales it by 512/16 (GEMM-dominated)"}
 
     return {"value": round(c1_value, 2), "unit": "GB/s",
-            "cores": O.num_threads(fast=True), "kind": "port",
+            "cores": O.num_threads(fast=True), "kind": "port", "isa": O.host_isa(),
             "sample": f"full config-1 workload (c = a*a + b, a [8192,8192], b [8192,1]) "
                       f"x {reps} reps, eager mul then broadcast add as Lamp3's CPU path "
-                      f"runs it, liblamp_cpu_fast.so (-O3 -ffast-math, OpenMP), {c1_el:.1f} s",
+                      f"runs it, {O.fast_library_name()} (-O3 -ffast-math, OpenMP, "
+                      f"{O.host_isa()}, flush-to-zero), {c1_el:.1f} s",
             "host": host,
             "configs": configs}
 

@@ -25,12 +25,16 @@
  * is what the reference's eager per-op execution specifies.  The timing
  * build (liblamp_cpu_fast.so) adds the reference's -O3 -ffast-math
  * (CMakeLists.txt:59-64) so the CPU baseline runs at the speed the
- * reference's own flags allow.
+ * reference's own flags allow.  It is linked without the fast-math startup
+ * code (-mno-daz-ftz), which would otherwise switch the loading process to
+ * flush-to-zero for good; lcpu_set_denormal_flush() gives that mode to the
+ * timed region explicitly instead.
  */
 #include <float.h>
 #include <math.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <xmmintrin.h>
 
 #ifdef _OPENMP
 #include <omp.h>
@@ -93,6 +97,24 @@ int lcpu_num_threads(void) {
 #else
   return 1;
 #endif
+}
+
+/* Flush-to-zero (MXCSR bit 15) and denormals-are-zero (bit 6) on or off, in
+ * the calling thread and in every thread of the OpenMP team: the mode a
+ * -ffast-math executable starts in.  Returns the number of threads set. */
+int lcpu_set_denormal_flush(int on) {
+  const unsigned bits = (1u << 15) | (1u << 6);
+  int n = 1;
+  _mm_setcsr(on ? (_mm_getcsr() | bits) : (_mm_getcsr() & ~bits));
+#ifdef _OPENMP
+#pragma omp parallel
+  {
+    _mm_setcsr(on ? (_mm_getcsr() | bits) : (_mm_getcsr() & ~bits));
+#pragma omp single
+    n = omp_get_num_threads();
+  }
+#endif
+  return n;
 }
 
 /* out has `ndim` dims of out_shape, contiguous.  sa/sb: per-dim element

@@ -38,7 +38,7 @@ _fast_default = False
 
 class fast_build:
     """Within this block the wrappers (and so OVar, mlp_step, mlp_train) run on
-    liblamp_cpu_fast.so, the reference's -O3 -ffast-math build, unless a call
+    the fast build (the reference's -O3 -ffast-math flags), unless a call
     passes fast= itself.  bench.py's CPU baseline times the MLPs this way."""
 
     def __enter__(self):
@@ -51,12 +51,39 @@ class fast_build:
         _fast_default = self._prev
 
 
+# CPU flags that x86-64-v4 code may use beyond x86-64-v3 (AVX-512 F, BW, CD,
+# DQ, VL): the fast build for that level runs only where all are present.
+_V4_FLAGS = {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"}
+
+
+def host_isa() -> str:
+    """'x86-64-v4' when /proc/cpuinfo lists every AVX-512 flag x86-64-v4
+    needs, else 'x86-64-v3' (AVX2 + FMA, the level every build requires)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("flags"):
+                flags = set(line.partition(":")[2].split())
+                return "x86-64-v4" if _V4_FLAGS <= flags else "x86-64-v3"
+    except OSError:
+        pass
+    return "x86-64-v3"
+
+
+def fast_library_name() -> str:
+    """The fast build load(fast=True) uses on this host: the x86-64-v4 one
+    where the CPU has AVX-512 (what the reference's -march=native gives
+    there) and it was built, else the x86-64-v3 one."""
+    if host_isa() == "x86-64-v4" and (HERE / "liblamp_cpu_fast_v4.so").exists():
+        return "liblamp_cpu_fast_v4.so"
+    return "liblamp_cpu_fast.so"
+
+
 def load(fast: bool | None = None) -> C.CDLL:
-    """liblamp_cpu.so (strict IEEE, for parity) or liblamp_cpu_fast.so
-    (the reference's -ffast-math flags, for the timed CPU baseline)."""
+    """liblamp_cpu.so (strict IEEE, for parity) or the fast build (the
+    reference's -ffast-math flags, for the timed CPU baseline)."""
     if fast is None:
         fast = _fast_default
-    name = "liblamp_cpu_fast.so" if fast else "liblamp_cpu.so"
+    name = fast_library_name() if fast else "liblamp_cpu.so"
     if name not in _libs:
         path = HERE / name
         if not path.exists():
@@ -73,6 +100,8 @@ def load(fast: bool | None = None) -> C.CDLL:
         lib.lcpu_fill_f32.argtypes = [P, i64, C.c_double]
         lib.lcpu_add_inplace_f32.argtypes = [P, P, i64]
         lib.lcpu_num_threads.restype = C.c_int
+        lib.lcpu_set_denormal_flush.argtypes = [C.c_int]
+        lib.lcpu_set_denormal_flush.restype = C.c_int
         for fn in ("lcpu_binary_f32", "lcpu_unary_f32", "lcpu_reduce_f32",
                    "lcpu_matmul_f32", "lcpu_transpose_f32", "lcpu_fill_f32",
                    "lcpu_add_inplace_f32"):
@@ -181,6 +210,19 @@ def add_inplace(dst: np.ndarray, src, fast: bool | None = None) -> None:
 
 def num_threads(fast: bool | None = None) -> int:
     return load(fast).lcpu_num_threads()
+
+
+class denormal_flush:
+    """Flush-to-zero and denormals-are-zero in this thread and the oracle's
+    OpenMP threads for the block (the mode a -ffast-math executable runs in),
+    IEEE denormals again afterwards."""
+
+    def __enter__(self):
+        load(fast=True).lcpu_set_denormal_flush(1)
+        return self
+
+    def __exit__(self, *exc):
+        load(fast=True).lcpu_set_denormal_flush(0)
 
 
 # ----------------------------------------------------------------- autograd

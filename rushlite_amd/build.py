@@ -4,7 +4,8 @@ Outputs (all in-tree so they travel with the repository snapshot):
   rushlite_amd/lib/liblmp_hip.so      C-ABI HIP backend (hipcc, gfx950)
   rushlite_amd/_C.<abi>.so             Lamp3 host framework + pybind11 module
   oracle/liblamp_cpu.so               CPU oracle, strict IEEE (test only)
-  oracle/liblamp_cpu_fast.so          CPU oracle with the reference's flags
+  oracle/liblamp_cpu_fast.so          CPU oracle with the reference's flags (AVX2 + FMA)
+  oracle/liblamp_cpu_fast_v4.so       the same for AVX-512 hosts
 
 Run ``python -m rushlite_amd.build`` (or ``__graft_entry__.build()``).
 """
@@ -107,20 +108,29 @@ def build_ext() -> Path:
 
 
 def build_oracle() -> list[Path]:
-    """Compile the CPU oracle twice: strict IEEE and reference flags."""
+    """Compile the CPU oracle: strict IEEE (parity) and the reference's
+    -O3 -ffast-math flags (timed baseline), the latter for two ISA levels."""
     src = ORACLE / "lamp_cpu.c"
-    # x86-64-v3 (AVX2 + FMA) rather than -march=native: the library is built
-    # here and must also load on the GPU host, whose CPU model differs.
-    common = [CC, "-O3", "-march=x86-64-v3", "-fopenmp", "-fPIC", "-shared",
-              "-std=c11"]
+    # Named ISA levels rather than -march=native: the libraries are built here
+    # and loaded on the GPU host, whose CPU differs.  The loader takes the
+    # x86-64-v4 (AVX-512) fast build where the host's CPU flags allow it, which
+    # is what -march=native gives on such a host, and x86-64-v3 (AVX2 + FMA)
+    # otherwise.  -mno-daz-ftz keeps gcc from linking its fast-math startup
+    # code into the fast builds: it would set flush-to-zero in every process
+    # that loads them (numpy included); the baseline sets that mode for its
+    # timed region itself (lcpu_set_denormal_flush).
+    common = [CC, "-O3", "-fopenmp", "-fPIC", "-shared", "-std=c11"]
     jobs = [
-        [*common, "-ffp-contract=off", str(src), "-o",
+        [*common, "-march=x86-64-v3", "-ffp-contract=off", str(src), "-o",
          str(ORACLE / "liblamp_cpu.so"), "-lm"],
-        [*common, "-ffast-math", str(src), "-o",
+        [*common, "-march=x86-64-v3", "-ffast-math", "-mno-daz-ftz", str(src), "-o",
          str(ORACLE / "liblamp_cpu_fast.so"), "-lm"],
+        [*common, "-march=x86-64-v4", "-ffast-math", "-mno-daz-ftz", str(src), "-o",
+         str(ORACLE / "liblamp_cpu_fast_v4.so"), "-lm"],
     ]
     _parallel(jobs)
-    return [ORACLE / "liblamp_cpu.so", ORACLE / "liblamp_cpu_fast.so"]
+    return [ORACLE / "liblamp_cpu.so", ORACLE / "liblamp_cpu_fast.so",
+            ORACLE / "liblamp_cpu_fast_v4.so"]
 
 
 def build_all() -> None:

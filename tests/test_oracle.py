@@ -31,6 +31,66 @@ def correctly_rounded(fn, *args):
     return fn(*[np.asarray(a, np.float64) for a in args]).astype(np.float32)
 
 
+# ------------------------------------------------------- timing (fast) builds
+
+
+def _fast_builds(oracle):
+    """Paths of the fast builds this host can run: x86-64-v3 always, the
+    AVX-512 one where the CPU has its flags."""
+    names = ["liblamp_cpu_fast.so"]
+    if oracle.host_isa() == "x86-64-v4":
+        names.append("liblamp_cpu_fast_v4.so")
+    return [oracle.HERE / n for n in names]
+
+
+def test_fast_builds_leave_the_process_denormal_mode_alone(oracle):
+    """Loading a -ffast-math build must not switch the process to
+    flush-to-zero (gcc's fast-math startup code would: numpy's 1e-40 * 2
+    would become 0 for the rest of the process)."""
+    import ctypes
+    for path in _fast_builds(oracle):
+        ctypes.CDLL(str(path))
+        assert np.float32(1e-40) * np.float32(2) != 0, path.name
+
+
+def test_denormal_flush_is_scoped(oracle):
+    x = np.array([1e-40, 3.0], np.float32)
+    two = np.array([2.0], np.float32)
+    with oracle.denormal_flush():
+        assert oracle.binary("mul", x, two, fast=True)[0] == 0  # flushed
+    assert oracle.binary("mul", x, two, fast=True)[0] == np.float32(1e-40) * np.float32(2)
+    assert np.float32(1e-40) * np.float32(2) != 0
+
+
+def test_fast_builds_agree_with_the_strict_build():
+    """Both ISA levels of the timed build compute what the parity build does:
+    single IEEE operations bit for bit, sums to the reductions' 1e-5."""
+    import ctypes
+    from oracle import lamp_oracle as O
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal(100003).astype(np.float32)
+    b = rng.standard_normal(100003).astype(np.float32)
+    want_mul = O.binary("mul", a, b, fast=False)
+    want_sum = O.reduce("sum", a.reshape(1, -1), 1, fast=False)
+    for path in _fast_builds(O):
+        lib = ctypes.CDLL(str(path))
+        P = ctypes.c_void_p
+        lib.lcpu_binary_f32.argtypes = [ctypes.c_int, P, P, P, ctypes.c_int, P, P, P,
+                                        ctypes.c_int, ctypes.c_double, ctypes.c_double]
+        lib.lcpu_reduce_f32.argtypes = [ctypes.c_int, P, P, ctypes.c_int, P, ctypes.c_int]
+        out = np.empty_like(a)
+        shape = np.array([a.size], np.int64)
+        strides = np.array([1], np.int64)
+        lib.lcpu_binary_f32(O.BIN["mul"], out.ctypes.data, a.ctypes.data, b.ctypes.data, 1,
+                            shape.ctypes.data, strides.ctypes.data, strides.ctypes.data, 0,
+                            0.0, 0.0)
+        assert np.array_equal(out, want_mul), path.name
+        red = np.empty((1, 1), np.float32)
+        shp2 = np.array([1, a.size], np.int64)
+        lib.lcpu_reduce_f32(O.RED["sum"], red.ctypes.data, a.ctypes.data, 2, shp2.ctypes.data, 1)
+        assert abs(float(red[0, 0]) - float(want_sum[0, 0])) <= 1e-5 * np.abs(a).sum(), path.name
+
+
 # ------------------------------------------------------------ golden vectors
 
 
