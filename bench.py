@@ -503,6 +503,9 @@ def cpu_baseline(seconds, gpu_extra, host):
     seconds per config; each entry states its sample and repetitions."""
     from oracle import lamp_oracle as O
     O.load(fast=True)
+    # numpy computes its float limits once, on first use; doing that here
+    # keeps it from meeting the flush-to-zero mode below
+    np.finfo(np.float32), np.finfo(np.float64)
     with O.denormal_flush():
         return _cpu_baseline(O, seconds, gpu_extra, host)
 

@@ -19,6 +19,7 @@ Two layers:
 from __future__ import annotations
 
 import ctypes as C
+import functools
 import sys
 from pathlib import Path
 
@@ -56,6 +57,7 @@ class fast_build:
 _V4_FLAGS = {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"}
 
 
+@functools.lru_cache(maxsize=None)
 def host_isa() -> str:
     """'x86-64-v4' when /proc/cpuinfo lists every AVX-512 flag x86-64-v4
     needs, else 'x86-64-v3' (AVX2 + FMA, the level every build requires)."""
@@ -69,6 +71,7 @@ def host_isa() -> str:
     return "x86-64-v3"
 
 
+@functools.lru_cache(maxsize=None)
 def fast_library_name() -> str:
     """The fast build load(fast=True) uses on this host: the x86-64-v4 one
     where the CPU has AVX-512 (what the reference's -march=native gives
