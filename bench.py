@@ -262,6 +262,7 @@ def extras(rsl, abi, a_list, b, steps, warmup, only=None):
     if want("c3") or want("c3thin"):
         # --- config 3: fp32 GEMMs through the C ABI (the same kernels Linear uses)
         gemm = {}
+        zero_fns = []
         shapes = ((32, 4096, 8192),) if not want("c3") else \
             ((4096, 4096, 4096), (8192, 8192, 8192), (32, 4096, 8192))
         for (m, n, k) in shapes:
@@ -303,6 +304,7 @@ def extras(rsl, abi, a_list, b, steps, warmup, only=None):
                         "algorithmic_bytes": int(algo), "TB/s": round(algo / ms / 1e9, 3),
                         "frac_of_hbm_peak": round(algo / ms / 1e6 / HBM_PEAK_GBS, 3),
                         "warm_loop_us": round(warm * 1e3, 2)}
+                    zero_fns.append((key, ta, tb, mm, nn, kk, lda, ldb))
                 else:
                     r = 3 if m >= 8192 else 10
                     # about 25 ms of warm-up so the clocks have settled
@@ -311,12 +313,40 @@ def extras(rsl, abi, a_list, b, steps, warmup, only=None):
                         "us": round(ms * 1e3, 1), "TFLOP/s": round(flop / ms / 1e9, 1),
                         "frac_of_fp32_peak": round(flop / ms / 1e9 / FP32_MFMA_PEAK_TFLOPS, 3)}
             del X, Ws, dY, Y, dX, dWs
+            if zero_fns:
+                # The same calls on all-zero operands: the same kernels, bytes
+                # and instructions; only the values the MFMAs see differ.  The
+                # gap is what the part's power limit costs these kernels
+                # (random operands lower the clock while HBM streams).
+                Z = [abi.DeviceBuffer((k, n)) for _ in range(copies)]
+                Zx, Zy = abi.DeviceBuffer((m, k)), abi.DeviceBuffer((m, n))
+                for buf in (*Z, Zx, Zy):
+                    abi.check(L.lmp_k_fill(abi.FLOAT32, buf.ptr, buf.nbytes // 4, 0.0))
+                out_y, out_x = abi.DeviceBuffer((m, n)), abi.DeviceBuffer((m, k))
+                outs = [abi.DeviceBuffer((k, n)) for _ in range(copies)]
+                for key, ta, tb, mm, nn, kk, lda, ldb in zero_fns:
+                    def make_zero(i, ta=ta, tb=tb, mm=mm, nn=nn, kk=kk, lda=lda, ldb=ldb, key=key):
+                        if key.endswith("_fwd"):
+                            a_, b_, c_ = Zx.ptr, Z[i].ptr, out_y.ptr
+                        elif key.endswith("_dX"):
+                            a_, b_, c_ = Zy.ptr, Z[i].ptr, out_x.ptr
+                        else:
+                            a_, b_, c_ = Zx.ptr, Zy.ptr, outs[i].ptr
+                        return lambda: abi.check(L.lmp_k_gemm_f32(ta, tb, mm, nn, kk, a_, lda, b_,
+                                                                  ldb, c_, nn, 0))
+                    r = 200
+                    zms = time_rotating(abi, [make_zero(i) for i in range(copies)], r, 40) / r
+                    gemm[key]["zero_operands_us"] = round(zms * 1e3, 2)
+                del Z, Zx, Zy, out_y, out_x, outs
+                zero_fns.clear()
         out["c3_gemm"] = gemm
         if any(s[0] <= 32 for s in shapes):
             out["c3_gemm"]["note"] = (
                 "skinny GEMMs: algorithmic bytes = 4*(M*K + K*N + M*N) per call; timed over 200 "
                 "calls back to back rotating over four copies of the 128 MiB weight (weight "
-                "gradient), so each call moves it through HBM; warm_loop_us repeats one copy")
+                "gradient), so each call moves it through HBM; warm_loop_us repeats one copy; "
+                "zero_operands_us runs the same calls on all-zero operands (same kernels and "
+                "bytes: the difference is the clock the power limit leaves random operands)")
 
     if want("f64"):
         # float64 GEMM (the reference's float64 suites run matmul on the device)
