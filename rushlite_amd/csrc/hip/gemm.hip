@@ -1287,6 +1287,157 @@ __global__ __launch_bounds__(64 * kRowsWaves, 1) void gemm_thin_rows(RowsArgs g)
   }
 }
 
+// ------------------------------------------------------------ short K
+//
+// C[m, n] (+)= sum_k A[k, m] * B[k, n] with K <= 32 (A stored [k, m]): the
+// weight gradient X^T dY of a Linear at a small batch, a 128 MiB C for a few
+// GFLOP.  The 128 x 128 LDS-tile kernel runs each tile as load -> MFMA ->
+// store with a workgroup per tile, and measured no faster with more
+// workgroups per CU.  Here 2 x CU workgroups stay resident and walk the tiles
+// (n fastest, so the workgroups in flight write whole rows of C): each prefetches its
+// next tile's panels into the other of two LDS stages before running the
+// current tile's MFMAs and stores, so one tile's loads are in flight while
+// the previous tile's C leaves.  Panels, swizzle, MFMA step order and the
+// column sums (first tile row only, k rows in order within two halves, then
+// the halves in order) are those of gemm_f32_lds<LdsSmall> with A transposed,
+// so both kernels give identical bits.  The C tile leaves through a
+// wave-private 32 x 36 LDS tile inside the stage just consumed.
+constexpr int kShortBM = 128, kShortBN = 128;
+
+__global__ __launch_bounds__(256, 2) void gemm_tn_short(GemmArgs g) {
+  constexpr int BM = kShortBM, BN = kShortBN, NW = 4, TM = 2, TN = 2;
+  constexpr int A_PANEL = BM * kBK, STAGE = (BM + BN) * kBK;  // floats
+  constexpr int A_DMA = BM * 8 / 64 / NW, B_DMA = BN * 8 / 64 / NW;
+  constexpr int CS_ROWS = kBK / 2;  // two halves of the k rows per column
+  __shared__ __attribute__((aligned(1024))) float smem[2 * STAGE];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int wm = wave / 2, wn = wave % 2;
+  const int li = lane & 31, lh = lane >> 5;
+  const int ntiles = g.tiles_m * g.tiles_n;
+  uint64_t zero_bits = reinterpret_cast<uint64_t>(g_direct_zeros);
+  asm volatile("" : "+s"(zero_bits));
+  const float* zero = reinterpret_cast<const float*>(zero_bits);
+
+  // DMA roles (N-major panels: k row kr, 16-byte chunk c ^ 8 (kr / 16)).
+  int a_kr[A_DMA], a_c[A_DMA], b_kr[B_DMA], b_c[B_DMA];
+#pragma unroll
+  for (int q = 0; q < A_DMA; ++q) {
+    const int p = (wave * A_DMA + q) * 64 + lane;
+    a_kr[q] = p / (BM / 4);
+    a_c[q] = 4 * ((p % (BM / 4)) ^ ((a_kr[q] >> 4) << 3));
+  }
+#pragma unroll
+  for (int q = 0; q < B_DMA; ++q) {
+    const int p = (wave * B_DMA + q) * 64 + lane;
+    b_kr[q] = p / (BN / 4);
+    b_c[q] = 4 * ((p % (BN / 4)) ^ ((b_kr[q] >> 4) << 3));
+  }
+  auto issue = [&](int t, int stage) {
+    const int m0 = (t / g.tiles_n) * BM, n0 = (t % g.tiles_n) * BN;
+    float* sa = smem + stage * STAGE;
+    float* sb = sa + A_PANEL;
+#pragma unroll
+    for (int q = 0; q < A_DMA; ++q) {
+      const bool ok = m0 + a_c[q] < g.m && a_kr[q] < g.k;
+      lds_dma16(ok ? g.a + int64_t(a_kr[q]) * g.lda + m0 + a_c[q] : zero,
+                sa + (wave * A_DMA + q) * 256);
+    }
+#pragma unroll
+    for (int q = 0; q < B_DMA; ++q) {
+      const bool ok = n0 + b_c[q] < g.n && b_kr[q] < g.k;
+      lds_dma16(ok ? g.b + int64_t(b_kr[q]) * g.ldb + n0 + b_c[q] : zero,
+                sb + (wave * B_DMA + q) * 256);
+    }
+  };
+
+  int t = int(blockIdx.x);
+  if (t < ntiles) issue(t, 0);
+  for (int it = 0; t < ntiles; ++it, t += int(gridDim.x)) {
+    const int stage = it & 1;
+    const int m0 = (t / g.tiles_n) * BM, n0 = (t % g.tiles_n) * BN;
+    // This tile's panels have landed (and the previous tile's stores have
+    // been accepted); every wave is past the previous tile's epilogue, which
+    // used the other stage, so it may be refilled.
+    wait_vmcnt<0>();
+    asm volatile("s_barrier" ::: "memory");
+    if (t + int(gridDim.x) < ntiles) issue(t + int(gridDim.x), stage ^ 1);
+
+    const float* sa = smem + stage * STAGE;
+    const float* sb = sa + A_PANEL;
+    v16f acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = v16f(0.0f);
+    // MFMA step s pairs k = s (lanes 0-31) with k = s + 16 (lanes 32-63).
+#pragma unroll
+    for (int s = 0; s < kBK / 2; ++s) {
+      const int kr = lh * (kBK / 2) + s;
+      float fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = sa[kr * BM + (((wm * TM + i) * 32 + li) ^ (lh << 5))];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = sb[kr * BN + (((wn * TN + j) * 32 + li) ^ (lh << 5))];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    // Column sums of B beside the first tile row: thread t owns column t % BN
+    // and k rows (t / BN) * 16 .. + 15.
+    const bool do_cs = g.colsum != nullptr && m0 == 0;
+    float cs = 0.0f;
+    if (do_cs) {
+      const int col = int(threadIdx.x) % BN, part = int(threadIdx.x) / BN;
+#pragma unroll
+      for (int r = 0; r < CS_ROWS; ++r) {
+        const int kr = part * CS_ROWS + r;
+        cs += sb[kr * BN + (col ^ ((kr >> 4) << 5))];
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");  // every wave is done reading this stage
+
+    float* region = smem + stage * STAGE;
+    if (do_cs) {
+      region[NW * 32 * 36 + threadIdx.x] = cs;
+      __syncthreads();
+      if (int(threadIdx.x) < BN) {
+        const float v = region[NW * 32 * 36 + threadIdx.x] + region[NW * 32 * 36 + BN + threadIdx.x];
+        const int col = n0 + int(threadIdx.x);
+        if (col < g.n) g.colsum[col] = g.colsum_acc ? g.colsum[col] + v : v;
+      }
+    }
+    float* tile = region + wave * (32 * 36);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          tile[((r / 4) * 8 + lh * 4 + (r % 4)) * 36 + li] = acc[i][j][r];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int row0 = m0 + (wm * TM + i) * 32, col0 = n0 + (wn * TN + j) * 32;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int idx = lane + 64 * q;
+          const int rr = idx >> 3, cc = (idx & 7) * 4;
+          const v4f v = *reinterpret_cast<const v4f*>(tile + rr * 36 + cc);
+          const int row = row0 + rr, col = col0 + cc;
+          if (row < g.m && col < g.n) {
+            v4f* p = reinterpret_cast<v4f*>(g.c + int64_t(row) * g.ldc + col);
+            if (g.accumulate) *p = *p + v;
+            else *p = v;
+          }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      }
+    }
+  }
+}
+
 // Default split of K: none once there is a tile for every CU; otherwise
 // enough splits to give each CU two workgroups, keeping at least four K tiles
 // per split.
@@ -1417,6 +1568,19 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, const Workspace& ws, int spli
   return LMP_OK;
 }
 
+// K <= 32 with A transposed on the persistent short-K kernel: two resident
+// workgroups per CU walk the 128 x 128 tiles.
+int launch_short(Runtime* rt, GemmArgs g, bool* colsum_done) {
+  g.tiles_m = (g.m + kShortBM - 1) / kShortBM;
+  g.tiles_n = (g.n + kShortBN - 1) / kShortBN;
+  const int64_t tiles = int64_t(g.tiles_m) * g.tiles_n;
+  if (g.colsum && colsum_done) *colsum_done = true;
+  const uint32_t grid = uint32_t(std::min<int64_t>(tiles, 2 * int64_t(rt->cu_count)));
+  hipLaunchKernelGGL(gemm_tn_short, dim3(grid), dim3(256), 0, rt->stream, g);
+  LMP_LAUNCH_CHECK("gemm_tn_short");
+  return LMP_OK;
+}
+
 // M <= 32 with B transposed on the whole-rows kernel: one workgroup per 32
 // columns, no split of K.
 int launch_rows(Runtime* rt, const GemmArgs& g0) {
@@ -1452,6 +1616,15 @@ int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok, const 
   if (tiny_ok(g)) {
     if (g.colsum && colsum_done) *colsum_done = true;
     return launch_tiny<TA, TB>(rt, g);
+  }
+  // K <= 32 with A transposed (a Linear's weight gradient at a small batch):
+  // the persistent short-K kernel, whose tiles and orders are those of the
+  // 128 x 128 LDS tiles it replaces here.
+  if constexpr (TA && !TB) {
+    const int64_t short_tiles = int64_t((g.m + kShortBM - 1) / kShortBM) *
+                                ((g.n + kShortBN - 1) / kShortBN);
+    if (vec && g.vec_out && g.k <= kBK && !g.bias && short_tiles <= 0x7fffffff)
+      return launch_short(rt, g, colsum_done);
   }
   // M <= 32 with B transposed and a 32-column block for every CU: whole rows
   // of B per workgroup, no split (config 3's dX: 46 -> 31-35 us cold).

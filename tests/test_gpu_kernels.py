@@ -411,10 +411,13 @@ def test_errors_are_reported(hip):
 # so it runs the GEMM and then the dim-0 reduction; config 4's weight
 # gradients (4096, 4096, 512) and (4096, 1000, 512) and the ragged
 # (4100, 1000, 500) run on LDS tiles without a split, where the first tile row
-# also sums B (when B is not transposed).
+# also sums B (when B is not transposed).  With A transposed and K <= 32,
+# (8192, 4096, 32) (config 3's weight gradient) and the ragged (1000, 996, 17)
+# run on the persistent short-K kernel, which sums B the same way.
 @pytest.mark.parametrize("m,n,k", [(256, 64, 32), (64, 10, 32), (40, 33, 7), (512, 300, 12),
                                    (300, 500, 600), (4096, 4096, 512), (4096, 1000, 512),
-                                   (4100, 1000, 500)], ids=str)
+                                   (4100, 1000, 500), (8192, 4096, 32), (1000, 996, 17)],
+                         ids=str)
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_gemm_colsum(hip, m, n, k, ta, tb):
     rng = np.random.default_rng(m * 5 + n + k + ta + 2 * tb)
@@ -442,9 +445,13 @@ def test_gemm_colsum(hip, m, n, k, ta, tb):
 
 
 # Short-K products with a large C (write-bound, like config 3's skinny weight
-# gradient): ragged M and N, odd K, K = 1.
+# gradient): ragged M and N, odd K, K = 1.  With A transposed, K <= 32 and
+# 16-byte rows, (2048, 2048, 32), (3000, 1500, 1), (8192, 4096, 32) and
+# (1000, 996, 17) run on the persistent short-K kernel (more tiles than
+# resident workgroups, ragged edge tiles).
 @pytest.mark.parametrize("m,n,k", [(4100, 1030, 31), (2048, 2048, 32), (3000, 1500, 1),
-                                   (4100, 1030, 33)], ids=str)
+                                   (4100, 1030, 33), (8192, 4096, 32), (1000, 996, 17)],
+                         ids=str)
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_gemm_short_k_large_c(hip, m, n, k, ta, tb):
     rng = np.random.default_rng(m + n + k + 10 * ta + 20 * tb)
