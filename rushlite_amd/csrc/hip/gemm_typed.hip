@@ -10,7 +10,8 @@
 // signed overflow occurs; for bool every product is a && b and the sum is an
 // OR.  Operands arrive already cast to the output type.
 //
-// float64 tiling.  A workgroup of 4 waves owns a 64 x 64 tile of C; each wave
+// float64 tiling.  A workgroup of 4 waves owns a 64 x 64 tile of C (128 x 128
+// once those tiles cover the CUs, gemm_f64_big); each wave
 // owns 2 x 2 blocks of 16 x 16 accumulated by v_mfma_f64_16x16x4f64 (lane l
 // supplies A[l % 16][l / 16] and B[l / 16][l % 16]; accumulator register r
 // holds row 4r + l / 16, column l % 16).  K advances 16 at a time through two
@@ -160,6 +161,115 @@ __global__ __launch_bounds__(kThreads) void gemm_f64_mfma(TypedArgs g) {
     }
 }
 
+// float64, large products: 128 x 128 tiles of 4 waves, each wave 64 x 64 =
+// 4 x 4 blocks of 16 x 16.  Per K step of 16 a workgroup moves 32 KiB from
+// L2 into LDS for 64 MFMAs per wave, a quarter of the 64 x 64 kernel's
+// traffic per flop, which leaves that kernel waiting on the L2 (61% MFMA busy
+// at 4096^3).  Staging, K step, MFMA sequence and accumulator layout are the
+// 64 x 64 kernel's, so both give the same bits; chosen once its tiles cover
+// the CUs.  LDS rows are 129 doubles: an odd pitch puts the 16 k rows that
+// consecutive threads write (A not transposed, B transposed) on distinct banks
+// (a pitch of 132 gave 4-way conflicts, a third of LDS-active cycles).
+constexpr int kBig = 128, kBigPitch = kBig + 1;
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(kThreads, 2) void gemm_f64_big(TypedArgs g) {
+  __shared__ double As[2][kBK * kBigPitch], Bs[2][kBK * kBigPitch];  // [k][m], [k][n]
+  const int tiles_n = (g.n + kBig - 1) / kBig;
+  const int m0 = int(blockIdx.x / tiles_n) * kBig, n0 = int(blockIdx.x % tiles_n) * kBig;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 15, lk = lane >> 4;
+  const double* A = static_cast<const double*>(g.a);
+  const double* B = static_cast<const double*>(g.b);
+  constexpr int PER = kBig * kBK / kThreads;  // 8 elements of each operand per thread
+
+  // Thread tid loads elements f = tid + 256 q; consecutive threads read
+  // consecutive addresses of the stored matrix.  (r, c): A as (m, k) or
+  // (k, m), B as (k, n) or (n, k), whichever is contiguous in memory.
+  double av[PER], bv[PER];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int f = tid + kThreads * q;
+      if constexpr (!TA) {
+        const int r = f / kBK, c = f % kBK;  // A[m0 + r][k0 + c]
+        av[q] = (m0 + r < g.m && k0 + c < g.k) ? A[int64_t(m0 + r) * g.lda + k0 + c] : 0.0;
+      } else {
+        const int r = f / kBig, c = f % kBig;  // A stored [k][m]: A[k0 + r][m0 + c]
+        av[q] = (k0 + r < g.k && m0 + c < g.m) ? A[int64_t(k0 + r) * g.lda + m0 + c] : 0.0;
+      }
+      if constexpr (!TB) {
+        const int r = f / kBig, c = f % kBig;  // B[k0 + r][n0 + c]
+        bv[q] = (k0 + r < g.k && n0 + c < g.n) ? B[int64_t(k0 + r) * g.ldb + n0 + c] : 0.0;
+      } else {
+        const int r = f / kBK, c = f % kBK;  // B stored [n][k]: B[n0 + r][k0 + c]
+        bv[q] = (n0 + r < g.n && k0 + c < g.k) ? B[int64_t(n0 + r) * g.ldb + k0 + c] : 0.0;
+      }
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int f = tid + kThreads * q;
+      if constexpr (!TA) As[buf][(f % kBK) * kBigPitch + f / kBK] = av[q];
+      else As[buf][(f / kBig) * kBigPitch + f % kBig] = av[q];
+      if constexpr (!TB) Bs[buf][(f / kBig) * kBigPitch + f % kBig] = bv[q];
+      else Bs[buf][(f % kBK) * kBigPitch + f / kBK] = bv[q];
+    }
+  };
+
+  v4d acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4d{0.0, 0.0, 0.0, 0.0};
+
+  const int k_tiles = (g.k + kBK - 1) / kBK;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < k_tiles;
+    if (more) load((kt + 1) * kBK);
+    const double* as = As[cur];
+    const double* bs = Bs[cur];
+#pragma unroll
+    for (int s = 0; s < kBK / 4; ++s) {
+      const int kk = 4 * s + lk;
+      double af[4], bf[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = as[kk * kBigPitch + wm * 64 + i * 16 + li];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[j] = bs[kk * kBigPitch + wn * 64 + j * 16 + li];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) store(cur ^ 1);
+    __syncthreads();
+  }
+
+  double* C = static_cast<double*>(g.c);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = n0 + wn * 64 + j * 16 + li;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 64 + i * 16 + 4 * r + lk;
+        if (row < g.m && col < g.n) {
+          double* p = C + int64_t(row) * g.ldc + col;
+          *p = g.accumulate ? *p + acc[i][j][r] : acc[i][j][r];
+        }
+      }
+    }
+}
+
 // ------------------------------------------------------------ bool / ints
 
 // Accumulator of each output type: wrap-around unsigned arithmetic of the
@@ -231,12 +341,18 @@ __global__ __launch_bounds__(kThreads) void gemm_int(TypedArgs g) {
 template <typename T, bool TA, bool TB>
 void launch_typed(Runtime* rt, const TypedArgs& g) {
   const int64_t tiles = int64_t((g.m + kTile - 1) / kTile) * ((g.n + kTile - 1) / kTile);
-  if constexpr (std::is_same_v<T, double>)
-    hipLaunchKernelGGL((gemm_f64_mfma<TA, TB>), dim3(uint32_t(tiles)), dim3(kThreads), 0,
-                       rt->stream, g);
-  else
+  const int64_t big_tiles = int64_t((g.m + kBig - 1) / kBig) * ((g.n + kBig - 1) / kBig);
+  if constexpr (std::is_same_v<T, double>) {
+    if (big_tiles >= rt->cu_count)
+      hipLaunchKernelGGL((gemm_f64_big<TA, TB>), dim3(uint32_t(big_tiles)), dim3(kThreads), 0,
+                         rt->stream, g);
+    else
+      hipLaunchKernelGGL((gemm_f64_mfma<TA, TB>), dim3(uint32_t(tiles)), dim3(kThreads), 0,
+                         rt->stream, g);
+  } else {
     hipLaunchKernelGGL((gemm_int<T, TA, TB>), dim3(uint32_t(tiles)), dim3(kThreads), 0,
                        rt->stream, g);
+  }
 }
 
 template <typename T>

@@ -180,6 +180,30 @@ def test_gemm_float64_random_and_large(hip):
         assert rel_err(got, want) <= 1e-12, (ta, tb)
 
 
+# float64 products whose 128 x 128 tiles cover the CUs run on the large-tile
+# kernel: ragged edges, short and odd K, every orientation, accumulate;
+# integer-valued operands exact, random ones within 1e-12 of numpy.
+@pytest.mark.parametrize("m,n,k", [(2048, 2048, 256), (2100, 2060, 37), (4100, 1030, 130)],
+                         ids=str)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_float64_large_tiles(hip, m, n, k, ta, tb):
+    rng = np.random.default_rng(m + 3 * n + 7 * k + 11 * ta + 13 * tb)
+    a = np.round(rng.standard_normal((m, k)) * 100)
+    b = np.round(rng.standard_normal((k, n)) * 100)
+    da = up(hip, a.T.copy() if ta else a)
+    db = up(hip, b.T.copy() if tb else b)
+    got = hip.gemm(da, db, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert np.array_equal(got, a @ b)  # integer products and sums below 2^53: exact
+    c0 = np.round(rng.standard_normal((m, n)) * 100)
+    dc = up(hip, c0)
+    hip.gemm(da, db, trans_a=bool(ta), trans_b=bool(tb), out=dc, accumulate=True)
+    assert np.array_equal(dc.numpy(), c0 + a @ b)
+    ar, br = rng.standard_normal((m, k)), rng.standard_normal((k, n))
+    got = hip.gemm(up(hip, ar.T.copy() if ta else ar), up(hip, br.T.copy() if tb else br),
+                   trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert rel_err(got, ar @ br) <= 1e-12
+
+
 # ------------------------------------------------- framework level
 
 @pytest.fixture(scope="module")
