@@ -513,6 +513,16 @@ void emit_params(std::ostringstream& os, const Region& r, const std::string& nam
   os << ") {\n";
 }
 
+// Leaves at least this large are read with the nontemporal hint: a tensor
+// as large as the 256 MB memory-side cache cannot stay in it between uses,
+// and reads that do not allocate there leave it to other data (a cold
+// 256 MiB read + write: 84.4 -> 81.5 us on MI355X).  Below that size a leaf
+// may still be in the cache from the kernel that wrote it (a warm 256 MiB
+// re-read: 64.7 us with ordinary loads, 78.5 us nontemporal), so it keeps
+// ordinary loads.  Leaf shapes are part of the structural key, so the choice
+// is fixed by it.
+constexpr size_t kStreamBytes = size_t(256) << 20;
+
 // The body of a float4 (vec) region: block `block` owns output float4s
 // [256 * block, 256 * block + 256) (one-shot).
 void emit_vec_body(std::ostringstream& os, const Region& r, const Plan& p, const Names& nm,
@@ -530,7 +540,11 @@ void emit_vec_body(std::ostringstream& os, const Region& r, const Plan& p, const
   for (size_t l = 0; l < nl; ++l) {
     const bool contig = !p.groups.empty() && p.groups[0].stride[l] == 1;
     const int64_t rs = rows ? p.groups[1].stride[l] : 0;
-    if (contig)
+    const bool stream = r.leaves[l]->nbytes() >= kStreamBytes;
+    if (contig && stream)
+      os << "  const lmp_v4 s" << l << " = __builtin_nontemporal_load(reinterpret_cast<const lmp_v4*>("
+         << nm.in << l << " + (unsigned long)r * " << rs << "ul + c));\n";
+    else if (contig)
       os << "  const lmp_v4 s" << l << " = *reinterpret_cast<const lmp_v4*>(" << nm.in << l
          << " + (unsigned long)r * " << rs << "ul + c);\n";
     else

@@ -81,13 +81,20 @@ bool aligned16(const void* p) {
 
 // ------------------------------------------------------------ fp32 2-D path
 
+// A float4 of a full operand: nontemporal when the operand is kStreamBytes or
+// more (`nt`, uniform across the launch).
+__device__ __forceinline__ v4f load_full4(const float* p, int nt) {
+  return nt ? __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p))
+            : *reinterpret_cast<const v4f*>(p);
+}
+
 // out[r, c] = op(a[r*a_row + c*a_in], b[r*b_row + c*b_in]) with a_in, b_in
 // in {0, 1} fixed at compile time; lane v produces float4 v of the output.
 template <int OP, bool A_IN, bool B_IN, bool ROWS>
 __global__ __launch_bounds__(kBlock) void bin2d_f32(
     float* __restrict__ out, const float* __restrict__ a,
     const float* __restrict__ b, uint32_t nvec, FastDiv cols4, int64_t a_row,
-    int64_t b_row, float lo, float hi) {
+    int64_t b_row, float lo, float hi, int nt) {
   const uint32_t v = blockIdx.x * kBlock + threadIdx.x;
   if (v >= nvec) return;
   const uint32_t r = ROWS ? cols4.div(v) : 0;
@@ -95,9 +102,9 @@ __global__ __launch_bounds__(kBlock) void bin2d_f32(
   const float* pa = a + int64_t(r) * a_row + (A_IN ? int64_t(c4) * 4 : 0);
   const float* pb = b + int64_t(r) * b_row + (B_IN ? int64_t(c4) * 4 : 0);
   v4f xa, xb;
-  if constexpr (A_IN) xa = *reinterpret_cast<const v4f*>(pa);
+  if constexpr (A_IN) xa = load_full4(pa, nt);
   else xa = v4f(*pa);
-  if constexpr (B_IN) xb = *reinterpret_cast<const v4f*>(pb);
+  if constexpr (B_IN) xb = load_full4(pb, nt);
   else xb = v4f(*pb);
   v4f o;
   o.x = binary_apply<OP, float>(xa.x, xb.x, lo, hi);
@@ -192,9 +199,10 @@ int launch_bin_f32(float* out, const float* a, const float* b,
       const FastDiv cols4(uint32_t(cols / 4));
       const int grid = grid_for(nvec, kBlock);
       const bool rws = rows > 1;
+      const int nt = uint64_t(rows) * uint64_t(cols) * sizeof(float) >= kStreamBytes ? 1 : 0;
 #define LMP_BIN2D(AI, BI, RW)                                                  \
   hipLaunchKernelGGL((bin2d_f32<OP, AI, BI, RW>), dim3(grid), dim3(kBlock), 0, \
-                     rt->stream, out, a, b, nvec, cols4, a_row, b_row, lo, hi)
+                     rt->stream, out, a, b, nvec, cols4, a_row, b_row, lo, hi, nt)
       if (a_in == 1 && b_in == 1) {
         if (rws) LMP_BIN2D(true, true, true); else LMP_BIN2D(true, true, false);
       } else if (a_in == 1) {
@@ -246,10 +254,10 @@ int dispatch_bin(int op, T* out, const T* a, const T* b, const Coalesced& c,
 template <int OP>
 __global__ __launch_bounds__(kBlock) void unary_f32_vec(
     float* __restrict__ out, const float* __restrict__ in, uint32_t nvec,
-    float lo, float hi) {
+    float lo, float hi, int nt) {
   const uint32_t v = blockIdx.x * kBlock + threadIdx.x;
   if (v >= nvec) return;
-  const v4f x = reinterpret_cast<const v4f*>(in)[v];
+  const v4f x = load_full4(in + uint64_t(v) * 4, nt);
   v4f o;
   o.x = unary_apply<OP, float>(x.x, lo, hi);
   o.y = unary_apply<OP, float>(x.y, lo, hi);
@@ -278,7 +286,7 @@ int launch_unary(T* out, const T* in, size_t n, double p0, double p1) {
       const int grid = grid_for(nvec, kBlock);
       hipLaunchKernelGGL((unary_f32_vec<OP>), dim3(grid), dim3(kBlock), 0,
                          rt->stream, out, in, nvec, static_cast<float>(p0),
-                         static_cast<float>(p1));
+                         static_cast<float>(p1), n * sizeof(float) >= kStreamBytes ? 1 : 0);
       LMP_LAUNCH_CHECK("unary_f32_vec");
       return LMP_OK;
     }
@@ -350,11 +358,11 @@ __global__ __launch_bounds__(kBlock) void add_inplace_scalar(
 }
 
 __global__ __launch_bounds__(kBlock) void add_inplace_f32_vec(
-    float* __restrict__ dst, const float* __restrict__ src, uint32_t nvec) {
+    float* __restrict__ dst, const float* __restrict__ src, uint32_t nvec, int nt) {
   const uint32_t v = blockIdx.x * kBlock + threadIdx.x;
   if (v >= nvec) return;
   v4f* d = reinterpret_cast<v4f*>(dst) + v;
-  *d = *d + reinterpret_cast<const v4f*>(src)[v];
+  *d = *d + load_full4(src + uint64_t(v) * 4, nt);
 }
 
 template <typename F>
@@ -467,7 +475,8 @@ int lmp_k_add_inplace(int dtype, void* dst, const void* src, size_t n) {
         hipLaunchKernelGGL(add_inplace_f32_vec,
                            dim3(grid_for(nvec, kBlock)), dim3(kBlock),
                            0, rt->stream, static_cast<float*>(dst),
-                           static_cast<const float*>(src), nvec);
+                           static_cast<const float*>(src), nvec,
+                           n * sizeof(float) >= kStreamBytes ? 1 : 0);
         LMP_LAUNCH_CHECK("add_inplace_f32_vec");
         return LMP_OK;
       }

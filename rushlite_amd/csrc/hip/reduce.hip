@@ -69,9 +69,16 @@ __device__ __forceinline__ v4f combine4(v4f a, v4f b) {
   return r;
 }
 
+// Inputs of kStreamBytes or more are read with the nontemporal hint.
+template <bool NT>
+__device__ __forceinline__ v4f load4(const v4f* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
 // Block (row, part) reduces float4 [part*seg4, min(len4, (part+1)*seg4)) of
 // its row and writes one value to out[row * parts + part].
-template <int OP>
+template <int OP, bool NT>
 __global__ __launch_bounds__(kBlock) void row_reduce_f32(
     float* __restrict__ out, const float* __restrict__ in, uint32_t len4,
     uint32_t seg4, FastDiv parts) {
@@ -85,14 +92,14 @@ __global__ __launch_bounds__(kBlock) void row_reduce_f32(
   v4f acc0 = id, acc1 = id, acc2 = id, acc3 = id;
   uint32_t i = beg + threadIdx.x;
   for (; i + 3 * kBlock < end; i += 4 * kBlock) {
-    v4f x0 = src[i], x1 = src[i + kBlock], x2 = src[i + 2 * kBlock],
-        x3 = src[i + 3 * kBlock];
+    v4f x0 = load4<NT>(src + i), x1 = load4<NT>(src + i + kBlock),
+        x2 = load4<NT>(src + i + 2 * kBlock), x3 = load4<NT>(src + i + 3 * kBlock);
     acc0 = combine4<OP>(acc0, x0);
     acc1 = combine4<OP>(acc1, x1);
     acc2 = combine4<OP>(acc2, x2);
     acc3 = combine4<OP>(acc3, x3);
   }
-  for (; i < end; i += kBlock) acc0 = combine4<OP>(acc0, src[i]);
+  for (; i < end; i += kBlock) acc0 = combine4<OP>(acc0, load4<NT>(src + i));
   v4f acc = combine4<OP>(combine4<OP>(acc0, acc1), combine4<OP>(acc2, acc3));
   float v = R::combine(R::combine(acc.x, acc.y), R::combine(acc.z, acc.w));
   v = wave_reduce<OP, float>(v);
@@ -182,7 +189,7 @@ __global__ __launch_bounds__(kBlock) void fold_parts(T* __restrict__ out,
 // of chunk s = [s*chunk, min(len, (s+1)*chunk)).  dst layout [outer, S, inner]
 // (S == 1 writes the final result).
 constexpr int kColUnroll = 8;
-template <int OP>
+template <int OP, bool NT>
 __global__ __launch_bounds__(kBlock) void col_reduce_f32(
     float* __restrict__ dst, const float* __restrict__ in, uint32_t inner4,
     uint32_t len, uint32_t chunk) {
@@ -202,11 +209,11 @@ __global__ __launch_bounds__(kBlock) void col_reduce_f32(
     for (; r + 4 * (kColUnroll - 1) < r1; r += 4 * kColUnroll) {
       v4f x[kColUnroll];
 #pragma unroll
-      for (int u = 0; u < kColUnroll; ++u) x[u] = src[uint64_t(r + 4 * u) * inner4];
+      for (int u = 0; u < kColUnroll; ++u) x[u] = load4<NT>(src + uint64_t(r + 4 * u) * inner4);
 #pragma unroll
       for (int u = 0; u < kColUnroll; ++u) acc[u] = combine4<OP>(acc[u], x[u]);
     }
-    for (; r < r1; r += 4) acc[0] = combine4<OP>(acc[0], src[uint64_t(r) * inner4]);
+    for (; r < r1; r += 4) acc[0] = combine4<OP>(acc[0], load4<NT>(src + uint64_t(r) * inner4));
   }
   v4f a = acc[0];
 #pragma unroll
@@ -394,9 +401,14 @@ int reduce_rows(Runtime* rt, T* out, const T* in, uint64_t rows, uint64_t len) {
         if (!tmp) return LMP_ERR_OOM;
         dst = tmp;
       }
-      hipLaunchKernelGGL((row_reduce_f32<OP>), dim3(uint32_t(rows * parts)),
-                         dim3(kBlock), 0, rt->stream, dst, in, uint32_t(len4),
-                         uint32_t(seg4), FastDiv(uint32_t(parts)));
+      if (rows * len4 * 16 >= kStreamBytes)
+        hipLaunchKernelGGL((row_reduce_f32<OP, true>), dim3(uint32_t(rows * parts)),
+                           dim3(kBlock), 0, rt->stream, dst, in, uint32_t(len4),
+                           uint32_t(seg4), FastDiv(uint32_t(parts)));
+      else
+        hipLaunchKernelGGL((row_reduce_f32<OP, false>), dim3(uint32_t(rows * parts)),
+                           dim3(kBlock), 0, rt->stream, dst, in, uint32_t(len4),
+                           uint32_t(seg4), FastDiv(uint32_t(parts)));
       LMP_LAUNCH_CHECK("row_reduce_f32");
       if (parts > 1) {
         hipLaunchKernelGGL((fold_parts<OP, float>), dim3(blocks_for(rows)),
@@ -482,8 +494,12 @@ int reduce_cols(Runtime* rt, T* out, const T* in, uint64_t outer, uint64_t len,
   const dim3 grid{uint32_t(gx), uint32_t(S), uint32_t(outer)};
   if constexpr (std::is_same_v<T, float>) {
     if (vec) {
-      hipLaunchKernelGGL((col_reduce_f32<OP>), grid, dim3(kBlock), 0, rt->stream,
-                         dst, in, uint32_t(inner / 4), uint32_t(len), uint32_t(chunk));
+      if (outer * len * inner * sizeof(float) >= kStreamBytes)
+        hipLaunchKernelGGL((col_reduce_f32<OP, true>), grid, dim3(kBlock), 0, rt->stream,
+                           dst, in, uint32_t(inner / 4), uint32_t(len), uint32_t(chunk));
+      else
+        hipLaunchKernelGGL((col_reduce_f32<OP, false>), grid, dim3(kBlock), 0, rt->stream,
+                           dst, in, uint32_t(inner / 4), uint32_t(len), uint32_t(chunk));
       LMP_LAUNCH_CHECK("col_reduce_f32");
       if (S > 1) {
         const uint64_t n4 = outer * (inner / 4);
