@@ -8,14 +8,15 @@ graph = one fused kernel launch.  `value` is HBM GB/s counted on algorithmic
 bytes (read a and b once, write c once: 536,903,680 B per step) over the
 steps timed back to back between two HIP events on the library stream.
 
-MI355X's 256 MB memory-side cache (MALL) would still hold part of `a` from
-the previous step, so the timed steps rotate over three copies of `a` (three
+MI355X's 256 MB memory-side cache (MALL) could hold part of `a` from the
+previous step, so the timed steps rotate over three copies of `a` (three
 256 MiB buffers with the same values): between two uses of one copy the
-other two stream 512 MiB of reads and 512 MiB of writes through the cache,
-so every step reads its `a` from HBM, and the steps still run back to back
-(no event pair or synchronisation per step).  `evicted_per_step` times each
-step alone after a 1 GiB read (HIP events around every step); `warm_loop`
-repeats one copy, part of which the MALL then serves.
+other two stream 512 MiB of reads and 512 MiB of writes, so every step reads
+its `a` from HBM, and the steps still run back to back (no event pair or
+synchronisation per step).  `evicted_per_step` times each step alone after a
+1 GiB read (HIP events around every step); `warm_loop` repeats one copy.
+(The fused kernel reads operands of 256 MiB or more with nontemporal loads,
+which do not allocate in the MALL, so today all three read HBM.)
 
 `extra` carries the other configs measured in the same process: the 6-op
 chain, the [16384,16384] dim reductions and broadcast-add backwards, the
@@ -704,8 +705,9 @@ def main():
                                      "read has emptied the MALL"},
         "warm_loop": {"ms_per_step": round(warm_ms, 5),
                       "GB/s": round(BYTES_C1 / warm_ms / 1e6, 1),
-                      "note": "one copy of a back to back: part of it is still in the 256 MB "
-                              "MALL from the previous step, so not all bytes come from HBM"},
+                      "note": "one copy of a back to back; a (256 MiB) is read with nontemporal "
+                              "loads, which do not allocate in the 256 MB MALL, so this loop "
+                              "reads HBM as well"},
     }
     if args.copy_probe:
         zero = rsl.Variable(np.zeros(1, np.float32))
