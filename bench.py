@@ -211,6 +211,40 @@ def extras(rsl, abi, a_list, b, steps, warmup, only=None):
         out["c1a_eager_unfused_2_launches"] = {"us": round(ms * 1e3, 2),
                                                "GB/s_algorithmic": round(BYTES_C1 / ms / 1e6, 1)}
 
+        # Host <-> device around the path (the boundary takes device buffers;
+        # `value` never includes these): upload of a and b from pageable
+        # numpy arrays (Variable(ndarray)), download of c (.numpy()), and the
+        # config-1 rate with both included.
+        a_np = np.random.default_rng(0).random((N8K, N8K), dtype=np.float32)
+        b_np = np.random.default_rng(1).random((N8K, 1), dtype=np.float32)
+        ups, downs, ends = [], [], []
+        for _ in range(3):
+            abi.synchronize()
+            t0 = time.perf_counter()
+            av, bv = rsl.Variable(a_np), rsl.Variable(b_np)
+            abi.synchronize()
+            t1 = time.perf_counter()
+            with rsl.capture_on():
+                cv = av * av + bv
+            cv.realize()
+            abi.synchronize()
+            t2 = time.perf_counter()
+            c_np = cv.numpy()
+            t3 = time.perf_counter()
+            ups.append(t1 - t0)
+            downs.append(t3 - t2)
+            ends.append(t3 - t0)
+            del av, bv, cv, c_np
+        up, down, end = min(ups), min(downs), min(ends)
+        out["c1_host_device"] = {
+            "h2d_GB/s": round((a_np.nbytes + b_np.nbytes) / up / 1e9, 2),
+            "d2h_GB/s": round(a_np.nbytes / down / 1e9, 2),
+            "end_to_end_ms": round(end * 1e3, 2),
+            "end_to_end_GB/s_algorithmic": round(BYTES_C1 / end / 1e9, 2),
+            "note": "best of 3: upload a and b from pageable host arrays, fused kernel, download "
+                    "c to a new host array; wall clock with a synchronisation after each part"}
+        del a_np, b_np
+
     if want("c2"):
         # --- config 2: dim reductions and the broadcast-add backward (1 GiB
         # operands, four times the MALL: every pass reads HBM)
