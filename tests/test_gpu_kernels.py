@@ -505,3 +505,50 @@ def test_linear_bias_epilogue_equals_gemm_then_add(hip, m, n, k, ta, tb):
                                               db.shape[1], dbias.ptr, out.ptr, n))
     relu = np.where(want < 0, np.float32(0), want)
     assert np.array_equal(out.numpy().view(np.uint32), relu.view(np.uint32))
+
+
+# Random shapes drawn on both sides of every kernel-selection threshold (M <= 32
+# register-direct and whole-rows, M <= 64 skinny tiles, K <= 32 short-K, the
+# tiny kernel's 2^21 multiply-adds, tiles covering the CUs, K split or not,
+# 16-byte rows or not), every orientation: the product against float64 within
+# 1e-5 of its largest value, accumulate as the fp32 sum of C and the product bit
+# for bit, and bias + ReLU on the same product bit for bit.
+def _random_gemm_shapes(count, seed):
+    rng = np.random.default_rng(seed)
+    shapes = []
+    while len(shapes) < count:
+        m = int(rng.choice([rng.integers(1, 33), rng.integers(33, 65), rng.integers(65, 700),
+                            rng.integers(700, 2100)]))
+        n = int(rng.choice([rng.integers(1, 130), rng.integers(130, 1100), rng.integers(1100, 4200)]))
+        k = int(rng.choice([rng.integers(1, 33), rng.integers(33, 600), rng.integers(600, 4200)]))
+        if rng.random() < 0.5:  # keep 16-byte rows half of the time
+            m, n, k = [max(4, d - d % 4) for d in (m, n, k)]
+        if m * n * k <= (1 << 31) and m * n <= (1 << 23):
+            shapes.append((m, n, k))
+    return shapes
+
+
+@pytest.mark.parametrize("m,n,k", _random_gemm_shapes(24, 2026) + [(20, 8200, 100), (600, 2100, 2100)],
+                         ids=str)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_random_shapes_every_path(hip, m, n, k, ta, tb):
+    rng = np.random.default_rng(m * 131 + n * 17 + k + 3 * ta + tb)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    da = up(hip, a.T.copy() if ta else a)
+    db = up(hip, b.T.copy() if tb else b)
+    got = hip.gemm(da, db, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    assert rel_err(got, want) <= 1e-5
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    dc = up(hip, c0)
+    hip.gemm(da, db, trans_a=bool(ta), trans_b=bool(tb), out=dc, accumulate=True)
+    assert np.array_equal(dc.numpy(), c0 + got)
+    bias = rng.standard_normal(n).astype(np.float32)
+    dbias = up(hip, bias)  # held: a freed buffer could be handed to the split-K partials
+    out = hip.DeviceBuffer((m, n), np.float32)
+    hip.check(hip.lib().lmp_k_linear_relu_f32(ta, tb, m, n, k, da.ptr, da.shape[1], db.ptr,
+                                              db.shape[1], dbias.ptr, out.ptr, n))
+    t = got + bias[None, :]
+    assert np.array_equal(out.numpy().view(np.uint32),
+                          np.where(t < 0, np.float32(0), t).view(np.uint32))
