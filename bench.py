@@ -211,6 +211,19 @@ def extras(rsl, abi, a_list, b, steps, warmup, only=None):
         out["c1a_eager_unfused_2_launches"] = {"us": round(ms * 1e3, 2),
                                                "GB/s_algorithmic": round(BYTES_C1 / ms / 1e6, 1)}
 
+        # The 6-op chain outside capture_on: one eager kernel per op (exp, mul,
+        # clamp, the [8192,1] b + 1, div, sub), every intermediate written to
+        # and read back from HBM
+        def make_chain_eager(a):
+            return lambda: (rsl.exp(a) * b - rsl.clamp(a, 0, dbl_max) / (b + 1)).realize()
+        s0 = rsl._stats()
+        ms = time_rotating(abi, [make_chain_eager(a) for a in a_list], r, 2) / r
+        s1 = rsl._stats()
+        out["c1b_chain6_eager_unfused"] = {
+            "us": round(ms * 1e3, 2),
+            "GB/s_algorithmic": round(BYTES_C1 / ms / 1e6, 1),
+            "launches_per_step": (s1["eager_launches"] - s0["eager_launches"]) / (r + 2)}
+
         # Host <-> device around the path (the boundary takes device buffers;
         # `value` never includes these): upload of a and b from pageable
         # numpy arrays (Variable(ndarray)), download of c (.numpy()), and the
