@@ -257,3 +257,133 @@ def test_random_graph_float32_matches_torch(rsl, seed, capture):
     programs, against torch float64 at the reference stress suites' 1e-4
     (tests/stress/pytorch_stress_test.py:92-110)."""
     check_graph(rsl, seed, capture, np.float32, 1e-4)
+
+
+# ---------------------------------------------------------------- other shapes
+#
+# The same kind of program over [R, C] leaves (with [R, 1], [1, C] and [C]
+# broadcasts), at shapes that take the other code paths: float4 bodies and
+# multi-wave rows (64 x 128, 130 x 64), the indexed path and short rows (33 x 7),
+# and long rows, large reductions and a K = 1000 GEMM (256 x 1000).  Float32
+# only, where the fused kernels differ most from the eager ones.  The checker is
+# the float32 oracle (Lamp3's CPU arithmetic and tie rule); a program whose
+# float32 oracle is itself more than 1e-4 from torch float64 is ill-conditioned
+# in float32 (a max/min tie that one rounding breaks, a cancelling sum), where
+# any two valid summation orders may differ by more than the bar, and is skipped.
+
+RC_SHAPES = [(64, 128), (33, 7), (130, 64), (256, 1000)]
+
+
+def make_program_rc(seed, R, C):
+    """make_program over [R, C]-based leaves; a matmul takes any 2-D value
+    and a right operand whose rows match its columns."""
+    rng = np.random.default_rng(seed)
+    pool_shapes = [(R, C), (R, 1), (1, C), (C,)]
+    leaves = [pool_shapes[i] for i in rng.integers(0, len(pool_shapes), 4)]
+    leaves[0] = (R, C)
+    shapes = list(leaves)
+    steps = []
+    for _ in range(int(rng.integers(10, 18))):
+        kind = rng.choice(["bin", "bin", "bin", "unary", "unary", "reduce", "matmul", "transpose"])
+        recent = list(range(max(0, len(shapes) - 5), len(shapes)))
+        if kind == "bin":
+            i = int(rng.choice(recent))
+            j = int(rng.choice([j for j in range(len(shapes)) if broadcast(shapes[i], shapes[j])]))
+            op = str(rng.choice(["add", "sub", "mul", "div", "pow"]))
+            steps.append(("bin", op, i, j))
+            shapes.append(broadcast(shapes[i], shapes[j]))
+        elif kind == "unary":
+            i = int(rng.choice(recent))
+            op = str(rng.choice(["neg", "exp", "log", "sqrt", "sin", "cos", "tan", "abs", "clamp"]))
+            steps.append(("unary", op, i))
+            shapes.append(shapes[i])
+        elif kind == "reduce":
+            cand = [i for i in recent if len(shapes[i]) == 2]
+            if not cand:
+                continue
+            i = int(rng.choice(cand))
+            axis = int(rng.integers(0, 2))
+            steps.append(("reduce", str(rng.choice(["sum", "max", "min"])), i, axis))
+            s = list(shapes[i])
+            s[axis] = 1
+            shapes.append(tuple(s))
+        elif kind == "matmul":
+            i = int(rng.choice([i for i in range(len(shapes)) if len(shapes[i]) == 2]))
+            rhs = [j for j in range(len(shapes))
+                   if len(shapes[j]) == 2 and shapes[j][0] == shapes[i][1]]
+            if not rhs:
+                continue
+            j = int(rng.choice(rhs))
+            steps.append(("matmul", "matmul", i, j))
+            shapes.append((shapes[i][0], shapes[j][1]))
+        else:
+            cand = [i for i in recent if len(shapes[i]) == 2]
+            if not cand:
+                continue
+            i = int(rng.choice(cand))
+            steps.append(("transpose", "transpose", i))
+            shapes.append((shapes[i][1], shapes[i][0]))
+    return leaves, steps, shapes
+
+
+def oracle_ops(O):
+    class OracleOps:
+        add = staticmethod(O.add)
+        sub = staticmethod(O.sub)
+        mul = staticmethod(O.mul)
+        div = staticmethod(O.div)
+        pow = staticmethod(O.pow_)
+        neg = staticmethod(O.neg)
+        exp = staticmethod(O.exp)
+        log = staticmethod(O.log)
+        sqrt = staticmethod(O.sqrt)
+        sin = staticmethod(O.sin)
+        cos = staticmethod(O.cos)
+        tan = staticmethod(O.tan)
+        abs = staticmethod(O.abs_)
+        clamp = staticmethod(O.clamp)
+        sum = staticmethod(O.sum_)
+        max = staticmethod(O.max_)
+        min = staticmethod(O.min_)
+        matmul = staticmethod(O.matmul_v)
+        transpose = staticmethod(O.transpose_v)
+
+        @staticmethod
+        def const(like, v):
+            return O.OVar(np.array([v], np.float32))
+    return OracleOps
+
+
+def _errors(out, grads, want_out, want_grads, leaves):
+    errs = [rel_err(np.asarray(out).reshape(-1), np.asarray(want_out).reshape(-1))]
+    for i, (g, w) in enumerate(zip(grads, want_grads)):
+        w = np.zeros(leaves[i]) if w is None else np.asarray(w)
+        errs.append(rel_err(np.asarray(g).reshape(w.shape), w))
+    return max(errs)
+
+
+@pytest.mark.parametrize("capture", [False, True], ids=["eager", "captured"])
+@pytest.mark.parametrize("shape", RC_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+@pytest.mark.parametrize("seed", range(6))
+def test_random_graph_float32_shapes_vs_oracle(rsl, oracle, seed, shape, capture):
+    R, C = shape
+    leaves, steps, shapes = make_program_rc(seed, R, C)
+    rng = np.random.default_rng(1000 + seed)
+    arrs = [rng.uniform(-1.0, 1.0, s).astype(np.float32) for s in leaves]
+    ov = [oracle.OVar(a.copy(), requires_grad=True) for a in arrs]
+    o_out = run(oracle_ops(oracle), ov, steps, shapes)
+    o_out.backward()
+    tv = [torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in arrs]
+    t_out = run(TorchOps, tv, steps, shapes)
+    t_out.backward()
+    conditioning = _errors(o_out.data, [o.grad for o in ov], t_out.detach().numpy(),
+                           [None if t.grad is None else t.grad.numpy() for t in tv], leaves)
+    if conditioning > 1e-4:
+        pytest.skip(f"ill-conditioned in float32: oracle vs torch float64 {conditioning:.2g}")
+    lv = [rsl.Variable(a, requires_grad=True) for a in arrs]
+    with rsl.capture_on(capture):
+        l_out = run(lamp_ops(rsl, rsl.dtype.float32), lv, steps, shapes)
+    l_out.backward()
+    err = _errors(l_out.numpy(), [v.grad.numpy() for v in lv], o_out.data,
+                  [o.grad for o in ov], leaves)
+    assert err <= 1e-4, (seed, shape, err, steps)
