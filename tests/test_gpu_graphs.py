@@ -179,39 +179,7 @@ def make_program(seed):
 
 
 def run(ops, leaves, steps, shapes):
-    pool = list(leaves)
-    one = ops.const(pool[0], 1.0)
-    half = ops.const(pool[0], 0.5)
-    for st in steps:
-        kind, op = st[0], st[1]
-        if kind == "bin":
-            a, b = pool[st[2]], pool[st[3]]
-            if op == "div":
-                r = ops.div(a, ops.add(ops.mul(b, b), one))          # denominator >= 1
-            elif op == "pow":
-                r = ops.pow(ops.add(ops.mul(a, a), half), ops.clamp(b, -1.5, 1.5))
-            else:
-                r = getattr(ops, op)(a, b)
-        elif kind == "unary":
-            a = pool[st[2]]
-            if op in ("log", "sqrt"):
-                r = getattr(ops, op)(ops.add(ops.mul(a, a), one))
-            elif op == "exp":
-                r = ops.exp(ops.clamp(a, -3.0, 3.0))
-            elif op == "tan":
-                r = ops.tan(ops.mul(ops.sin(a), half))
-            elif op == "clamp":
-                r = ops.clamp(a, -0.75, 0.75)
-            else:
-                r = getattr(ops, op)(a)
-        elif kind == "reduce":
-            r = getattr(ops, op)(pool[st[2]], st[3])
-        elif kind == "matmul":
-            r = ops.matmul(pool[st[2]], pool[st[3]])
-        else:
-            r = ops.transpose(pool[st[2]])
-        pool.append(r)
-    out = pool[-1]
+    out = _run_steps(ops, leaves, steps)
     if len(shapes[-1]) == 1:
         return ops.sum(out, 0)
     return ops.sum(ops.sum(out, 0), 1)
@@ -387,3 +355,121 @@ def test_random_graph_float32_shapes_vs_oracle(rsl, oracle, seed, shape, capture
     err = _errors(l_out.numpy(), [v.grad.numpy() for v in lv], o_out.data,
                   [o.grad for o in ov], leaves)
     assert err <= 1e-4, (seed, shape, err, steps)
+
+
+# ---------------------------------------------------------------- 3-d programs
+#
+# Elementwise and keep-dims reduction programs over 3-d leaves with every kind
+# of broadcast ([A,B,C] against [A,1,C], [1,B,1], [B,C], [C], [A,B,1],
+# [1,1,C]) and reductions over any axis: the n-d indexed kernels, 3-d fused
+# regions and rows.  Float64 against torch float64 at 1e-9; float32 against the
+# float32 oracle at 1e-4, skipping a program ill-conditioned in float32 as above.
+
+D3_SHAPES = [(4, 33, 64), (3, 5, 7), (2, 130, 256)]
+
+
+def make_program_3d(seed, A, B, C):
+    rng = np.random.default_rng(seed)
+    pool_shapes = [(A, B, C), (A, 1, C), (1, B, 1), (B, C), (C,), (A, B, 1), (1, 1, C)]
+    leaves = [pool_shapes[i] for i in rng.integers(0, len(pool_shapes), 4)]
+    leaves[0] = (A, B, C)
+    shapes = list(leaves)
+    steps = []
+    for _ in range(int(rng.integers(8, 16))):
+        kind = rng.choice(["bin", "bin", "bin", "unary", "unary", "reduce"])
+        recent = list(range(max(0, len(shapes) - 5), len(shapes)))
+        i = int(rng.choice(recent))
+        if kind == "bin":
+            j = int(rng.choice([j for j in range(len(shapes)) if broadcast(shapes[i], shapes[j])]))
+            steps.append(("bin", str(rng.choice(["add", "sub", "mul", "div", "pow"])), i, j))
+            shapes.append(broadcast(shapes[i], shapes[j]))
+        elif kind == "unary":
+            op = str(rng.choice(["neg", "exp", "log", "sqrt", "sin", "cos", "tan", "abs", "clamp"]))
+            steps.append(("unary", op, i))
+            shapes.append(shapes[i])
+        else:
+            axis = int(rng.integers(0, len(shapes[i])))
+            steps.append(("reduce", str(rng.choice(["sum", "max", "min"])), i, axis))
+            s = list(shapes[i])
+            s[axis] = 1
+            shapes.append(tuple(s))
+    return leaves, steps, shapes
+
+
+@pytest.mark.parametrize("capture", [False, True], ids=["eager", "captured"])
+@pytest.mark.parametrize("shape", D3_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("seed", range(4))
+def test_random_graph_3d(rsl, oracle, seed, shape, capture):
+    leaves, steps, shapes = make_program_3d(seed, *shape)
+    rng = np.random.default_rng(1000 + seed)
+    arrs = [rng.uniform(-1.0, 1.0, s) for s in leaves]
+    for dtype in (np.float64, np.float32):
+        a = [x.astype(dtype) for x in arrs]
+        tv = [torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in a]
+        t_out = _sum_all(TorchOps, _run_steps(TorchOps, tv, steps), shapes)
+        t_out.backward()
+        t_grads = [None if t.grad is None else t.grad.numpy() for t in tv]
+        if dtype == np.float64:
+            want, want_grads, tol = t_out.detach().numpy(), t_grads, 1e-9
+            kind = rsl.dtype.float64
+        else:
+            ov = [oracle.OVar(x.copy(), requires_grad=True) for x in a]
+            o_ops = oracle_ops(oracle)
+            o_out = _sum_all(o_ops, _run_steps(o_ops, ov, steps), shapes)
+            o_out.backward()
+            want, want_grads, tol = o_out.data, [o.grad for o in ov], 1e-4
+            if _errors(want, want_grads, t_out.detach().numpy(), t_grads, leaves) > 1e-4:
+                continue  # ill-conditioned in float32
+            kind = rsl.dtype.float32
+        lv = [rsl.Variable(x, requires_grad=True, dtype=kind) for x in a]
+        l_ops = lamp_ops(rsl, kind)
+        with rsl.capture_on(capture):
+            l_out = _sum_all(l_ops, _run_steps(l_ops, lv, steps), shapes)
+        l_out.backward()
+        err = _errors(l_out.numpy(), [v.grad.numpy() for v in lv], want, want_grads, leaves)
+        assert err <= tol, (seed, shape, np.dtype(dtype).name, err, steps)
+
+
+def _run_steps(ops, leaves, steps):
+    """Evaluates the steps over the value pool, every operation kept in a tame
+    range (denominators >= 1, positive log/sqrt/pow arguments, bounded tan);
+    returns the last value."""
+    pool = list(leaves)
+    one = ops.const(pool[0], 1.0)
+    half = ops.const(pool[0], 0.5)
+    for st in steps:
+        kind, op = st[0], st[1]
+        if kind == "bin":
+            a, b = pool[st[2]], pool[st[3]]
+            if op == "div":
+                r = ops.div(a, ops.add(ops.mul(b, b), one))
+            elif op == "pow":
+                r = ops.pow(ops.add(ops.mul(a, a), half), ops.clamp(b, -1.5, 1.5))
+            else:
+                r = getattr(ops, op)(a, b)
+        elif kind == "unary":
+            a = pool[st[2]]
+            if op in ("log", "sqrt"):
+                r = getattr(ops, op)(ops.add(ops.mul(a, a), one))
+            elif op == "exp":
+                r = ops.exp(ops.clamp(a, -3.0, 3.0))
+            elif op == "tan":
+                r = ops.tan(ops.mul(ops.sin(a), half))
+            elif op == "clamp":
+                r = ops.clamp(a, -0.75, 0.75)
+            else:
+                r = getattr(ops, op)(a)
+        elif kind == "reduce":
+            r = getattr(ops, op)(pool[st[2]], st[3])
+        elif kind == "matmul":
+            r = ops.matmul(pool[st[2]], pool[st[3]])
+        else:
+            r = ops.transpose(pool[st[2]])
+        pool.append(r)
+    return pool[-1]
+
+
+def _sum_all(ops, out, shapes):
+    for ax in range(len(shapes[-1]) - 1, -1, -1):
+        out = ops.sum(out, ax)
+    return out
