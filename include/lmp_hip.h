@@ -151,8 +151,10 @@ int lmp_rt_empty_cache(void);
 int lmp_rt_pool_stats_get(lmp_rt_pool_stats* stats);
 
 /* Copies on the library stream.  h2d/d2h synchronise before returning so the
- * host buffer may be reused or read.  Replace the memcpy halves of
- * copy_cuda / vecCopyHostToDevice (memory.cu:103-174). */
+ * host buffer may be reused or read; from 4 MiB up they run through pinned
+ * staging buffers, host threads and the DMA engine overlapped chunk by chunk.
+ * Replace the memcpy halves of copy_cuda / vecCopyHostToDevice
+ * (memory.cu:103-174). */
 int lmp_rt_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int lmp_rt_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int lmp_rt_memcpy_d2d(void* dst, const void* src, size_t bytes);

@@ -552,3 +552,33 @@ def test_gemm_random_shapes_every_path(hip, m, n, k, ta, tb):
     t = got + bias[None, :]
     assert np.array_equal(out.numpy().view(np.uint32),
                           np.where(t < 0, np.float32(0), t).view(np.uint32))
+
+
+# ------------------------------------------------------------ host <-> device
+
+STAGE = 16 << 20  # bytes per staging chunk of lmp_rt_memcpy_h2d/d2h
+STAGED_MIN = 4 << 20
+
+
+@pytest.mark.parametrize("nbytes", [STAGED_MIN - 4, STAGED_MIN, STAGE, STAGE + 4,
+                                    3 * STAGE + 12, 100 * (1 << 20) + 8])
+def test_host_device_round_trip_every_byte(hip, nbytes):
+    """Copies below and above the staging threshold, of whole, partial and
+    several chunks, keep every bit (random words, NaN payloads included), in
+    both directions; a download right after a kernel sees its result."""
+    n = nbytes // 4
+    words = np.random.default_rng(nbytes).integers(0, 2 ** 32, n, dtype=np.uint32)
+    src = words.view(np.float32)
+    buf = up(hip, src)
+    back = buf.numpy()
+    assert back.view(np.uint32).tobytes() == words.tobytes()
+    # the download is ordered after the work queued before it
+    check_fill = hip.lib().lmp_k_fill(hip.CODE_OF[np.dtype(np.float32)], buf.ptr, n, 0.75)
+    hip.check(check_fill)
+    assert np.all(buf.numpy() == np.float32(0.75))
+    # upload into part of a larger buffer (offset destination), download the part
+    big = hip.DeviceBuffer((n + 3,), np.float32)
+    hip.check(hip.lib().lmp_rt_memcpy_h2d(big.ptr + 12, src.ctypes.data, n * 4))
+    part = np.empty(n, np.float32)
+    hip.check(hip.lib().lmp_rt_memcpy_d2h(part.ctypes.data, big.ptr + 12, n * 4))
+    assert part.view(np.uint32).tobytes() == words.tobytes()
