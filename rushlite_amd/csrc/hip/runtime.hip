@@ -9,6 +9,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <system_error>
 #include <thread>
 #include <vector>
 
@@ -247,8 +248,15 @@ class HostCopyPool {
  private:
   HostCopyPool() {
     const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
-    workers_ = std::min(kCopyThreads, hw) - 1;
-    for (unsigned i = 0; i < workers_; ++i) std::thread([this, i] { run(int(i) + 1); }).detach();
+    const unsigned want = std::min(kCopyThreads, hw) - 1;
+    // Fewer workers if the system refuses a thread (copy() uses what started).
+    try {
+      for (unsigned i = 0; i < want; ++i) {
+        std::thread([this, i] { run(int(i) + 1); }).detach();
+        workers_ = i + 1;
+      }
+    } catch (const std::system_error&) {
+    }
   }
 
   // Worker `part` copies slice `part` of each job that has one.
