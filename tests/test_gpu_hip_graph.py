@@ -183,3 +183,55 @@ def test_graph_memory_returns_after_release(rsl):
         assert np.all(once() == first)
     # each capture grows its own pool by one segment and frees it afterwards
     assert rsl._stats()["pool_device_mallocs"] - base == 3
+
+
+@pytest.mark.parametrize("capture_on", [False, True], ids=["eager_ops", "fused_ops"])
+@pytest.mark.parametrize("shape", [(64, 128), (33, 7)], ids=lambda s: f"{s[0]}x{s[1]}")
+@pytest.mark.parametrize("seed", range(4))
+def test_random_program_graph_replays_equal_eager(rsl, seed, shape, capture_on):
+    """A random program of the differential suite (broadcast binary ops,
+    unary ops, reductions, matmul, transpose), forward and backward, captured
+    into a graph; after the inputs are updated in place, every replay equals
+    an eager run on the new inputs bit for bit, output and every gradient."""
+    import test_gpu_graphs as TG
+    leaves, steps, shapes = TG.make_program_rc(seed, *shape)
+    rng = np.random.default_rng(1000 + seed)
+    lv = [rsl.Variable(rng.uniform(-1, 1, s).astype(np.float32), requires_grad=True)
+          for s in leaves]
+    base = TG.lamp_ops(rsl, rsl.dtype.float32)
+    consts = {v: rsl.Variable(np.array([v], np.float32)) for v in (1.0, 0.5)}
+
+    class ops(base):  # constants made before the capture: no upload inside it
+        @staticmethod
+        def const(like, v):
+            return consts[v]
+
+    def step():
+        for v in lv:
+            v.zero_grad()
+        with rsl.capture_on(capture_on):
+            out = TG.run(ops, lv, steps, shapes)
+        out.backward()
+        for v in lv:
+            v.grad.realize()
+        out.realize()
+        return out
+
+    step()  # compiles every kernel the capture records
+    graph = rsl.hip.Graph()
+    with graph.capture():
+        out_g = step()
+    grads_g = [v.grad for v in lv]
+    for rep in range(3):
+        new = [np.random.default_rng(7 * rep + seed).uniform(-1, 1, s).astype(np.float32)
+               for s in leaves]
+        for v, a in zip(lv, new):
+            v.data.copy(rsl.Variable(a).data)
+        graph.replay()
+        ev = [rsl.Variable(a, requires_grad=True) for a in new]
+        with rsl.capture_on(capture_on):
+            oe = TG.run(ops, ev, steps, shapes)
+        oe.backward()
+        assert np.array_equal(out_g.numpy(), oe.numpy()), rep
+        for i, (g, v) in enumerate(zip(grads_g, ev)):
+            assert np.array_equal(g.numpy(), v.grad.numpy()), (rep, i)
