@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define LMP_HIP_ABI_VERSION 7
+#define LMP_HIP_ABI_VERSION 8
 #define LMP_MAX_DIMS 16 /* align_utils.hpp:7 */
 /* Size of the fixed per-device workspace of lmp_k_gemm_f32_noalloc. */
 #define LMP_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
@@ -283,6 +283,23 @@ int lmp_k_gemm_colsum_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k
                           const float* a, size_t lda, const float* b, size_t ldb,
                           float* c, size_t ldc, int accumulate, float* colsum,
                           int colsum_accumulate);
+
+/* lmp_k_gemm_colsum_f32 (B untransposed) with ReLU's backward applied to B
+ * first: C (+)= op(A) * B' and colsum (+)= the column sums of B', where
+ * B'[k][j] = B[k][j] if 0 < mask[k][j] < +inf, else +0.0 -- ClampBackward's
+ * strict bounds for clamp(t, 0, DBL_MAX) (functions/unary_ops.cpp:27,
+ * cpu/kernels.hpp:143-152), `mask` the ReLU output stored like B (ldb).  A
+ * Linear -> ReLU pair's weight and bias gradients when its input needs no
+ * gradient, without materialising the masked gradient: the reference runs
+ * ReLU's backward, a transpose, a matmul and a reduction.  Small products
+ * (K <= 512, at most 2^21 multiply-adds) mask B as it is loaded, in one
+ * launch; larger ones mask into a scratch buffer, then take the column-sum
+ * GEMM.  Same bits as the clamp-backward kernel followed by
+ * lmp_k_gemm_colsum_f32. */
+int lmp_k_gemm_colsum_masked_f32(int trans_a, size_t m, size_t n, size_t k,
+                                 const float* a, size_t lda, const float* b,
+                                 const float* mask, size_t ldb, float* c, size_t ldc,
+                                 int accumulate, float* colsum, int colsum_accumulate);
 
 /* C = relu(op(A) * op(B) + bias): lmp_k_linear_f32 with ReLU applied in the
  * same epilogue, as the clamp functor computes clamp(t, 0, DBL_MAX) in float32

@@ -101,6 +101,8 @@ SIGNATURES = {
     "lmp_k_linear_relu_f32": (_i, [_i, _i, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _vp, _sz]),
     "lmp_k_gemm_colsum_f32": (_i, [_i, _i, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _i,
                                    _vp, _i]),
+    "lmp_k_gemm_colsum_masked_f32": (_i, [_i, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _sz, _vp, _sz,
+                                          _i, _vp, _i]),
     "lmp_k_transpose": (_i, [_i, _vp, _vp, _sz, _sz]),
     "lmp_jit_lookup": (_i, [C.c_uint64, C.POINTER(_vp)]),
     "lmp_jit_compile": (_i, [C.c_uint64, C.c_char_p, C.c_char_p,

@@ -164,7 +164,8 @@ void Variable::incr_grad_matmul(const Tensor& a, const Tensor& b, bool trans_a,
   tops::matmul_acc(impl_->grad, a, b, trans_a, trans_b);
 }
 
-bool Variable::incr_grad_linear(Variable& w, Variable& b, const Tensor& x, const Tensor& g) {
+bool Variable::incr_grad_linear(Variable& w, Variable& b, const Tensor& x, const Tensor& g,
+                                const Tensor* relu_out) {
   LMP_CHECK(w.requires_grad() && b.requires_grad())
       << "Cannot access grad() if requires_grad = false";
   const size_t n = g.shape().size() == 2 ? g.shape()[1] : 0;
@@ -173,7 +174,9 @@ bool Variable::incr_grad_linear(Variable& w, Variable& b, const Tensor& x, const
   // Accumulation is in place on realised buffers (their identity is kept).
   if (wg.defined()) wg.realize();
   if (bg.defined()) bg.realize();
-  if (!tops::matmul_colsum(x, g, true, false, &wg, &bg)) return false;
+  const bool done = relu_out ? tops::matmul_colsum_masked(x, g, *relu_out, true, &wg, &bg)
+                             : tops::matmul_colsum(x, g, true, false, &wg, &bg);
+  if (!done) return false;
   if (!w.impl_->grad.defined()) {
     // A GEMM accumulates from +0, so its product equals 0 + product exactly;
     // the column sums start from +0 as well.
@@ -455,7 +458,14 @@ Variable linear_relu(const Variable& x, const Variable& w, const Variable& b) {
   // every t, including NaN, +-0 and +-inf, so the pre-activation is not kept.
   return record(tops::linear(x.data(), w.data(), b.data(), true), {x, w, b},
                 "LinearReluBackward", [](LMP_BW_ARGS) {
-                  linear_backward(tops::clamp_backward(out.data(), G, 0.0,
+                  const Tensor h = out.data();
+                  // An input that needs no gradient (a first layer): only the
+                  // weight and bias gradients remain, and the GEMM applies the
+                  // mask as it loads G, so the masked gradient is never stored.
+                  if (!in[0].requires_grad() && in[1].requires_grad() && in[2].requires_grad() &&
+                      Variable::incr_grad_linear(in[1], in[2], in[0].data(), G, &h))
+                    return;
+                  linear_backward(tops::clamp_backward(h, G, 0.0,
                                                        std::numeric_limits<double>::max()),
                                   in);
                 });

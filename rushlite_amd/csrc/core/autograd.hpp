@@ -67,8 +67,11 @@ class Variable {
   void incr_grad_matmul(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b);
   // A Linear's weight and bias gradients together: w.grad += x^T @ g and
   // b.grad += the column sums of g, in one launch where the backend has the
-  // form (false, nothing done, otherwise).
-  static bool incr_grad_linear(Variable& w, Variable& b, const Tensor& x, const Tensor& g);
+  // form (false, nothing done, otherwise).  With relu_out (a Linear -> ReLU
+  // pair's output), g is first masked by ReLU's backward (g where
+  // 0 < relu_out < max, else 0) as the GEMM loads it.
+  static bool incr_grad_linear(Variable& w, Variable& b, const Tensor& x, const Tensor& g,
+                               const Tensor* relu_out = nullptr);
   void set_grad_fn(std::shared_ptr<Function> fn);
   void copy(const Variable& other);
   void fill(Scalar value);

@@ -321,6 +321,31 @@ void matmul_colsum_hip(const TensorImpl& a, const TensorImpl& b, bool ta, bool t
          "lmp_k_gemm_colsum_f32");
 }
 
+void matmul_colsum_masked_hip(const TensorImpl& a, const TensorImpl& b, const TensorImpl& mask,
+                              bool ta, TensorImpl& c, bool acc_c, TensorImpl& s, bool acc_s) {
+  const GemmShape sh = gemm_shape(a, b, ta, false);
+  LMP_CHECK(c.shape().size() == 2 && c.shape()[0] == sh.m && c.shape()[1] == sh.n)
+      << "add_inplace requires tensors with identical shapes";
+  LMP_CHECK(s.numel() == sh.n) << "add_inplace requires tensors with identical shapes";
+  if (!sh.m || !sh.n) return;
+  HostTimer timer(&backend_stats().gemm_host_ns);
+  const void* pa = mut(a);
+  const void* pb = mut(b);
+  const void* pm = mut(mask);
+  void* pc = c.data();
+  void* ps = s.data();
+  // One launch in the tiny-GEMM range (K <= 512, at most 2^21 multiply-adds),
+  // where the mask is applied as B is loaded; otherwise the mask kernel too.
+  count_launch();
+  if (sh.k > 512 || double(sh.m) * double(sh.n) * double(sh.k) > double(1 << 21)) count_launch();
+  hip_ok(lmp_k_gemm_colsum_masked_f32(ta, sh.m, sh.n, sh.k, static_cast<const float*>(pa),
+                                      a.shape()[1], static_cast<const float*>(pb),
+                                      static_cast<const float*>(pm), b.shape()[1],
+                                      static_cast<float*>(pc), sh.n, acc_c ? 1 : 0,
+                                      static_cast<float*>(ps), acc_s ? 1 : 0),
+         "lmp_k_gemm_colsum_masked_f32");
+}
+
 TensorImpl linear_hip(const TensorImpl& x, const TensorImpl& w, const TensorImpl& b,
                       bool relu) {
   const GemmShape s = gemm_shape(x, w, false, false);
@@ -417,6 +442,7 @@ LMP_REGISTER_DISPATCH(matmul_t_stub, kHip, matmul_t_hip)
 LMP_REGISTER_DISPATCH(matmul_acc_stub, kHip, matmul_acc_hip)
 LMP_REGISTER_DISPATCH(linear_stub, kHip, linear_hip)
 LMP_REGISTER_DISPATCH(matmul_colsum_stub, kHip, matmul_colsum_hip)
+LMP_REGISTER_DISPATCH(matmul_colsum_masked_stub, kHip, matmul_colsum_masked_hip)
 LMP_REGISTER_DISPATCH(transpose_stub, kHip, transpose_hip)
 
 }  // namespace lmp::tensor::hip

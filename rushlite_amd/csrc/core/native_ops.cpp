@@ -33,6 +33,7 @@ LMP_DEFINE_DISPATCH(matmul_t_fn, matmul_t_stub)
 LMP_DEFINE_DISPATCH(matmul_acc_fn, matmul_acc_stub)
 LMP_DEFINE_DISPATCH(linear_fn, linear_stub)
 LMP_DEFINE_DISPATCH(matmul_colsum_fn, matmul_colsum_stub)
+LMP_DEFINE_DISPATCH(matmul_colsum_masked_fn, matmul_colsum_masked_stub)
 
 namespace {
 using Acc = detail::UnsafeTensorAccessor;
@@ -233,6 +234,28 @@ bool matmul_colsum(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b,
   if (!acc_s) *s = wrap(TensorImpl(Storage(n * sizeof(float), dev), {n}, DataType::Float32));
   matmul_colsum_stub()(dev, *Acc::getImpl(a), *Acc::getImpl(b), trans_a, trans_b,
                        *Acc::getImpl(*c), acc_c, *Acc::getImpl(*s), acc_s);
+  return true;
+}
+
+bool matmul_colsum_masked(const Tensor& a, const Tensor& b, const Tensor& mask, bool trans_a,
+                          Tensor* c, Tensor* s) {
+  const DeviceType dev = a.device();
+  if (!matmul_colsum_masked_stub().has(dev) || b.device() != dev || mask.device() != dev)
+    return false;
+  const auto f32 = [](const Tensor& t) { return t.type() == DataType::Float32; };
+  if (!f32(a) || !f32(b) || !f32(mask) || a.shape().size() != 2 || b.shape().size() != 2 ||
+      mask.shape() != b.shape())
+    return false;
+  if (c->defined() && (!f32(*c) || c->device() != dev)) return false;
+  if (s->defined() && (!f32(*s) || s->device() != dev)) return false;
+  const size_t m = a.shape()[trans_a ? 1 : 0], n = b.shape()[1];
+  if (a.shape()[trans_a ? 0 : 1] == 0) return false;  // empty batch: the unfused path
+  const bool acc_c = c->defined(), acc_s = s->defined();
+  if (!acc_c)
+    *c = wrap(TensorImpl(Storage(m * n * sizeof(float), dev), {m, n}, DataType::Float32));
+  if (!acc_s) *s = wrap(TensorImpl(Storage(n * sizeof(float), dev), {n}, DataType::Float32));
+  matmul_colsum_masked_stub()(dev, *Acc::getImpl(a), *Acc::getImpl(b), *Acc::getImpl(mask),
+                              trans_a, *Acc::getImpl(*c), acc_c, *Acc::getImpl(*s), acc_s);
   return true;
 }
 

@@ -75,6 +75,14 @@ using linear_fn = TensorImpl (*)(const TensorImpl& x, const TensorImpl& w,
 using matmul_colsum_fn = void (*)(const TensorImpl& a, const TensorImpl& b, bool ta, bool tb,
                                   TensorImpl& c, bool acc_c, TensorImpl& s, bool acc_s);
 
+// matmul_colsum with ReLU's backward applied to b first (b' = b where
+// 0 < mask < max, else 0; mask stored like b): a Linear -> ReLU pair's weight
+// and bias gradients from its output gradient and its ReLU output.  b is not
+// transposed.
+using matmul_colsum_masked_fn = void (*)(const TensorImpl& a, const TensorImpl& b,
+                                         const TensorImpl& mask, bool ta, TensorImpl& c,
+                                         bool acc_c, TensorImpl& s, bool acc_s);
+
 #define LMP_FOR_BINARY_OPS(_) \
   _(add) _(sub) _(mul) _(div) _(pow) _(eq) _(ne) _(ge) _(le) _(gt) _(lt)
 #define LMP_FOR_UNARY_OPS(_) _(neg) _(exp) _(log) _(sqrt) _(abs) _(sin) _(cos) _(tan)
@@ -106,6 +114,7 @@ LMP_DECLARE_DISPATCH(matmul_t_fn, matmul_t_stub)
 LMP_DECLARE_DISPATCH(matmul_acc_fn, matmul_acc_stub)
 LMP_DECLARE_DISPATCH(linear_fn, linear_stub)
 LMP_DECLARE_DISPATCH(matmul_colsum_fn, matmul_colsum_stub)
+LMP_DECLARE_DISPATCH(matmul_colsum_masked_fn, matmul_colsum_masked_stub)
 
 Tensor clamp(const Tensor& a, Scalar lo, Scalar hi);
 Tensor abs_backward(const Tensor& input, const Tensor& grad);
@@ -123,6 +132,10 @@ Tensor linear(const Tensor& x, const Tensor& w, const Tensor& b, bool relu = fal
 // device has no such form or the dtypes are not float32.
 bool matmul_colsum(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b, Tensor* c,
                    Tensor* s);
+// The same with ReLU's backward mask applied to b (b untransposed; mask the
+// ReLU output, b's shape): *c (+)= op(a) @ b' and *s (+)= column sums of b'.
+bool matmul_colsum_masked(const Tensor& a, const Tensor& b, const Tensor& mask, bool trans_a,
+                          Tensor* c, Tensor* s);
 Tensor transpose(const Tensor& a);
 Tensor reshape(const Tensor& a, std::vector<size_t> shape);
 Tensor squeeze(const Tensor& a, size_t dim);

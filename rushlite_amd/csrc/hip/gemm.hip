@@ -31,6 +31,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <limits>
 #include <string>
 #include <type_traits>
 
@@ -84,7 +85,16 @@ struct GemmArgs {
   float* colsum;       // column sums of op(B) (+)= into it (or null): tiny kernel and LDS
                        // tiles with B untransposed and K unsplit
   int colsum_acc;
+  const float* bmask;  // tiny kernel, B untransposed: B[k][j] counts only where
+                       // 0 < bmask[k][j] < +inf (ReLU's backward mask; same layout as B)
 };
+
+// ReLU's backward mask on a gradient value: ClampBackward's strict bounds for
+// clamp(t, 0, DBL_MAX) in float32, t in (0, +inf) keeps g, anything else
+// (including NaN) gives +0.0.
+__device__ __forceinline__ float relu_masked(float g, float t) {
+  return (t > 0.0f && t < __builtin_huge_valf()) ? g : 0.0f;
+}
 
 // Linear's epilogue: v + b, then, when asked, ReLU as the clamp functor
 // computes clamp(t, 0, +inf) in float32: t < 0 ? 0 : t (NaN and -0.0 pass).
@@ -658,8 +668,9 @@ struct TinyMma<16> {
   __device__ __forceinline__ static int row(int r, int q) { return q * 4 + r; }
 };
 
-template <int BS, bool TA, bool TB, bool VA, bool VB>
+template <int BS, bool TA, bool TB, bool VA, bool VB, bool MB = false>
 __global__ __launch_bounds__(256) void gemm_tiny(GemmArgs g) {
+  static_assert(!MB || !TB, "the B mask is for B untransposed");
   using M = TinyMma<BS>;
   constexpr int G = 4 * (64 / BS);              // k values per group
   constexpr int kGroups = kTinyMaxK / G / 4;    // a wave's quarter of K <= 512
@@ -678,9 +689,9 @@ __global__ __launch_bounds__(256) void gemm_tiny(GemmArgs g) {
   const TinyOperand<VA> opa{tiny_rsrc(g.a, a_bytes),
                             row < g.m ? 4u * uint32_t(TA ? row : row * g.lda) : kTinyOob,
                             TA ? 4u * uint32_t(g.lda) : 4u};
-  const TinyOperand<VB> opb{tiny_rsrc(g.b, b_bytes),
-                            col < g.n ? 4u * uint32_t(TB ? col * g.ldb : col) : kTinyOob,
-                            TB ? 4u : 4u * uint32_t(g.ldb)};
+  const uint32_t b_base = col < g.n ? 4u * uint32_t(TB ? col * g.ldb : col) : kTinyOob;
+  const uint32_t b_kstep = TB ? 4u : 4u * uint32_t(g.ldb);
+  const TinyOperand<VB> opb{tiny_rsrc(g.b, b_bytes), b_base, b_kstep};
   // Every load of the wave's range is issued before the first MFMA (group
   // branches are uniform), so the range costs one memory latency.
   v4f a[kGroups], b[kGroups];
@@ -690,6 +701,20 @@ __global__ __launch_bounds__(256) void gemm_tiny(GemmArgs g) {
       a[c] = opa.load(G * (j0 + c) + 4 * q, kend);
       b[c] = opb.load(G * (j0 + c) + 4 * q, kend);
     }
+  if constexpr (MB) {
+    // The mask has B's layout: the same offsets, loaded beside B; values
+    // past the matrix read 0 and mask to 0, as B's do.
+    const TinyOperand<VB> opm{tiny_rsrc(g.bmask, b_bytes), b_base, b_kstep};
+    v4f mk[kGroups];
+#pragma unroll
+    for (int c = 0; c < kGroups; ++c)
+      if (j0 + c < j1) mk[c] = opm.load(G * (j0 + c) + 4 * q, kend);
+#pragma unroll
+    for (int c = 0; c < kGroups; ++c)
+      if (j0 + c < j1)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) b[c][s] = relu_masked(b[c][s], mk[c][s]);
+  }
   typename M::Acc acc = typename M::Acc(0.0f);
 #pragma unroll
   for (int c = 0; c < kGroups; ++c)
@@ -753,6 +778,17 @@ bool aligned16(const void* p);
 template <int BS, bool TA, bool TB>
 void launch_tiny_bs(Runtime* rt, const GemmArgs& g, bool va, bool vb) {
   const dim3 grid{uint32_t((g.m + BS - 1) / BS), uint32_t((g.n + BS - 1) / BS), 1u};
+  if constexpr (!TB) {
+    if (g.bmask) {  // B is never 128-bit along k here (k strides by ldb)
+      if (va)
+        hipLaunchKernelGGL((gemm_tiny<BS, TA, TB, !TA, false, true>), grid, dim3(256), 0,
+                           rt->stream, g);
+      else
+        hipLaunchKernelGGL((gemm_tiny<BS, TA, TB, false, false, true>), grid, dim3(256), 0,
+                           rt->stream, g);
+      return;
+    }
+  }
   if (va && vb)
     hipLaunchKernelGGL((gemm_tiny<BS, TA, TB, !TA, TB>), grid, dim3(256), 0, rt->stream, g);
   else if (va)
@@ -1823,6 +1859,56 @@ extern "C" int lmp_k_gemm_colsum_f32(int trans_a, int trans_b, size_t m, size_t 
   rc = lmp_k_reduce(LMP_RED_SUM, LMP_FLOAT32, dst, b, outer, len, inner);
   if (rc == LMP_OK && colsum_accumulate) rc = lmp_k_add_inplace(LMP_FLOAT32, colsum, dst, n);
   if (colsum_accumulate) scratch_free(dst);
+  return rc;
+}
+
+extern "C" int lmp_k_gemm_colsum_masked_f32(int trans_a, size_t m, size_t n, size_t k,
+                                            const float* a, size_t lda, const float* b,
+                                            const float* bmask, size_t ldb, float* c,
+                                            size_t ldc, int accumulate, float* colsum,
+                                            int colsum_accumulate) {
+  if (!colsum || !bmask) return fail(LMP_ERR_INVALID, "gemm_colsum_masked: null column sums or mask");
+  if (m == 0 || n == 0 || k == 0 || !a || !b || !c)
+    return fail(LMP_ERR_UNSUPPORTED, "gemm_colsum_masked: empty or null operand");
+  const size_t lim = 0x7fffffff;
+  if (m > lim || n > lim || k > lim || lda > lim || ldb > lim || ldc > lim)
+    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension above 2^31");
+  if ((trans_a ? lda < m : lda < k) || ldb < n || ldc < n)
+    return fail(LMP_ERR_INVALID, "gemm: leading dimension too small");
+  GemmArgs g{};
+  g.a = a;
+  g.b = b;
+  g.c = c;
+  g.m = int(m);
+  g.n = int(n);
+  g.k = int(k);
+  g.lda = int(lda);
+  g.ldb = int(ldb);
+  g.ldc = int(ldc);
+  g.accumulate = accumulate ? 1 : 0;
+  g.colsum = colsum;
+  g.colsum_acc = colsum_accumulate ? 1 : 0;
+  g.bmask = bmask;
+  if (tiny_ok(g)) {  // the mask applied as B is loaded: one launch
+    LMP_RUNTIME_OR_FAIL(rt);
+    return trans_a ? launch_tiny<true, false>(rt, g) : launch_tiny<false, false>(rt, g);
+  }
+  // Larger products: the masked gradient into a contiguous scratch [k, n] by
+  // the clamp-backward kernel, then the column-sum GEMM on it.
+  float* gm = static_cast<float*>(scratch_alloc(k * n * sizeof(float)));
+  if (!gm) return LMP_ERR_OOM;
+  lmp_bcast d{};
+  d.ndim = 2;
+  d.shape[0] = int64_t(k);
+  d.shape[1] = int64_t(n);
+  d.stride_a[0] = d.stride_b[0] = int64_t(ldb);
+  d.stride_a[1] = d.stride_b[1] = 1;
+  int rc = lmp_k_binary(LMP_BIN_CLAMP_BACKWARD, LMP_FLOAT32, gm, bmask, b, &d, 0.0,
+                        std::numeric_limits<double>::max());
+  if (rc == LMP_OK)
+    rc = lmp_k_gemm_colsum_f32(trans_a, 0, m, n, k, a, lda, gm, n, c, ldc, accumulate, colsum,
+                               colsum_accumulate);
+  scratch_free(gm);  // stream-ordered: the GEMM reads it first
   return rc;
 }
 

@@ -998,15 +998,17 @@ def test_leaf_region_storing_a_shared_node(rsl):
         assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
 
 
+@pytest.mark.parametrize("x_grad", [True, False], ids=["x_grad", "x_const"])
 @pytest.mark.parametrize("dt", ["float32", "float64"])
 @pytest.mark.parametrize("m,k,n", [(32, 256, 64), (20, 70, 10), (512, 2048, 2048), (64, 130, 33)],
                          ids=str)
-def test_linear_relu_node_matches_linear_then_relu(rsl, m, k, n, dt):
+def test_linear_relu_node_matches_linear_then_relu(rsl, m, k, n, dt, x_grad):
     """linear_relu (Sequential's Linear -> ReLU as one node, ReLU in the GEMM
     epilogue for float32) gives the values and the x, w, b gradients of linear
     followed by clamp(., 0, DBL_MAX), bit for bit, with infinities and NaN in
     x (the backward masks by the output, which must equal masking by the
-    input)."""
+    input).  With x needing no gradient (a first layer) the float32 weight and
+    bias gradients apply ReLU's mask inside the column-sum GEMM."""
     rng = np.random.default_rng(m * k + n + 1)
     x_np = rng.standard_normal((m, k)).astype(dt)
     x_np[0, :3] = [np.inf, -np.inf, np.nan] if m > 1 else x_np[0, :3]
@@ -1015,13 +1017,13 @@ def test_linear_relu_node_matches_linear_then_relu(rsl, m, k, n, dt):
     view = np.uint32 if dt == "float32" else np.uint64
     outs, grads = [], []
     for fused in (True, False):
-        x = rsl.Variable(x_np, dtype=getattr(rsl.dtype, dt), requires_grad=True)
+        x = rsl.Variable(x_np, dtype=getattr(rsl.dtype, dt), requires_grad=x_grad)
         w = rsl.Variable(w_np, dtype=getattr(rsl.dtype, dt), requires_grad=True)
         b = rsl.Variable(b_np, dtype=getattr(rsl.dtype, dt), requires_grad=True)
         y = rsl._C.linear_relu(x, w, b) if fused else rsl.clamp(rsl.linear(x, w, b), 0, DBL_MAX)
         (y * 0.5 + 1.0).sum(1).sum(0).backward()
         outs.append(y.numpy())
-        grads.append([x.grad.numpy(), w.grad.numpy(), b.grad.numpy()])
+        grads.append(([x.grad.numpy()] if x_grad else []) + [w.grad.numpy(), b.grad.numpy()])
     assert np.array_equal(outs[0].view(view), outs[1].view(view))
     for g0, g1 in zip(*grads):
         assert np.array_equal(g0.view(view), g1.view(view))

@@ -582,3 +582,47 @@ def test_host_device_round_trip_every_byte(hip, nbytes):
     part = np.empty(n, np.float32)
     hip.check(hip.lib().lmp_rt_memcpy_d2h(part.ctypes.data, big.ptr + 12, n * 4))
     assert part.view(np.uint32).tobytes() == words.tobytes()
+
+
+@pytest.mark.parametrize("m,n,k,ta,ldb_pad", [
+    (256, 64, 32, 1, 0), (64, 10, 32, 1, 0), (5, 7, 3, 1, 0), (96, 40, 17, 0, 0),
+    (64, 33, 20, 1, 3), (4096, 1000, 512, 1, 0), (300, 260, 600, 1, 4)], ids=str)
+@pytest.mark.parametrize("acc", [False, True], ids=["write", "accumulate"])
+def test_gemm_colsum_masked_equals_mask_then_colsum(hip, m, n, k, ta, ldb_pad, acc):
+    """lmp_k_gemm_colsum_masked_f32 (ReLU's backward applied to B inside the
+    column-sum GEMM, or through a scratch buffer for large products) equals
+    the clamp-backward kernel followed by lmp_k_gemm_colsum_f32 bit for bit,
+    for masks holding NaN, +-0, +-inf, negative and positive values, strided
+    B and both A orientations."""
+    L = hip.lib()
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    ldb = n + ldb_pad
+    a_np = rng.standard_normal((k, m) if ta else (m, k)).astype(np.float32)
+    g_np = rng.standard_normal((k, ldb)).astype(np.float32)
+    h_np = rng.standard_normal((k, ldb)).astype(np.float32)
+    specials = np.array([np.nan, 0.0, -0.0, np.inf, -np.inf, 1e-38, -1e-38, 3.0], np.float32)
+    h_np.reshape(-1)[: min(h_np.size, 64)] = np.resize(specials, min(h_np.size, 64))
+    g_np.reshape(-1)[5::97] = -0.0
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    s0 = rng.standard_normal(n).astype(np.float32)
+    a, g, h = up(hip, a_np), up(hip, g_np), up(hip, h_np)
+    lda = m if ta else k
+    # reference: mask into a contiguous buffer, then the column-sum GEMM
+    gm = hip.DeviceBuffer((k, n), np.float32)
+    d, _ = hip.make_bcast((k, n), (k, n))
+    d.stride_a[0] = d.stride_b[0] = ldb
+    hip.check(L.lmp_k_binary(hip.BIN["clamp_backward"], hip.CODE_OF[np.dtype(np.float32)],
+                             gm.ptr, h.ptr, g.ptr, C.byref(d), 0.0, 1.7976931348623157e308))
+    c_ref, s_ref = up(hip, c0), up(hip, s0)
+    hip.check(L.lmp_k_gemm_colsum_f32(ta, 0, m, n, k, a.ptr, lda, gm.ptr, n, c_ref.ptr, n,
+                                      int(acc), s_ref.ptr, int(acc)))
+    c_got, s_got = up(hip, c0), up(hip, s0)
+    hip.check(L.lmp_k_gemm_colsum_masked_f32(ta, m, n, k, a.ptr, lda, g.ptr, h.ptr, ldb,
+                                             c_got.ptr, n, int(acc), s_got.ptr, int(acc)))
+    assert np.array_equal(c_got.numpy().view(np.uint32), c_ref.numpy().view(np.uint32))
+    assert np.array_equal(s_got.numpy().view(np.uint32), s_ref.numpy().view(np.uint32))
+    # and the product is the masked one (against float64 on the host)
+    gmask = np.where((h_np[:, :n] > 0) & (h_np[:, :n] < np.inf), g_np[:, :n], 0.0)
+    aa = a_np.T if ta else a_np
+    want = aa.astype(np.float64) @ gmask.astype(np.float64) + (c0 if acc else 0.0)
+    assert rel_err(c_got.numpy(), want) <= 1e-5
