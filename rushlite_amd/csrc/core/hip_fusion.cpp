@@ -522,6 +522,13 @@ void emit_params(std::ostringstream& os, const Region& r, const std::string& nam
 // ordinary loads.  Leaf shapes are part of the structural key, so the choice
 // is fixed by it.
 constexpr size_t kStreamBytes = size_t(256) << 20;
+// Outputs of more than half the MALL are stored with the nontemporal hint,
+// smaller ones with ordinary stores, so that the kernel reading them next can
+// find them in the MALL (measured on MI355X: a producer and its consumer over
+// 64 MiB operands 56.8 -> 46.5 us with ordinary stores; 192 MiB and up,
+// nontemporal stores are faster).  The output shape is part of the
+// structural key, so the choice is fixed by it.
+constexpr size_t kStreamStoreBytes = size_t(128) << 20;
 
 // The body of a float4 (vec) region: block `block` owns output float4s
 // [256 * block, 256 * block + 256) (one-shot).
@@ -564,10 +571,17 @@ void emit_vec_body(std::ostringstream& os, const Region& r, const Plan& p, const
       os << "    x" << k << "." << comp[c] << " = t" << r.node_of.at(r.outputs[k]) << ";\n";
     os << "  }\n";
   }
-  for (size_t k = 0; k < r.outputs.size(); ++k)
-    os << "  __builtin_nontemporal_store(x" << k << ", reinterpret_cast<lmp_v4*>(" << nm.xo << k
-       << ") + v);\n";
-  os << "  __builtin_nontemporal_store(o, reinterpret_cast<lmp_v4*>(" << nm.out << ") + v);\n";
+  // Every output of a float4 region has the root's shape.
+  const bool stream_out = p.n * sizeof(float) > kStreamStoreBytes;
+  const auto store = [&](const std::string& val, const std::string& dst) {
+    if (stream_out)
+      os << "  __builtin_nontemporal_store(" << val << ", reinterpret_cast<lmp_v4*>(" << dst
+         << ") + v);\n";
+    else
+      os << "  reinterpret_cast<lmp_v4*>(" << dst << ")[v] = " << val << ";\n";
+  };
+  for (size_t k = 0; k < r.outputs.size(); ++k) store("x" + std::to_string(k), nm.xo + std::to_string(k));
+  store("o", nm.out);
   os << "  }\n  }\n";
 }
 

@@ -87,6 +87,12 @@ __device__ __forceinline__ v4f load_full4(const float* p, int nt) {
   return nt ? __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p))
             : *reinterpret_cast<const v4f*>(p);
 }
+// A float4 of the output: nontemporal when the output is more than
+// kStreamStoreBytes (`nts`, uniform across the launch).
+__device__ __forceinline__ void store_full4(float* p, v4f v, int nts) {
+  if (nts) __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(p));
+  else *reinterpret_cast<v4f*>(p) = v;
+}
 
 // out[r, c] = op(a[r*a_row + c*a_in], b[r*b_row + c*b_in]) with a_in, b_in
 // in {0, 1} fixed at compile time; lane v produces float4 v of the output.
@@ -94,7 +100,7 @@ template <int OP, bool A_IN, bool B_IN, bool ROWS>
 __global__ __launch_bounds__(kBlock) void bin2d_f32(
     float* __restrict__ out, const float* __restrict__ a,
     const float* __restrict__ b, uint32_t nvec, FastDiv cols4, int64_t a_row,
-    int64_t b_row, float lo, float hi, int nt) {
+    int64_t b_row, float lo, float hi, int nt, int nts) {
   const uint32_t v = blockIdx.x * kBlock + threadIdx.x;
   if (v >= nvec) return;
   const uint32_t r = ROWS ? cols4.div(v) : 0;
@@ -111,7 +117,7 @@ __global__ __launch_bounds__(kBlock) void bin2d_f32(
   o.y = binary_apply<OP, float>(xa.y, xb.y, lo, hi);
   o.z = binary_apply<OP, float>(xa.z, xb.z, lo, hi);
   o.w = binary_apply<OP, float>(xa.w, xb.w, lo, hi);
-  __builtin_nontemporal_store(o, reinterpret_cast<v4f*>(out) + v);
+  store_full4(out + uint64_t(v) * 4, o, nts);
 }
 
 // ------------------------------------------------------------ generic path
@@ -199,10 +205,12 @@ int launch_bin_f32(float* out, const float* a, const float* b,
       const FastDiv cols4(uint32_t(cols / 4));
       const int grid = grid_for(nvec, kBlock);
       const bool rws = rows > 1;
-      const int nt = uint64_t(rows) * uint64_t(cols) * sizeof(float) >= kStreamBytes ? 1 : 0;
+      const uint64_t out_bytes = uint64_t(rows) * uint64_t(cols) * sizeof(float);
+      const int nt = out_bytes >= kStreamBytes ? 1 : 0;
+      const int nts = out_bytes > kStreamStoreBytes ? 1 : 0;
 #define LMP_BIN2D(AI, BI, RW)                                                  \
   hipLaunchKernelGGL((bin2d_f32<OP, AI, BI, RW>), dim3(grid), dim3(kBlock), 0, \
-                     rt->stream, out, a, b, nvec, cols4, a_row, b_row, lo, hi, nt)
+                     rt->stream, out, a, b, nvec, cols4, a_row, b_row, lo, hi, nt, nts)
       if (a_in == 1 && b_in == 1) {
         if (rws) LMP_BIN2D(true, true, true); else LMP_BIN2D(true, true, false);
       } else if (a_in == 1) {
@@ -254,7 +262,7 @@ int dispatch_bin(int op, T* out, const T* a, const T* b, const Coalesced& c,
 template <int OP>
 __global__ __launch_bounds__(kBlock) void unary_f32_vec(
     float* __restrict__ out, const float* __restrict__ in, uint32_t nvec,
-    float lo, float hi, int nt) {
+    float lo, float hi, int nt, int nts) {
   const uint32_t v = blockIdx.x * kBlock + threadIdx.x;
   if (v >= nvec) return;
   const v4f x = load_full4(in + uint64_t(v) * 4, nt);
@@ -263,7 +271,7 @@ __global__ __launch_bounds__(kBlock) void unary_f32_vec(
   o.y = unary_apply<OP, float>(x.y, lo, hi);
   o.z = unary_apply<OP, float>(x.z, lo, hi);
   o.w = unary_apply<OP, float>(x.w, lo, hi);
-  __builtin_nontemporal_store(o, reinterpret_cast<v4f*>(out) + v);
+  store_full4(out + uint64_t(v) * 4, o, nts);
 }
 
 template <int OP, typename T>
@@ -286,7 +294,8 @@ int launch_unary(T* out, const T* in, size_t n, double p0, double p1) {
       const int grid = grid_for(nvec, kBlock);
       hipLaunchKernelGGL((unary_f32_vec<OP>), dim3(grid), dim3(kBlock), 0,
                          rt->stream, out, in, nvec, static_cast<float>(p0),
-                         static_cast<float>(p1), n * sizeof(float) >= kStreamBytes ? 1 : 0);
+                         static_cast<float>(p1), n * sizeof(float) >= kStreamBytes ? 1 : 0,
+                         n * sizeof(float) > kStreamStoreBytes ? 1 : 0);
       LMP_LAUNCH_CHECK("unary_f32_vec");
       return LMP_OK;
     }
@@ -333,9 +342,9 @@ __global__ __launch_bounds__(kBlock) void fill_scalar(T* __restrict__ out,
 
 __global__ __launch_bounds__(kBlock) void fill_f32_vec(float* __restrict__ out,
                                                        uint32_t nvec,
-                                                       float value) {
+                                                       float value, int nts) {
   const uint32_t v = blockIdx.x * kBlock + threadIdx.x;
-  if (v < nvec) __builtin_nontemporal_store(v4f(value), reinterpret_cast<v4f*>(out) + v);
+  if (v < nvec) store_full4(out + uint64_t(v) * 4, v4f(value), nts);
 }
 
 template <typename S, typename D>
@@ -428,7 +437,8 @@ int lmp_k_fill(int dtype, void* out, size_t n, double value) {
         const uint32_t nvec = uint32_t(n / 4);
         hipLaunchKernelGGL(fill_f32_vec, dim3(grid_for(nvec, kBlock)),
                            dim3(kBlock), 0, rt->stream, static_cast<float*>(out),
-                           nvec, static_cast<float>(value));
+                           nvec, static_cast<float>(value),
+                           n * sizeof(float) > kStreamStoreBytes ? 1 : 0);
         LMP_LAUNCH_CHECK("fill_f32_vec");
         return LMP_OK;
       }
