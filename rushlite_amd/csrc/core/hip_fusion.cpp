@@ -580,7 +580,8 @@ void emit_vec_body(std::ostringstream& os, const Region& r, const Plan& p, const
     else
       os << "  reinterpret_cast<lmp_v4*>(" << dst << ")[v] = " << val << ";\n";
   };
-  for (size_t k = 0; k < r.outputs.size(); ++k) store("x" + std::to_string(k), nm.xo + std::to_string(k));
+  for (size_t k = 0; k < r.outputs.size(); ++k)
+    store("x" + std::to_string(k), nm.xo + std::to_string(k));
   store("o", nm.out);
   os << "  }\n  }\n";
 }

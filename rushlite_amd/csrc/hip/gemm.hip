@@ -1867,7 +1867,8 @@ extern "C" int lmp_k_gemm_colsum_masked_f32(int trans_a, size_t m, size_t n, siz
                                             const float* bmask, size_t ldb, float* c,
                                             size_t ldc, int accumulate, float* colsum,
                                             int colsum_accumulate) {
-  if (!colsum || !bmask) return fail(LMP_ERR_INVALID, "gemm_colsum_masked: null column sums or mask");
+  if (!colsum || !bmask)
+    return fail(LMP_ERR_INVALID, "gemm_colsum_masked: null column sums or mask");
   if (m == 0 || n == 0 || k == 0 || !a || !b || !c)
     return fail(LMP_ERR_UNSUPPORTED, "gemm_colsum_masked: empty or null operand");
   const size_t lim = 0x7fffffff;
