@@ -2,16 +2,19 @@
 // (best fit, split, coalesce, segment release, unknown-address rejection),
 // its growth policy on an out-of-memory device (wait, release the cached free
 // segments, retry once; allocator.cu:101-125) against a synthetic device, and
-// the magic-number divider.  Built and run by tests/test_host_native.py with
-// g++; no GPU involved.
+// the magic-number divider, and the host thread pool of the staged copies
+// (slices of random lengths and offsets copied byte for byte).  Built and run
+// by tests/test_host_native.py with g++; no GPU involved.
 #include <cassert>
 #include <cstdio>
+#include <cstring>
 #include <random>
 #include <string>
 #include <vector>
 
 #include "arena.hpp"
 #include "fastdiv.hpp"
+#include "host_copy.hpp"
 
 using lmp_hip::Arena;
 using lmp_hip::DeviceAlloc;
@@ -216,8 +219,29 @@ int fastdiv_checks() {
   return 0;
 }
 
+int host_copy_checks() {
+  lmp_hip::HostCopyPool& pool = lmp_hip::HostCopyPool::get();
+  CHECK(pool.threads() >= 1 && pool.threads() <= lmp_hip::kCopyThreads);
+  std::mt19937_64 rng(11);
+  std::vector<unsigned char> src(24u << 20), dst;
+  for (auto& b : src) b = static_cast<unsigned char>(rng());
+  const size_t sizes[] = {0, 1, 63, 64, 65, 4096, (1u << 20) - 1, 1u << 20, (1u << 20) + 1,
+                          3u << 20, (5u << 20) + 17, (16u << 20) + 12345, 24u << 20};
+  for (int round = 0; round < 3; ++round) {
+    for (size_t n : sizes) {
+      const size_t off = n < src.size() ? rng() % (src.size() - n + 1) : 0;
+      dst.assign(n + 32, 0xAB);
+      pool.copy(dst.data() + 16, src.data() + off, n);
+      CHECK(std::memcmp(dst.data() + 16, src.data() + off, n) == 0);
+      for (int i = 0; i < 16; ++i) CHECK(dst[i] == 0xAB && dst[n + 16 + i] == 0xAB);
+    }
+  }
+  return 0;
+}
+
 int main() {
   if (arena_checks()) return 1;
+  if (host_copy_checks()) return 1;
   if (growth_policy_checks()) return 1;
   if (fastdiv_checks()) return 1;
   std::printf("host checks ok\n");

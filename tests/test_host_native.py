@@ -46,14 +46,22 @@ def test_library_exports_every_declared_symbol():
 
 
 @pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
-def test_arena_and_fastdiv(tmp_path):
+@pytest.mark.parametrize("sanitize", [None, "thread"], ids=["plain", "tsan"])
+def test_arena_fastdiv_and_copy_pool(tmp_path, sanitize):
+    """The arena, its growth policy, the divider and the staged copies' host
+    thread pool; once more under ThreadSanitizer for the pool's hand-offs."""
     exe = tmp_path / "host_check"
-    subprocess.run(["g++", "-O2", "-std=c++20", f"-I{HIP_SRC}",
-                    str(ROOT / "tests" / "native" / "host_check.cpp"), "-o", str(exe)],
-                   check=True)
-    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    flags = ["-O1", "-g", f"-fsanitize={sanitize}"] if sanitize else ["-O2"]
+    build = subprocess.run(["g++", *flags, "-std=c++20", "-pthread", f"-I{HIP_SRC}",
+                            str(ROOT / "tests" / "native" / "host_check.cpp"), "-o", str(exe)],
+                           capture_output=True, text=True)
+    if sanitize and build.returncode != 0:
+        pytest.skip(f"g++ cannot build with -fsanitize={sanitize} here")
+    assert build.returncode == 0, build.stderr
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert out.returncode == 0, out.stdout + out.stderr
     assert "host checks ok" in out.stdout
+    assert "WARNING: ThreadSanitizer" not in out.stderr, out.stderr
 
 
 def test_package_imports_and_gpu_ops_fail_loudly_without_gpu():
