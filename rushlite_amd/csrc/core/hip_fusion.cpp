@@ -533,7 +533,7 @@ constexpr size_t kStreamStoreBytes = size_t(128) << 20;
 // The body of a float4 (vec) region: block `block` owns output float4s
 // [256 * block, 256 * block + 256) (one-shot).
 void emit_vec_body(std::ostringstream& os, const Region& r, const Plan& p, const Names& nm,
-                   const std::string& block) {
+                   const std::string& block, bool stream_stores = false) {
   const size_t nl = r.leaves.size();
   const bool rows = p.groups.size() == 2;
   os << "  {\n  const unsigned v = " << block << " * " << kBlock << "u + threadIdx.x;\n";
@@ -572,7 +572,7 @@ void emit_vec_body(std::ostringstream& os, const Region& r, const Plan& p, const
     os << "  }\n";
   }
   // Every output of a float4 region has the root's shape.
-  const bool stream_out = p.n * sizeof(float) > kStreamStoreBytes;
+  const bool stream_out = stream_stores || p.n * sizeof(float) > kStreamStoreBytes;
   const auto store = [&](const std::string& val, const std::string& dst) {
     if (stream_out)
       os << "  __builtin_nontemporal_store(" << val << ", reinterpret_cast<lmp_v4*>(" << dst
@@ -662,11 +662,19 @@ std::string codegen_multi(const std::vector<const Region*>& rs, const std::vecto
   for (size_t i = 0; i < rs.size(); ++i)
     emit_region_params(os, *rs[i], f64[i] ? "double" : "float", region_names(i), i == 0);
   os << ") {\n";
+  // A group is an optimizer's parameter updates, read again only by the next
+  // step: past the store threshold as a whole, its outputs take nontemporal
+  // stores even where one region alone would not (37.66 M updated parameters
+  // of config 4: 69.1 -> 67.4 us).
+  uint64_t out_bytes = 0;
+  for (size_t i = 0; i < rs.size(); ++i)
+    out_bytes += ps[i]->n * (f64[i] ? sizeof(double) : sizeof(float)) * (1 + rs[i]->outputs.size());
+  const bool stream_group = out_bytes > kStreamStoreBytes;
   uint64_t off = 0;
   for (size_t i = 0; i < rs.size(); ++i) {
     os << (i ? "  else " : "  ") << "if (blockIdx.x < " << off + blocks[i] << "u)\n";
     const std::string block = "(blockIdx.x - " + std::to_string(off) + "u)";
-    if (ps[i]->vec) emit_vec_body(os, *rs[i], *ps[i], region_names(i), block);
+    if (ps[i]->vec) emit_vec_body(os, *rs[i], *ps[i], region_names(i), block, stream_group);
     else emit_indexed_body(os, *rs[i], *ps[i], f64[i] ? "double" : "float", region_names(i), block);
     off += blocks[i];
   }
