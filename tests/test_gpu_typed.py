@@ -204,6 +204,35 @@ def test_gemm_float64_large_tiles(hip, m, n, k, ta, tb):
     assert rel_err(got, ar @ br) <= 1e-12
 
 
+def _up_offset(hip, arr):
+    """arr stored one double past a 16-byte boundary, rows padded by one
+    element: returns (buffer, address of element [0, 0], leading dimension)."""
+    rows, cols = arr.shape
+    flat = np.zeros(1 + rows * (cols + 1), np.float64)
+    flat[1:].reshape(rows, cols + 1)[:, :cols] = arr
+    buf = up(hip, flat)
+    return buf, buf.ptr + 8, cols + 1
+
+
+# The large-tile kernel loads 16-byte pairs without bounds checks for tiles
+# inside C when both operands are 16-byte aligned with even leading
+# dimensions, and checked pairs otherwise.  Both fill the same LDS tile, so the
+# same random product through operands one double off alignment with odd
+# leading dimensions gives the same bits.
+@pytest.mark.parametrize("m,n,k", [(2048, 2048, 200), (2180, 1990, 96)], ids=str)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_float64_large_tiles_unaligned_same_bits(hip, m, n, k, ta, tb):
+    rng = np.random.default_rng(5 * m + n + 3 * k + 17 * ta + 19 * tb)
+    a, b = rng.standard_normal((m, k)), rng.standard_normal((k, n))
+    sa, sb = (a.T.copy() if ta else a), (b.T.copy() if tb else b)
+    got = hip.gemm(up(hip, sa), up(hip, sb), trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert rel_err(got, a @ b) <= 1e-12
+    (ba, pa, lda), (bb, pb, ldb) = _up_offset(hip, sa), _up_offset(hip, sb)
+    out = hip.DeviceBuffer((m, n), np.float64)
+    hip.check(hip.lib().lmp_k_gemm(out.code, ta, tb, m, n, k, pa, lda, pb, ldb, out.ptr, n, 0))
+    assert np.array_equal(out.numpy().view(np.int64), got.view(np.int64))
+
+
 # ------------------------------------------------- framework level
 
 @pytest.fixture(scope="module")
