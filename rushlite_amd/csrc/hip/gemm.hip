@@ -1041,10 +1041,18 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
   };
 
+  // Sub-steps alternate between two fragment buffers; the last one of a tile
+  // (odd, NU being even) uses fa1/fb1.  Its MFMAs are held back until after
+  // the next tile's barrier: they need only registers, so they keep the
+  // matrix cores busy while the waves issue that tile's DMA and wait for its
+  // first fragments, where the 8 waves of one workgroup would otherwise all
+  // stall together.  The MFMA order of every accumulator is unchanged.
+  static_assert(NU % 2 == 0, "the last sub-step's fragments are fa1/fb1");
   float fa0[TM][SU], fb0[TN][SU], fa1[TM][SU], fb1[TN][SU];
 #pragma unroll
   for (int t = 0; t < S - 1; ++t)
     if (kt0 + t < kt1) issue(kt0 + t, t);
+  bool owed = false;  // the previous tile's last sub-step is still to run
   for (int kt = kt0; kt < kt1; ++kt) {
     const int rel = kt - kt0;
     const int stage = rel % S;
@@ -1054,21 +1062,44 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
     // The memory clobber keeps the compiler from moving LDS accesses across.
     asm volatile("s_barrier" ::: "memory");
     // The stage refilled here was last read in the previous iteration, whose
-    // reads every wave retired before this barrier.
-    if (kt + S - 1 < kt1) issue(kt + S - 1, (rel + S - 1) % S);
+    // reads every wave retired before this barrier (the held-back MFMAs read
+    // registers only).
     read_frag(stage, 0, fa0, fb0);
+    if (owed) mma(fa1, fb1);
+    if (kt + S - 1 < kt1) issue(kt + S - 1, (rel + S - 1) % S);
+    // Order for the scheduler (masks: 0x8 MFMA, 0x20 global load, 0x100 LDS
+    // read, 0x2 / 0x4 VALU / SALU): the first fragments' LDS reads, then one
+    // held-back MFMA per DMA instruction with its address work.
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x006, 6, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      if (u + 1 < NU) {
-        if (u % 2 == 0) read_frag(stage, u + 1, fa1, fb1);
-        else read_frag(stage, u + 1, fa0, fb0);
+    for (int u = 0; u + 1 < NU; ++u) {
+      if (u % 2 == 0) {
+        read_frag(stage, u + 1, fa1, fb1);
+        mma(fa0, fb0);
+      } else {
+        read_frag(stage, u + 1, fa0, fb0);
+        mma(fa1, fb1);
       }
-      __builtin_amdgcn_sched_barrier(0);
-      if (u % 2 == 0) mma(fa0, fb0);
-      else mma(fa1, fb1);
+      // The next sub-step's LDS reads one per MFMA among the first of this
+      // sub-step's MFMAs, with their address work.
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
+    owed = true;
     if constexpr (!TB) {
       if (do_cs) {
         const float* sb = smem + stage * C::STAGE + C::A_PANEL;
@@ -1081,6 +1112,7 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
+  if (owed) mma(fa1, fb1);
 
   if constexpr (!TB) {
     if (do_cs) {
