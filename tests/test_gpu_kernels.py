@@ -288,6 +288,34 @@ def test_gemm(hip, oracle, m, n, k, ta, tb):
     assert rel_err(dc.numpy(), c0.astype(np.float64) + want) <= 1e-4
 
 
+# Shapes that reach each LDS-DMA configuration with ragged tiles and a ragged
+# last K tile: 256 x 256 tiles (their tiles cover the CUs), 256 x 128 tiles
+# split over K (M >= 512, N >= 2048, K >= 2048), 128 x 128 tiles unsplit and
+# split 13 ways.  Operands are small integers, so every product and partial
+# sum is exact in float32 and the result must equal the float64 product bit
+# for bit whatever the order: a skipped, repeated or misplaced MFMA step, tile
+# or K split shows as a wrong integer.
+LDS_EXACT_SHAPES = [(4000, 4100, 300), (520, 2100, 2080), (2100, 2100, 700),
+                    (600, 1000, 4096)]
+
+
+@pytest.mark.parametrize("m,n,k", LDS_EXACT_SHAPES, ids=str)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_lds_paths_exact_on_integer_operands(hip, m, n, k, ta, tb):
+    rng = np.random.default_rng(m + 5 * n + 7 * k + 11 * ta + 13 * tb)
+    a = rng.integers(-4, 5, (m, k)).astype(np.float32)
+    b = rng.integers(-4, 5, (k, n)).astype(np.float32)
+    want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+    da = up(hip, a.T.copy() if ta else a)
+    db = up(hip, b.T.copy() if tb else b)
+    got = hip.gemm(da, db, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert np.array_equal(got, want)
+    c0 = rng.integers(-100, 101, (m, n)).astype(np.float32)
+    dc = up(hip, c0)
+    hip.gemm(da, db, trans_a=bool(ta), trans_b=bool(tb), out=dc, accumulate=True)
+    assert np.array_equal(dc.numpy(), c0 + want)
+
+
 def test_gemm_config3_square(hip, oracle):
     """M=N=K=4096 with entries N(0, 0.02): fwd, dX and dW orientations against
     float64 (the oracle's naive fp32 GEMM at this size takes minutes; its
