@@ -90,7 +90,7 @@ def load(fast: bool | None = None) -> C.CDLL:
     if name not in _libs:
         path = HERE / name
         if not path.exists():
-            raise RuntimeError(f"{path} missing: run `python -m rushlite_amd.build oracle`")
+            raise RuntimeError(f"{path} missing: run `python rushlite_amd/build.py oracle`")
         lib = C.CDLL(str(path))
         P = C.c_void_p
         i64 = C.c_int64

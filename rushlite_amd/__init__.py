@@ -6,7 +6,7 @@ capture, no_grad, Module and nets.layers, with the GPU device being the
 HIP backend (rsl.device.hip; rsl.device.cuda is the same device).
 
 The compiled parts are in-tree shared libraries built by
-`python -m rushlite_amd.build`; importing fails loudly when they are missing.
+`python rushlite_amd/build.py`; importing fails loudly when they are missing.
 """
 from __future__ import annotations
 
@@ -14,7 +14,7 @@ try:
     from . import _C  # noqa: F401
 except ImportError as e:  # pragma: no cover - exercised only without a build
     raise ImportError(
-        "rushlite_amd._C is not built; run `python -m rushlite_amd.build`"
+        "rushlite_amd._C is not built; run `python rushlite_amd/build.py`"
     ) from e
 
 from ._C import *  # noqa: F401,F403

@@ -103,6 +103,8 @@ SIGNATURES = {
                                    _vp, _i]),
     "lmp_k_gemm_colsum_masked_f32": (_i, [_i, _sz, _sz, _sz, _vp, _sz, _vp, _vp, _sz, _vp, _sz,
                                           _i, _vp, _i]),
+    "lmp_k_linear_backward_f32": (_i, [_sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz,
+                                       _i, _vp, _sz, _i, _vp, _i]),
     "lmp_k_transpose": (_i, [_i, _vp, _vp, _sz, _sz]),
     "lmp_jit_lookup": (_i, [C.c_uint64, C.POINTER(_vp)]),
     "lmp_jit_compile": (_i, [C.c_uint64, C.c_char_p, C.c_char_p,
@@ -121,7 +123,7 @@ def lib() -> C.CDLL:
     if _lib is None:
         if not LIB_PATH.exists():
             raise RuntimeError(
-                f"{LIB_PATH} is missing: build it with `python -m rushlite_amd.build`")
+                f"{LIB_PATH} is missing: build it with `python rushlite_amd/build.py hip`")
         handle = C.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | C.RTLD_GLOBAL)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(handle, name)

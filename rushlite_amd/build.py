@@ -7,7 +7,10 @@ Outputs (all in-tree so they travel with the repository snapshot):
   oracle/liblamp_cpu_fast.so          CPU oracle with the reference's flags (AVX2 + FMA)
   oracle/liblamp_cpu_fast_v4.so       the same for AVX-512 hosts
 
-Run ``python -m rushlite_amd.build`` (or ``__graft_entry__.build()``).
+Run ``python rushlite_amd/build.py [all|hip|ext|oracle]`` from the repository
+root (or ``__graft_entry__.build()``).  It imports nothing from the package, so
+it also runs in a fresh checkout, where importing ``rushlite_amd`` (and with it
+``python -m rushlite_amd.build``) fails until the extension exists.
 """
 from __future__ import annotations
 
