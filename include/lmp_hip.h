@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define LMP_HIP_ABI_VERSION 8
+#define LMP_HIP_ABI_VERSION 9
 #define LMP_MAX_DIMS 16 /* align_utils.hpp:7 */
 /* Size of the fixed per-device workspace of lmp_k_gemm_f32_noalloc. */
 #define LMP_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
@@ -300,6 +300,22 @@ int lmp_k_gemm_colsum_masked_f32(int trans_a, size_t m, size_t n, size_t k,
                                  const float* a, size_t lda, const float* b,
                                  const float* mask, size_t ldb, float* c, size_t ldc,
                                  int accumulate, float* colsum, int colsum_accumulate);
+
+/* The three gradients of a Linear y = x * w + b (x [batch, in] with row
+ * stride ldx, w [in, out] with ldw) from its output gradient g [batch, out]
+ * (ldg): dx (+)= g * w^T [batch, in] (lddx), dw (+)= x^T * g [in, out] (lddw)
+ * and db (+)= the column sums of g [out]; each *_accumulate adds instead of
+ * writing.  The reference forms them by MatrixMultiplicationBackward and the
+ * broadcast add's sum (functions/matrix_ops.cpp:8-35, autograd/utils/
+ * grad_utils.cpp:10-36): two transposes, two matmuls and a reduction.  When
+ * both products fit the tiny GEMM's 16 x 16 blocks (K <= 512, at most 2^21
+ * multiply-adds, blocks of 32 x 32 short of a quarter of the CUs) they run as
+ * one launch; otherwise lmp_k_gemm_f32 (dx) then lmp_k_gemm_colsum_f32 (dw,
+ * db).  Either way the same bits as those two calls. */
+int lmp_k_linear_backward_f32(size_t batch, size_t in, size_t out, const float* x, size_t ldx,
+                              const float* w, size_t ldw, const float* g, size_t ldg,
+                              float* dx, size_t lddx, int dx_accumulate, float* dw,
+                              size_t lddw, int dw_accumulate, float* db, int db_accumulate);
 
 /* C = relu(op(A) * op(B) + bias): lmp_k_linear_f32 with ReLU applied in the
  * same epilogue, as the clamp functor computes clamp(t, 0, DBL_MAX) in float32

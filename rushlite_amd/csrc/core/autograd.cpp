@@ -165,18 +165,35 @@ void Variable::incr_grad_matmul(const Tensor& a, const Tensor& b, bool trans_a,
 }
 
 bool Variable::incr_grad_linear(Variable& w, Variable& b, const Tensor& x, const Tensor& g,
-                                const Tensor* relu_out) {
+                                const Tensor* relu_out, Variable* xv) {
   LMP_CHECK(w.requires_grad() && b.requires_grad())
       << "Cannot access grad() if requires_grad = false";
   const size_t n = g.shape().size() == 2 ? g.shape()[1] : 0;
   if (b.impl_->data.numel() != n || w.impl_->data.shape().size() != 2) return false;
-  Tensor wg = w.impl_->grad, bg = b.impl_->grad;
+  LMP_INTERNAL_ASSERT(!(xv && relu_out)) << "the input gradient is not formed with a mask";
+  // An input that is also the weight or the bias accumulates through the
+  // separate calls.
+  if (xv && (xv->impl_ == w.impl_ || xv->impl_ == b.impl_)) return false;
+  Tensor wg = w.impl_->grad, bg = b.impl_->grad, xg;
   // Accumulation is in place on realised buffers (their identity is kept).
   if (wg.defined()) wg.realize();
   if (bg.defined()) bg.realize();
-  const bool done = relu_out ? tops::matmul_colsum_masked(x, g, *relu_out, true, &wg, &bg)
-                             : tops::matmul_colsum(x, g, true, false, &wg, &bg);
+  if (xv) {
+    LMP_CHECK(xv->requires_grad()) << "Cannot access grad() if requires_grad = false";
+    xg = xv->impl_->grad;
+    if (xg.defined()) xg.realize();
+  }
+  const bool done = xv         ? tops::linear_backward(x, w.impl_->data, g, &xg, &wg, &bg)
+                    : relu_out ? tops::matmul_colsum_masked(x, g, *relu_out, true, &wg, &bg)
+                               : tops::matmul_colsum(x, g, true, false, &wg, &bg);
   if (!done) return false;
+  if (xv && !xv->impl_->grad.defined()) {
+    // g @ w^T accumulated from +0 equals 0 + the product exactly.
+    LMP_INTERNAL_ASSERT(xg.shape() == xv->impl_->data.shape())
+        << "There should be no broadcasting in incr_grad";
+    xv->impl_->grad = xg;
+    xv->impl_->grad_pass = t_backward_pass;
+  }
   if (!w.impl_->grad.defined()) {
     // A GEMM accumulates from +0, so its product equals 0 + product exactly;
     // the column sums start from +0 as well.
@@ -434,6 +451,10 @@ namespace {
 // matmul + broadcast add, layers/linear.cpp:21-26): dx = g w^T, and dw = x^T g
 // with db = the dim-0 sum of g in one launch where the backend has the form.
 void linear_backward(const Tensor& g, variable_list& in) {
+  // All three gradients in one call (one launch for small products).
+  if (in[0].requires_grad() && in[1].requires_grad() && in[2].requires_grad() &&
+      Variable::incr_grad_linear(in[1], in[2], in[0].data(), g, nullptr, &in[0]))
+    return;
   if (in[0].requires_grad()) in[0].incr_grad_matmul(g, in[1].data(), false, true);
   if (in[1].requires_grad() && in[2].requires_grad() &&
       Variable::incr_grad_linear(in[1], in[2], in[0].data(), g))

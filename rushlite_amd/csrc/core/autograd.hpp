@@ -69,9 +69,11 @@ class Variable {
   // b.grad += the column sums of g, in one launch where the backend has the
   // form (false, nothing done, otherwise).  With relu_out (a Linear -> ReLU
   // pair's output), g is first masked by ReLU's backward (g where
-  // 0 < relu_out < max, else 0) as the GEMM loads it.
+  // 0 < relu_out < max, else 0) as the GEMM loads it.  With xv (the variable
+  // whose data is x; not with relu_out), xv.grad += g @ w^T as well, all three
+  // in one launch where the products are small.
   static bool incr_grad_linear(Variable& w, Variable& b, const Tensor& x, const Tensor& g,
-                               const Tensor* relu_out = nullptr);
+                               const Tensor* relu_out = nullptr, Variable* xv = nullptr);
   void set_grad_fn(std::shared_ptr<Function> fn);
   void copy(const Variable& other);
   void fill(Scalar value);

@@ -346,6 +346,45 @@ void matmul_colsum_masked_hip(const TensorImpl& a, const TensorImpl& b, const Te
          "lmp_k_gemm_colsum_masked_f32");
 }
 
+// Whether lmp_k_linear_backward_f32 runs both products on the tiny GEMM's
+// 16 x 16 blocks in one launch (K <= 512, at most 2^21 multiply-adds, and
+// 32 x 32 blocks short of a quarter of the CUs), for the launch count.
+bool linear_backward_one_launch(size_t batch, size_t in, size_t out) {
+  static const int cu = [] {
+    lmp_rt_info info{};
+    return lmp_rt_device_info(&info) == LMP_OK ? int(info.cu_count) : 0;
+  }();
+  const auto tiny16 = [](size_t m, size_t n, size_t k) {
+    return k <= 512 && double(m) * double(n) * double(k) <= double(1 << 21) &&
+           double((m + 31) / 32) * double((n + 31) / 32) * 4 < double(cu);
+  };
+  return tiny16(in, out, batch) && tiny16(batch, in, out);
+}
+
+void linear_backward_hip(const TensorImpl& x, const TensorImpl& w, const TensorImpl& g,
+                         TensorImpl& dx, bool acc_dx, TensorImpl& dw, bool acc_dw,
+                         TensorImpl& db, bool acc_db) {
+  const size_t batch = x.shape()[0], in = x.shape()[1], out = w.shape()[1];
+  LMP_CHECK(dx.shape().size() == 2 && dx.shape()[0] == batch && dx.shape()[1] == in)
+      << "add_inplace requires tensors with identical shapes";
+  LMP_CHECK(dw.shape().size() == 2 && dw.shape()[0] == in && dw.shape()[1] == out)
+      << "add_inplace requires tensors with identical shapes";
+  LMP_CHECK(db.numel() == out) << "add_inplace requires tensors with identical shapes";
+  HostTimer timer(&backend_stats().gemm_host_ns);
+  const void* px = mut(x);
+  const void* pw = mut(w);
+  const void* pg = mut(g);
+  count_launch();
+  if (!linear_backward_one_launch(batch, in, out)) count_launch();
+  hip_ok(lmp_k_linear_backward_f32(batch, in, out, static_cast<const float*>(px), in,
+                                   static_cast<const float*>(pw), out,
+                                   static_cast<const float*>(pg), out,
+                                   static_cast<float*>(dx.data()), in, acc_dx ? 1 : 0,
+                                   static_cast<float*>(dw.data()), out, acc_dw ? 1 : 0,
+                                   static_cast<float*>(db.data()), acc_db ? 1 : 0),
+         "lmp_k_linear_backward_f32");
+}
+
 TensorImpl linear_hip(const TensorImpl& x, const TensorImpl& w, const TensorImpl& b,
                       bool relu) {
   const GemmShape s = gemm_shape(x, w, false, false);
@@ -443,6 +482,7 @@ LMP_REGISTER_DISPATCH(matmul_acc_stub, kHip, matmul_acc_hip)
 LMP_REGISTER_DISPATCH(linear_stub, kHip, linear_hip)
 LMP_REGISTER_DISPATCH(matmul_colsum_stub, kHip, matmul_colsum_hip)
 LMP_REGISTER_DISPATCH(matmul_colsum_masked_stub, kHip, matmul_colsum_masked_hip)
+LMP_REGISTER_DISPATCH(linear_backward_stub, kHip, linear_backward_hip)
 LMP_REGISTER_DISPATCH(transpose_stub, kHip, transpose_hip)
 
 }  // namespace lmp::tensor::hip

@@ -34,6 +34,7 @@ LMP_DEFINE_DISPATCH(matmul_acc_fn, matmul_acc_stub)
 LMP_DEFINE_DISPATCH(linear_fn, linear_stub)
 LMP_DEFINE_DISPATCH(matmul_colsum_fn, matmul_colsum_stub)
 LMP_DEFINE_DISPATCH(matmul_colsum_masked_fn, matmul_colsum_masked_stub)
+LMP_DEFINE_DISPATCH(linear_backward_fn, linear_backward_stub)
 
 namespace {
 using Acc = detail::UnsafeTensorAccessor;
@@ -256,6 +257,33 @@ bool matmul_colsum_masked(const Tensor& a, const Tensor& b, const Tensor& mask, 
   if (!acc_s) *s = wrap(TensorImpl(Storage(n * sizeof(float), dev), {n}, DataType::Float32));
   matmul_colsum_masked_stub()(dev, *Acc::getImpl(a), *Acc::getImpl(b), *Acc::getImpl(mask),
                               trans_a, *Acc::getImpl(*c), acc_c, *Acc::getImpl(*s), acc_s);
+  return true;
+}
+
+bool linear_backward(const Tensor& x, const Tensor& w, const Tensor& g, Tensor* dx, Tensor* dw,
+                     Tensor* db) {
+  const DeviceType dev = g.device();
+  if (!linear_backward_stub().has(dev) || x.device() != dev || w.device() != dev) return false;
+  const auto f32 = [](const Tensor& t) { return t.type() == DataType::Float32; };
+  if (!f32(x) || !f32(w) || !f32(g) || x.shape().size() != 2 || w.shape().size() != 2 ||
+      g.shape().size() != 2)
+    return false;
+  const size_t batch = x.shape()[0], in = x.shape()[1], out = w.shape()[1];
+  if (w.shape()[0] != in || g.shape()[0] != batch || g.shape()[1] != out) return false;
+  // An empty batch or layer takes the unfused path (zero products, empty sums).
+  if (batch == 0 || in == 0 || out == 0) return false;
+  for (const Tensor* t : {dx, dw, db})
+    if (t->defined() && (!f32(*t) || t->device() != dev)) return false;
+  const bool acc_dx = dx->defined(), acc_dw = dw->defined(), acc_db = db->defined();
+  if (!acc_dx)
+    *dx = wrap(TensorImpl(Storage(batch * in * sizeof(float), dev), {batch, in},
+                          DataType::Float32));
+  if (!acc_dw)
+    *dw = wrap(TensorImpl(Storage(in * out * sizeof(float), dev), {in, out}, DataType::Float32));
+  if (!acc_db) *db = wrap(TensorImpl(Storage(out * sizeof(float), dev), {out}, DataType::Float32));
+  linear_backward_stub()(dev, *Acc::getImpl(x), *Acc::getImpl(w), *Acc::getImpl(g),
+                         *Acc::getImpl(*dx), acc_dx, *Acc::getImpl(*dw), acc_dw,
+                         *Acc::getImpl(*db), acc_db);
   return true;
 }
 

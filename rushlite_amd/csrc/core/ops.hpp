@@ -83,6 +83,14 @@ using matmul_colsum_masked_fn = void (*)(const TensorImpl& a, const TensorImpl& 
                                          const TensorImpl& mask, bool ta, TensorImpl& c,
                                          bool acc_c, TensorImpl& s, bool acc_s);
 
+// A Linear's three gradients from its output gradient g [batch, out], input
+// x [batch, in] and weight w [in, out]: dx (+)= g w^T, dw (+)= x^T g and
+// db (+)= the column sums of g (accumulate when acc_*).  Float32 2-D operands
+// only.
+using linear_backward_fn = void (*)(const TensorImpl& x, const TensorImpl& w,
+                                    const TensorImpl& g, TensorImpl& dx, bool acc_dx,
+                                    TensorImpl& dw, bool acc_dw, TensorImpl& db, bool acc_db);
+
 #define LMP_FOR_BINARY_OPS(_) \
   _(add) _(sub) _(mul) _(div) _(pow) _(eq) _(ne) _(ge) _(le) _(gt) _(lt)
 #define LMP_FOR_UNARY_OPS(_) _(neg) _(exp) _(log) _(sqrt) _(abs) _(sin) _(cos) _(tan)
@@ -115,6 +123,7 @@ LMP_DECLARE_DISPATCH(matmul_acc_fn, matmul_acc_stub)
 LMP_DECLARE_DISPATCH(linear_fn, linear_stub)
 LMP_DECLARE_DISPATCH(matmul_colsum_fn, matmul_colsum_stub)
 LMP_DECLARE_DISPATCH(matmul_colsum_masked_fn, matmul_colsum_masked_stub)
+LMP_DECLARE_DISPATCH(linear_backward_fn, linear_backward_stub)
 
 Tensor clamp(const Tensor& a, Scalar lo, Scalar hi);
 Tensor abs_backward(const Tensor& input, const Tensor& grad);
@@ -136,6 +145,12 @@ bool matmul_colsum(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b,
 // ReLU output, b's shape): *c (+)= op(a) @ b' and *s (+)= column sums of b'.
 bool matmul_colsum_masked(const Tensor& a, const Tensor& b, const Tensor& mask, bool trans_a,
                           Tensor* c, Tensor* s);
+// A Linear's gradients: *dx (+)= g @ w^T, *dw (+)= x^T @ g and *db (+)= the
+// column sums of g; an undefined output is allocated and written.  Returns
+// false (and does nothing) where the device has no such form, the dtypes are
+// not float32 or the batch is empty.
+bool linear_backward(const Tensor& x, const Tensor& w, const Tensor& g, Tensor* dx, Tensor* dw,
+                     Tensor* db);
 Tensor transpose(const Tensor& a);
 Tensor reshape(const Tensor& a, std::vector<size_t> shape);
 Tensor squeeze(const Tensor& a, size_t dim);

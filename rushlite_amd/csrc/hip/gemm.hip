@@ -668,8 +668,11 @@ struct TinyMma<16> {
   __device__ __forceinline__ static int row(int r, int q) { return q * 4 + r; }
 };
 
-template <int BS, bool TA, bool TB, bool VA, bool VB, bool MB = false>
-__global__ __launch_bounds__(256) void gemm_tiny(GemmArgs g) {
+// One BS x BS block (bx, by) of C = op(A) op(B) by the tiny kernel's four
+// waves; red holds 4 * TinyMma<BS>::kRegs * 64 floats, red_cs 4 * 64.
+template <int BS, bool TA, bool TB, bool VA, bool VB, bool MB>
+__device__ __forceinline__ void tiny_block(const GemmArgs& g, int bx, int by, float* red,
+                                           float* red_cs) {
   static_assert(!MB || !TB, "the B mask is for B untransposed");
   using M = TinyMma<BS>;
   constexpr int G = 4 * (64 / BS);              // k values per group
@@ -677,7 +680,7 @@ __global__ __launch_bounds__(256) void gemm_tiny(GemmArgs g) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int li = lane % BS, q = lane / BS;
-  const int m0 = int(blockIdx.x) * BS, n0 = int(blockIdx.y) * BS;
+  const int m0 = bx * BS, n0 = by * BS;
   const int groups = (g.k + G - 1) / G;
   const int per = (groups + 3) / 4;
   const int j0 = min(groups, wave * per), j1 = min(groups, j0 + per);
@@ -725,8 +728,7 @@ __global__ __launch_bounds__(256) void gemm_tiny(GemmArgs g) {
   // gradient): the first row of blocks adds the B values its lanes already
   // hold -- each lane its k values in order, then the lane parts and the
   // waves in order through LDS.  Sums start from +0, so -0.0 never appears.
-  const bool colsum = g.colsum != nullptr && blockIdx.x == 0;
-  __shared__ float red_cs[4 * 64];
+  const bool colsum = g.colsum != nullptr && bx == 0;
   if (colsum) {
     float cs = 0.0f;
 #pragma unroll
@@ -738,7 +740,6 @@ __global__ __launch_bounds__(256) void gemm_tiny(GemmArgs g) {
   }
   // Blocks of the four waves summed in wave order: [wave][r][lane].
   constexpr int R = M::kRegs;
-  __shared__ float red[4 * R * 64];
 #pragma unroll
   for (int r = 0; r < R; ++r) red[(wave * R + r) * 64 + lane] = acc[r];
   __syncthreads();
@@ -763,6 +764,33 @@ __global__ __launch_bounds__(256) void gemm_tiny(GemmArgs g) {
     float* o = g.c + int64_t(orow) * g.ldc + ocol;
     if (g.accumulate) *o = *o + v;
     else *o = g.bias ? lin_epi(v, g.bias[ocol], g.relu) : v;
+  }
+}
+
+template <int BS, bool TA, bool TB, bool VA, bool VB, bool MB = false>
+__global__ __launch_bounds__(256) void gemm_tiny(GemmArgs g) {
+  __shared__ float red[4 * TinyMma<BS>::kRegs * 64];
+  __shared__ float red_cs[4 * 64];
+  tiny_block<BS, TA, TB, VA, VB, MB>(g, int(blockIdx.x), int(blockIdx.y), red, red_cs);
+}
+
+// A Linear's three gradients in one launch, on 16 x 16 blocks: workgroups
+// below wblocks take a block of dW = X^T G (A = X stored [batch, in]) with the
+// column sums of G as db; the rest a block of dX = G W^T (B = W stored
+// [in, out]).  Each block is the tiny kernel's, so every output has the bits
+// of the two separate launches.
+template <bool VA, bool VB>
+__global__ __launch_bounds__(256) void gemm_tiny_linear_backward(GemmArgs gw, GemmArgs gx,
+                                                                 int wblocks_m, int wblocks) {
+  __shared__ float red[4 * TinyMma<16>::kRegs * 64];
+  __shared__ float red_cs[4 * 64];
+  const int b = int(blockIdx.x);
+  if (b < wblocks) {
+    tiny_block<16, true, false, false, false, false>(gw, b % wblocks_m, b / wblocks_m, red,
+                                                      red_cs);
+  } else {
+    const int t = b - wblocks, xm = (gx.m + 15) / 16;
+    tiny_block<16, false, true, VA, VB, false>(gx, t % xm, t / xm, red, red_cs);
   }
 }
 
@@ -811,6 +839,37 @@ int launch_tiny(Runtime* rt, const GemmArgs& g) {
   if (blocks32 * 4 >= rt->cu_count) launch_tiny_bs<32, TA, TB>(rt, g, va, vb);
   else launch_tiny_bs<16, TA, TB>(rt, g, va, vb);
   LMP_LAUNCH_CHECK("gemm_tiny");
+  return LMP_OK;
+}
+
+// Whether launch_tiny would run g on 16 x 16 blocks.
+bool tiny16(const Runtime* rt, const GemmArgs& g) {
+  const int64_t blocks32 = int64_t((g.m + 31) / 32) * ((g.n + 31) / 32);
+  return tiny_ok(g) && blocks32 * 4 < rt->cu_count;
+}
+
+// gw: dW = X^T G with db (launch_tiny<true, false>); gx: dX = G W^T
+// (launch_tiny<false, true>), both on 16 x 16 blocks, in one grid.
+int launch_tiny_linear_backward(Runtime* rt, const GemmArgs& gw, const GemmArgs& gx) {
+  const bool k4 = gx.k % 4 == 0;
+  const bool va = k4 && gx.lda % 4 == 0 && aligned16(gx.a);
+  const bool vb = k4 && gx.ldb % 4 == 0 && aligned16(gx.b);
+  const int wm = (gw.m + 15) / 16, wblocks = wm * ((gw.n + 15) / 16);
+  const int xblocks = ((gx.m + 15) / 16) * ((gx.n + 15) / 16);
+  const dim3 grid{uint32_t(wblocks + xblocks)};
+  if (va && vb)
+    hipLaunchKernelGGL((gemm_tiny_linear_backward<true, true>), grid, dim3(256), 0, rt->stream,
+                       gw, gx, wm, wblocks);
+  else if (va)
+    hipLaunchKernelGGL((gemm_tiny_linear_backward<true, false>), grid, dim3(256), 0, rt->stream,
+                       gw, gx, wm, wblocks);
+  else if (vb)
+    hipLaunchKernelGGL((gemm_tiny_linear_backward<false, true>), grid, dim3(256), 0, rt->stream,
+                       gw, gx, wm, wblocks);
+  else
+    hipLaunchKernelGGL((gemm_tiny_linear_backward<false, false>), grid, dim3(256), 0,
+                       rt->stream, gw, gx, wm, wblocks);
+  LMP_LAUNCH_CHECK("gemm_tiny_linear_backward");
   return LMP_OK;
 }
 
@@ -1943,6 +2002,54 @@ extern "C" int lmp_k_gemm_colsum_masked_f32(int trans_a, size_t m, size_t n, siz
                                colsum_accumulate);
   scratch_free(gm);  // stream-ordered: the GEMM reads it first
   return rc;
+}
+
+extern "C" int lmp_k_linear_backward_f32(size_t batch, size_t in, size_t out, const float* x,
+                                         size_t ldx, const float* w, size_t ldw, const float* g,
+                                         size_t ldg, float* dx, size_t lddx, int dx_accumulate,
+                                         float* dw, size_t lddw, int dw_accumulate, float* db,
+                                         int db_accumulate) {
+  if (!dx || !dw || !db) return fail(LMP_ERR_INVALID, "linear_backward: null output");
+  if (batch == 0 || in == 0 || out == 0 || !x || !w || !g)
+    return fail(LMP_ERR_UNSUPPORTED, "linear_backward: empty or null operand");
+  const size_t lim = 0x7fffffff;
+  if (batch > lim || in > lim || out > lim || ldx > lim || ldw > lim || ldg > lim ||
+      lddx > lim || lddw > lim)
+    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension above 2^31");
+  if (ldx < in || ldw < out || ldg < out || lddx < in || lddw < out)
+    return fail(LMP_ERR_INVALID, "gemm: leading dimension too small");
+  // dW [in, out] = X^T G over the batch, with db beside it.
+  GemmArgs gw{};
+  gw.a = x;
+  gw.b = g;
+  gw.c = dw;
+  gw.m = int(in);
+  gw.n = int(out);
+  gw.k = int(batch);
+  gw.lda = int(ldx);
+  gw.ldb = int(ldg);
+  gw.ldc = int(lddw);
+  gw.accumulate = dw_accumulate ? 1 : 0;
+  gw.colsum = db;
+  gw.colsum_acc = db_accumulate ? 1 : 0;
+  // dX [batch, in] = G W^T over the outputs.
+  GemmArgs gx{};
+  gx.a = g;
+  gx.b = w;
+  gx.c = dx;
+  gx.m = int(batch);
+  gx.n = int(in);
+  gx.k = int(out);
+  gx.lda = int(ldg);
+  gx.ldb = int(ldw);
+  gx.ldc = int(lddx);
+  gx.accumulate = dx_accumulate ? 1 : 0;
+  LMP_RUNTIME_OR_FAIL(rt);
+  if (tiny16(rt, gw) && tiny16(rt, gx)) return launch_tiny_linear_backward(rt, gw, gx);
+  const int rc = lmp_k_gemm_f32(0, 1, batch, in, out, g, ldg, w, ldw, dx, lddx, dx_accumulate);
+  if (rc != LMP_OK) return rc;
+  return lmp_k_gemm_colsum_f32(1, 0, in, out, batch, x, ldx, g, ldg, dw, lddw, dw_accumulate,
+                               db, db_accumulate);
 }
 
 extern "C" int lmp_k_linear_relu_f32(int trans_a, int trans_b, size_t m, size_t n,

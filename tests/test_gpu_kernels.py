@@ -612,6 +612,51 @@ def test_host_device_round_trip_every_byte(hip, nbytes):
     assert part.view(np.uint32).tobytes() == words.tobytes()
 
 
+# (batch, in, out): the README MLP's two layers, odd and single-row sizes in
+# the one-launch range, then a product just past it (K > 512) and config 4's
+# last layer, which take the two separate launches.
+@pytest.mark.parametrize("batch,fan_in,fan_out", [
+    (32, 64, 10), (32, 256, 64), (7, 33, 5), (1, 3, 1), (40, 17, 600), (512, 4096, 1000)],
+    ids=str)
+@pytest.mark.parametrize("acc", [False, True], ids=["write", "accumulate"])
+def test_linear_backward_equals_separate_calls(hip, batch, fan_in, fan_out, acc):
+    """lmp_k_linear_backward_f32 (dX = G W^T, dW = X^T G and db = the column
+    sums of G, one launch for small products) equals lmp_k_gemm_f32 for dX
+    and lmp_k_gemm_colsum_f32 for dW and db bit for bit, writing and
+    accumulating; and dW is X^T G against float64 on the host."""
+    L = hip.lib()
+    rng = np.random.default_rng(batch * 7 + fan_in * 3 + fan_out)
+    x_np = rng.standard_normal((batch, fan_in)).astype(np.float32)
+    w_np = rng.standard_normal((fan_in, fan_out)).astype(np.float32)
+    g_np = rng.standard_normal((batch, fan_out)).astype(np.float32)
+    g_np.reshape(-1)[3::41] = -0.0
+    dx0 = rng.standard_normal((batch, fan_in)).astype(np.float32)
+    dw0 = rng.standard_normal((fan_in, fan_out)).astype(np.float32)
+    db0 = rng.standard_normal(fan_out).astype(np.float32)
+    x, w, g = up(hip, x_np), up(hip, w_np), up(hip, g_np)
+    dx_ref, dw_ref, db_ref = up(hip, dx0), up(hip, dw0), up(hip, db0)
+    hip.check(L.lmp_k_gemm_f32(0, 1, batch, fan_in, fan_out, g.ptr, fan_out, w.ptr, fan_out,
+                               dx_ref.ptr, fan_in, int(acc)))
+    hip.check(L.lmp_k_gemm_colsum_f32(1, 0, fan_in, fan_out, batch, x.ptr, fan_in, g.ptr,
+                                      fan_out, dw_ref.ptr, fan_out, int(acc), db_ref.ptr,
+                                      int(acc)))
+    dx, dw, db = up(hip, dx0), up(hip, dw0), up(hip, db0)
+    hip.check(L.lmp_k_linear_backward_f32(batch, fan_in, fan_out, x.ptr, fan_in, w.ptr, fan_out,
+                                          g.ptr, fan_out, dx.ptr, fan_in, int(acc), dw.ptr,
+                                          fan_out, int(acc), db.ptr, int(acc)))
+    for got, ref in ((dx, dx_ref), (dw, dw_ref), (db, db_ref)):
+        assert np.array_equal(got.numpy().view(np.uint32), ref.numpy().view(np.uint32))
+    want = x_np.T.astype(np.float64) @ g_np.astype(np.float64) + (dw0 if acc else 0.0)
+    assert rel_err(dw.numpy(), want) <= 1e-5
+    # null outputs are rejected, an empty batch is unsupported
+    assert L.lmp_k_linear_backward_f32(batch, fan_in, fan_out, x.ptr, fan_in, w.ptr, fan_out,
+                                       g.ptr, fan_out, None, fan_in, 0, dw.ptr, fan_out, 0,
+                                       db.ptr, 0) == hip.ERR_INVALID
+    assert L.lmp_k_linear_backward_f32(0, fan_in, fan_out, x.ptr, fan_in, w.ptr, fan_out,
+                                       g.ptr, fan_out, dx.ptr, fan_in, 0, dw.ptr, fan_out, 0,
+                                       db.ptr, 0) == hip.ERR_UNSUPPORTED
+
+
 @pytest.mark.parametrize("m,n,k,ta,ldb_pad", [
     (256, 64, 32, 1, 0), (64, 10, 32, 1, 0), (5, 7, 3, 1, 0), (96, 40, 17, 0, 0),
     (64, 33, 20, 1, 3), (4096, 1000, 512, 1, 0), (300, 260, 600, 1, 4)], ids=str)

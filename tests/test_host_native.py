@@ -28,10 +28,11 @@ def declared_functions():
 
 def test_header_declares_the_abi():
     names = declared_functions()
-    assert len(names) == 42
+    assert len(names) == 43
     for group in ("lmp_rt_malloc", "lmp_k_binary", "lmp_k_reduce", "lmp_k_gemm_f32",
                   "lmp_jit_compile", "lmp_rt_graph_begin", "lmp_rt_graph_launch",
-                  "lmp_k_gemm_f32_noalloc", "lmp_k_gemm_colsum_masked_f32"):
+                  "lmp_k_gemm_f32_noalloc", "lmp_k_gemm_colsum_masked_f32",
+                  "lmp_k_linear_backward_f32"):
         assert group in names
 
 
@@ -42,7 +43,7 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     assert set(declared_functions()) == set(abi.SIGNATURES)
     abi.lib()  # argtypes/restype binding succeeds for every entry
-    assert abi.lib().lmp_rt_abi_version() == 8
+    assert abi.lib().lmp_rt_abi_version() == 9
 
 
 @pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
