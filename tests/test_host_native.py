@@ -10,6 +10,7 @@
 import ctypes
 import re
 import shutil
+import sys
 import subprocess
 from pathlib import Path
 
@@ -44,6 +45,26 @@ def test_library_exports_every_declared_symbol():
     assert set(declared_functions()) == set(abi.SIGNATURES)
     abi.lib()  # argtypes/restype binding succeeds for every entry
     assert abi.lib().lmp_rt_abi_version() == 9
+
+
+def test_build_recipe_imports_nothing_from_the_package():
+    """rushlite_amd/build.py must run in a fresh checkout, where importing the
+    package fails until the extension it builds exists: it imports nothing
+    from the package, and __graft_entry__.build() loads it by path."""
+    import ast
+    tree = ast.parse((ROOT / "rushlite_amd" / "build.py").read_text())
+    mods = set()
+    for node in ast.walk(tree):
+        if isinstance(node, ast.Import):
+            mods.update(a.name.split(".")[0] for a in node.names)
+        elif isinstance(node, ast.ImportFrom):
+            assert node.level == 0, "relative import in build.py"
+            mods.add((node.module or "").split(".")[0])
+    assert "rushlite_amd" not in mods and "oracle" not in mods
+    # beyond the standard library only the binding generator's include paths
+    assert mods - set(sys.stdlib_module_names) <= {"pybind11"}
+    entry = (ROOT / "__graft_entry__.py").read_text()
+    assert "spec_from_file_location" in entry and "from rushlite_amd import build" not in entry
 
 
 @pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
