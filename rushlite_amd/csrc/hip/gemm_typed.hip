@@ -102,66 +102,6 @@ constexpr int kLds = kBK * (kTile + 1);
 
 // ------------------------------------------------------------------ float64
 
-template <bool TA, bool TB>
-__global__ __launch_bounds__(kThreads) void gemm_f64_mfma(TypedArgs g) {
-  __shared__ double smem[2][2][kLds];  // [buffer][A|B]
-  const int tiles_n = (g.n + kTile - 1) / kTile;
-  const int m0 = int(blockIdx.x / tiles_n) * kTile, n0 = int(blockIdx.x % tiles_n) * kTile;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int li = lane & 15, lk = lane >> 4;
-
-  v4d acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v4d{0.0, 0.0, 0.0, 0.0};
-
-  TileLoader<double, TA, TB, kPer> ld;
-  const int k_tiles = (g.k + kBK - 1) / kBK;
-  ld.load(g, m0, n0, 0);
-  ld.store(smem[0][0], smem[0][1]);
-  __syncthreads();
-  for (int kt = 0; kt < k_tiles; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < k_tiles;
-    if (more) ld.load(g, m0, n0, (kt + 1) * kBK);
-    const double* As = smem[cur][0];
-    const double* Bs = smem[cur][1];
-#pragma unroll
-    for (int s = 0; s < kBK / 4; ++s) {
-      const int kk = 4 * s + lk;
-      double af[2], bf[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = As[kk * (kTile + 1) + wm * 32 + i * 16 + li];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = Bs[kk * (kTile + 1) + wn * 32 + j * 16 + li];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    if (more) ld.store(smem[cur ^ 1][0], smem[cur ^ 1][1]);
-    __syncthreads();
-  }
-
-  double* C = static_cast<double*>(g.c);
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + wn * 32 + j * 16 + li;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * 32 + i * 16 + 4 * r + lk;
-        if (row < g.m && col < g.n) {
-          double* p = C + int64_t(row) * g.ldc + col;
-          *p = g.accumulate ? *p + acc[i][j][r] : acc[i][j][r];
-        }
-      }
-    }
-}
 
 // float64, large products: 128 x 128 tiles of 4 waves, each wave 64 x 64 =
 // 4 x 4 blocks of 16 x 16.  Per K step of 16 a workgroup moves 32 KiB from
@@ -182,15 +122,15 @@ __global__ __launch_bounds__(kThreads) void gemm_f64_mfma(TypedArgs g) {
 // fill the same LDS tile, so every path gives the same bits.
 constexpr int kBig = 128, kBigPitch = kBig + 1;
 
-// One operand's share of a [128 x 16] tile.  Pair q of thread tid is
+// One operand's share of a [TILE x 16] tile.  Pair q of thread tid is
 // p = tid + 256 q.  KC (the stored matrix is contiguous along k): row
 // r = p / 8 of the m (or n) extent and k offset c = 2 (p % 8); otherwise k
-// row r = p / 64 and m (or n) offset c = 2 (p % 64).  In LDS the tile is
-// [k][m or n] with pitch kBigPitch.
-template <bool KC>
+// row r = p / (TILE / 2) and m (or n) offset c = 2 (p % (TILE / 2)).  In LDS
+// the tile is [k][m or n] with row pitch PITCH.
+template <bool KC, int TILE = kBig, int PITCH = kBigPitch>
 struct PairOperand {
-  static constexpr int kPairs = kBig * kBK / 2 / kThreads;  // 4
-  static constexpr int kRowPairs = KC ? kBK / 2 : kBig / 2;
+  static constexpr int kPairs = TILE * kBK / 2 / kThreads;  // 4 (128-wide tiles), 2 (64)
+  static constexpr int kRowPairs = KC ? kBK / 2 : TILE / 2;
   v2d v[kPairs];
   const double* at[kPairs];  // pair start at k0 = 0, for tiles inside the matrix
 
@@ -229,11 +169,11 @@ struct PairOperand {
     for (int q = 0; q < kPairs; ++q) {
       const int p = tid + kThreads * q, r = p / kRowPairs, c = 2 * (p % kRowPairs);
       if constexpr (KC) {
-        S[c * kBigPitch + r] = v[q].x;
-        S[(c + 1) * kBigPitch + r] = v[q].y;
+        S[c * PITCH + r] = v[q].x;
+        S[(c + 1) * PITCH + r] = v[q].y;
       } else {
-        S[r * kBigPitch + c] = v[q].x;
-        S[r * kBigPitch + c + 1] = v[q].y;
+        S[r * PITCH + c] = v[q].x;
+        S[r * PITCH + c + 1] = v[q].y;
       }
     }
   }
@@ -264,6 +204,121 @@ __device__ __forceinline__ void f64_step_schedule() {
     __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
   }
+}
+
+// float64 on 64 x 64 tiles of 4 waves, each wave 2 x 2 blocks of 16 x 16, for
+// products whose 128 x 128 tiles do not cover the CUs.  Loads as in
+// gemm_f64_big (pairs of the [64 x 16] panels, unchecked for aligned tiles
+// inside C, checked otherwise, the same LDS tile either way); each unchecked
+// K step puts the 4 loads of the next tile one per MFMA at its start and the
+// LDS stores one per MFMA among its last MFMAs.  Measured against its
+// element-wise checked loads: 1024^3 71-77 -> 60-64 us, 1536^3 206-214 ->
+// 176-191 us (three orientations each).
+template <bool TA, bool TB>
+__global__ __launch_bounds__(kThreads) void gemm_f64_mfma(TypedArgs g) {
+  __shared__ double smem[2][2][kLds];  // [buffer][A|B], each [k][m or n], pitch kTile + 1
+  const int tiles_n = (g.n + kTile - 1) / kTile;
+  const int m0 = int(blockIdx.x / tiles_n) * kTile, n0 = int(blockIdx.x % tiles_n) * kTile;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 15, lk = lane >> 4;
+  const double* A = static_cast<const double*>(g.a);
+  const double* B = static_cast<const double*>(g.b);
+  PairOperand<!TA, kTile, kTile + 1> pa;
+  PairOperand<TB, kTile, kTile + 1> pb;
+  pa.init(A, g.lda, m0, tid);
+  pb.init(B, g.ldb, n0, tid);
+  const bool inside = g.vec && m0 + kTile <= g.m && n0 + kTile <= g.n && g.k >= kBK;
+  auto load_checked = [&](int k0) {
+    pa.load_checked(A, g.lda, m0, g.m, k0, g.k, tid);
+    pb.load_checked(B, g.ldb, n0, g.n, k0, g.k, tid);
+  };
+  auto store = [&](int buf) {
+    pa.store(smem[buf][0], tid);
+    pb.store(smem[buf][1], tid);
+  };
+
+  v4d acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v4d{0.0, 0.0, 0.0, 0.0};
+  auto compute = [&](int cur) {
+    const double* As = smem[cur][0];
+    const double* Bs = smem[cur][1];
+#pragma unroll
+    for (int s = 0; s < kBK / 4; ++s) {
+      const int kk = 4 * s + lk;
+      double af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = As[kk * (kTile + 1) + wm * 32 + i * 16 + li];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = Bs[kk * (kTile + 1) + wn * 32 + j * 16 + li];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  const int k_tiles = (g.k + kBK - 1) / kBK;
+  // Steps kt < unchecked_end load tile kt + 1, which lies wholly inside K.
+  const int unchecked_end = inside ? g.k / kBK - 1 : 0;
+  if (inside) {
+    pa.load_unchecked(0, g.lda);
+    pb.load_unchecked(0, g.ldb);
+  } else {
+    load_checked(0);
+  }
+  store(0);
+  __syncthreads();
+  int kt = 0;
+  for (; kt < unchecked_end; ++kt) {
+    const int cur = kt & 1;
+    pa.load_unchecked((kt + 1) * kBK, g.lda);
+    pb.load_unchecked((kt + 1) * kBK, g.ldb);
+    compute(cur);
+    store(cur ^ 1);
+    // masks: 0x8 MFMA, 0x20 global load, 0x100 LDS read, 0x200 LDS write
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    __syncthreads();
+  }
+  for (; kt < k_tiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < k_tiles;
+    if (more) load_checked((kt + 1) * kBK);
+    compute(cur);
+    if (more) store(cur ^ 1);
+    __syncthreads();
+  }
+
+  double* C = static_cast<double*>(g.c);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + wn * 32 + j * 16 + li;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 32 + i * 16 + 4 * r + lk;
+        if (row < g.m && col < g.n) {
+          double* p = C + int64_t(row) * g.ldc + col;
+          *p = g.accumulate ? *p + acc[i][j][r] : acc[i][j][r];
+        }
+      }
+    }
 }
 
 template <bool TA, bool TB>

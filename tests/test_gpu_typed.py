@@ -214,12 +214,14 @@ def _up_offset(hip, arr):
     return buf, buf.ptr + 8, cols + 1
 
 
-# The large-tile kernel loads 16-byte pairs without bounds checks for tiles
-# inside C when both operands are 16-byte aligned with even leading
-# dimensions, and checked pairs otherwise.  Both fill the same LDS tile, so the
-# same random product through operands one double off alignment with odd
-# leading dimensions gives the same bits.
-@pytest.mark.parametrize("m,n,k", [(2048, 2048, 200), (2180, 1990, 96)], ids=str)
+# Both float64 kernels (128 x 128 tiles once those cover the CUs, 64 x 64
+# below) load 16-byte pairs without bounds checks for tiles inside C when both
+# operands are 16-byte aligned with even leading dimensions, and checked pairs
+# otherwise.  Both fill the same LDS tile, so the same random product through
+# operands one double off alignment with odd leading dimensions gives the same
+# bits.
+@pytest.mark.parametrize("m,n,k", [(2048, 2048, 200), (2180, 1990, 96), (1000, 1030, 96),
+                                   (200, 130, 50)], ids=str)
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_gemm_float64_large_tiles_unaligned_same_bits(hip, m, n, k, ta, tb):
     rng = np.random.default_rng(5 * m + n + 3 * k + 17 * ta + 19 * tb)
