@@ -409,6 +409,17 @@ def extras(rsl, abi, a_list, b, steps, warmup, only=None):
         flop = 2.0 * n ** 3
         out["gemm_f64_4096"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(flop / ms / 1e9, 1),
                                 "frac_of_fp64_peak": round(flop / ms / 1e9 / FP64_MFMA_PEAK_TFLOPS, 3)}
+        # 1024^3: too few 128 x 128 tiles to cover the CUs, so the 64 x 64 kernel
+        m = 1024
+
+        def run64s():
+            abi.check(L.lmp_k_gemm(abi.FLOAT64, 0, 0, m, m, m, A64.ptr, n, B64.ptr, n, C64.ptr, n, 0))
+        ms = time_steps(abi, run64s, 20, 3) / 20
+        flop = 2.0 * m ** 3
+        out["gemm_f64_1024"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(flop / ms / 1e9, 1),
+                                "frac_of_fp64_peak": round(flop / ms / 1e9 / FP64_MFMA_PEAK_TFLOPS, 3),
+                                "note": "the top-left 1024 x 1024 blocks of the 4096 x 4096 operands "
+                                        "(leading dimension 4096), on the 64 x 64-tile kernel"}
         del A64, B64, C64
 
     if want("mlp"):
