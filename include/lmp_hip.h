@@ -244,8 +244,11 @@ int lmp_k_gemm_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
 
 /* lmp_k_gemm_f32 without allocation.  No counterpart in the reference: it is
  * for callers that cannot allocate device memory -- code under HIP graph
- * capture on streams of their own, tight serving loops, harnesses that forbid
- * hipMalloc.  Same arguments, kernels and results (bit for bit) as
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Like every
+ * kernel entry point it launches on the library stream (lmp_rt_stream()): a
+ * capture records it when that stream is captured, by lmp_rt_graph_begin or
+ * by a caller that makes the library stream wait on an event recorded in its
+ * own capturing stream and joins back the same way.  Same arguments, kernels and results (bit for bit) as
  * lmp_k_gemm_f32; the split-K partials of products that split K go to a
  * fixed workspace of LMP_NOALLOC_SCRATCH_BYTES (a device array, one copy per
  * device, reserved when the library's code object loads there and held until
@@ -275,10 +278,14 @@ int lmp_k_linear_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
  * together.  LinearBackward in the reference computes them apart: the bias
  * through AddBackward's grad-of-broadcast reduction (grad_utils.cpp:10-36)
  * and the weight through transpose + matmul (functions/matrix_ops.cpp:15-20).
- * Small products (K <= 512, at most 2^21 multiply-adds) take one launch, the
- * column sums formed from the B fragments the GEMM already loads; larger ones
- * run the GEMM and then the dim-0 reduction (B must then be contiguous).
- * accumulate / colsum_accumulate add into C / colsum instead of writing. */
+ * The column sums ride in the GEMM's own launch on the tiny kernel (K <= 512,
+ * at most 2^21 multiply-adds), on the LDS tiles when B is untransposed and K
+ * is not split, and on the short-K kernel (A transposed, K <= 32); otherwise
+ * a second launch forms them after the GEMM (the dim-0 reduction for a
+ * contiguous B, a strided column sum for any ldb).  Anything the second launch
+ * needs is reserved before the first, so an error return leaves C and colsum
+ * unchanged.  accumulate / colsum_accumulate add into C / colsum instead of
+ * writing. */
 int lmp_k_gemm_colsum_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
                           const float* a, size_t lda, const float* b, size_t ldb,
                           float* c, size_t ldc, int accumulate, float* colsum,
@@ -310,8 +317,10 @@ int lmp_k_gemm_colsum_masked_f32(int trans_a, size_t m, size_t n, size_t k,
  * grad_utils.cpp:10-36): two transposes, two matmuls and a reduction.  When
  * both products fit the tiny GEMM's 16 x 16 blocks (K <= 512, at most 2^21
  * multiply-adds, blocks of 32 x 32 short of a quarter of the CUs) they run as
- * one launch; otherwise lmp_k_gemm_f32 (dx) then lmp_k_gemm_colsum_f32 (dw,
- * db).  Either way the same bits as those two calls. */
+ * one launch; otherwise lmp_k_gemm_colsum_f32 (dw, db) then lmp_k_gemm_f32
+ * (dx).  Either way the same bits as those two calls.  Argument errors are
+ * returned before anything is written; after the first of the two calls only
+ * running out of device memory can fail, which leaves dx unwritten. */
 int lmp_k_linear_backward_f32(size_t batch, size_t in, size_t out, const float* x, size_t ldx,
                               const float* w, size_t ldw, const float* g, size_t ldg,
                               float* dx, size_t lddx, int dx_accumulate, float* dw,

@@ -519,10 +519,12 @@ def mlp_step(weights, biases, x, y, f64_gemm: bool = False, relu_masks=None):
     return float(loss.data.reshape(-1)[0]), [w.grad for w in W], [b.grad for b in B]
 
 
-def mlp_train(weights, biases, x, y, steps: int, lr: float = 1e-3):
+def mlp_train(weights, biases, x, y, steps: int, lr: float = 1e-3, f64_gemm: bool = False):
     """Train Linear-ReLU-...-Linear-Softmax with the README loop
     (README.md:116-126): loss = sum(sum(-y * log(p + 1e-3), 1), 0), full
     backward, then p <- p.data - lr * p.grad rebuilt as a fresh leaf.
+    f64_gemm swaps every GEMM (forward and backward) for the float64-
+    accumulated one (matmul_f64), another valid summation order.
     Returns (per-step losses, final weights, final biases)."""
     W = [OVar(w, True) for w in weights]
     B = [OVar(b, True) for b in biases]
@@ -531,7 +533,7 @@ def mlp_train(weights, biases, x, y, steps: int, lr: float = 1e-3):
     for _ in range(steps):
         h = xv
         for i in range(len(W)):
-            h = (h @ W[i]) + B[i]
+            h = matmul_v(h, W[i], f64_gemm) + B[i]
             if i < len(W) - 1:
                 h = relu(h)
         p = softmax(h, -1)

@@ -31,7 +31,8 @@ namespace {
 // Values and shape of Python data that is not an ndarray (nested lists or
 // tuples of numbers, or one number), read through numpy.asarray: numpy works
 // out the shape and refuses ragged nesting, the dtype kind tells numbers from
-// anything else, and the values arrive as float64 -- Lamp3's Scalar -- for
+// anything else (an object array is checked item by item), and the values
+// arrive as float64 -- Lamp3's Scalar -- for
 // the tensor constructor to convert to the target dtype.  The two error texts
 // are the ones Lamp3's Python users see (bindings/variable.hpp:21-48).
 void values_of(const py::handle& data, std::vector<Scalar>& flat, std::vector<size_t>& shape) {
@@ -43,6 +44,31 @@ void values_of(const py::handle& data, std::vector<Scalar>& flat, std::vector<si
     throw py::value_error("Rushlite: invalid input type");
   }
   const char kind = arr.dtype().kind();
+  if (kind == 'O') {
+    // Items numpy kept as Python objects: integers beyond 64 bits (Lamp3
+    // casts each item to double, so they are taken at their float64 value)
+    // or, on numpy before 1.24, ragged nesting.  Anything else is not a number.
+    py::module_ np = py::module_::import("numpy");
+    const py::object complex_kind = np.attr("complexfloating");
+    shape.assign(arr.shape(), arr.shape() + arr.ndim());
+    if (shape.empty()) shape.push_back(1);
+    flat.clear();
+    for (const py::handle item : arr.attr("ravel")()) {
+      if (py::isinstance<py::list>(item) || py::isinstance<py::tuple>(item))
+        throw py::value_error("Rushlite: array must be uniform");
+      if (item.is_none() || py::isinstance<py::str>(item) || py::isinstance<py::bytes>(item) ||
+          PyComplex_Check(item.ptr()) || py::isinstance(item, complex_kind) ||
+          !PyNumber_Check(item.ptr()))
+        throw py::value_error("Rushlite: invalid input type");
+      const double v = PyFloat_AsDouble(item.ptr());
+      if (v == -1.0 && PyErr_Occurred()) {
+        PyErr_Clear();
+        throw py::value_error("Rushlite: invalid input type");
+      }
+      flat.push_back(v);
+    }
+    return;
+  }
   if (kind != 'b' && kind != 'i' && kind != 'u' && kind != 'f')
     throw py::value_error("Rushlite: invalid input type");
   const auto values = py::array_t<double, py::array::c_style | py::array::forcecast>::ensure(arr);

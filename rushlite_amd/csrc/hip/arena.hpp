@@ -184,8 +184,12 @@ DeviceAlloc grow_and_allocate(Arena& target, Arena& cache, std::size_t bytes,
   DeviceAlloc st = dev.malloc(seg, &base);
   if (st == DeviceAlloc::kOutOfMemory && may_release) {
     if (!dev.sync()) return DeviceAlloc::kError;
+    // Every taken segment is released even past a failed release: they are
+    // no longer tracked by the arena, so one skipped here would leak.
+    bool released = true;
     for (const Arena::Span& s : cache.take_free_segments())
-      if (!dev.free(s.addr)) return DeviceAlloc::kError;
+      released = dev.free(s.addr) && released;
+    if (!released) return DeviceAlloc::kError;
     st = dev.malloc(seg, &base);
   }
   if (st != DeviceAlloc::kOk) return st;

@@ -1783,6 +1783,36 @@ bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
+// ------------------------------------------------------ strided column sums
+
+// colsum[j] (+)= sum over r < k of op(B)[r][j], folded in index order, for a B
+// whose rows are strided (ldb): the column-sum GEMM's second launch when the
+// sums could not ride in the GEMM.  B untransposed ([k, ldb]): one lane per
+// column, coalesced row by row.  B transposed (stored [n, ldb]): one wave per
+// output, lanes striding over the row, then a butterfly.  256 lanes per
+// workgroup; the grid is ceil(n / 256) or ceil(n / 4) workgroups.
+__global__ __launch_bounds__(256) void colsum_strided_f32(float* __restrict__ out,
+                                                          const float* __restrict__ b, int k,
+                                                          int n, int ldb, int trans_b,
+                                                          int accumulate) {
+  if (!trans_b) {
+    const int j = int(blockIdx.x) * 256 + int(threadIdx.x);
+    if (j >= n) return;
+    float s = 0.0f;
+    for (int r = 0; r < k; ++r) s += b[size_t(r) * size_t(ldb) + size_t(j)];
+    out[j] = accumulate ? out[j] + s : s;
+    return;
+  }
+  const int j = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
+  const int lane = int(threadIdx.x & 63);
+  if (j >= n) return;  // the whole wave leaves together
+  const float* row = b + size_t(j) * size_t(ldb);
+  float s = 0.0f;
+  for (int r = lane; r < k; r += 64) s += row[r];
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) out[j] = accumulate ? out[j] + s : s;
+}
+
 // ------------------------------------------------------------- transpose
 
 template <typename T>
@@ -1929,27 +1959,35 @@ extern "C" int lmp_k_gemm_colsum_f32(int trans_a, int trans_b, size_t m, size_t 
                               : launch_tiny<false, false>(rt, g));
   }
   // Larger products: the column sums ride in the GEMM when it runs on LDS
-  // tiles with B untransposed and K unsplit (the first tile row adds up the B
-  // panels); otherwise the GEMM, then the column sums of op(B) by the
-  // reduction kernels (contiguous B only), accumulated through a scratch
-  // buffer when asked.
-  if (ldb != (trans_b ? k : n))
-    return fail(LMP_ERR_UNSUPPORTED, "gemm_colsum: strided B on the two-launch path");
-  bool fused = false;
-  int rc = gemm_f32_entry(trans_a, trans_b, m, n, k, a, lda, b, ldb, nullptr, c, ldc,
-                          accumulate, 0, Workspace{}, colsum, colsum_accumulate, &fused);
-  if (rc != LMP_OK || fused) return rc;
-  // sum over k of op(B)[k][j]: B [k, n] reduces over its rows, B^T (stored
-  // [n, k]) over its columns.
-  const size_t outer = trans_b ? n : 1, len = k, inner = trans_b ? 1 : n;
+  // tiles (B untransposed, K unsplit) or on the short-K kernel; otherwise the
+  // GEMM, then the column sums of op(B) by the reduction kernels (contiguous
+  // B) or by colsum_strided_f32 (strided B).  Everything the second launch
+  // needs is reserved before the first, so a refusal leaves C untouched.
+  const bool contiguous_b = ldb == (trans_b ? k : n);
   float* dst = colsum;
-  if (colsum_accumulate) {
+  if (contiguous_b && colsum_accumulate) {
     dst = static_cast<float*>(scratch_alloc(n * sizeof(float)));
     if (!dst) return LMP_ERR_OOM;
   }
-  rc = lmp_k_reduce(LMP_RED_SUM, LMP_FLOAT32, dst, b, outer, len, inner);
-  if (rc == LMP_OK && colsum_accumulate) rc = lmp_k_add_inplace(LMP_FLOAT32, colsum, dst, n);
-  if (colsum_accumulate) scratch_free(dst);
+  bool fused = false;
+  int rc = gemm_f32_entry(trans_a, trans_b, m, n, k, a, lda, b, ldb, nullptr, c, ldc,
+                          accumulate, 0, Workspace{}, colsum, colsum_accumulate, &fused);
+  if (rc == LMP_OK && !fused) {
+    if (contiguous_b) {
+      // sum over k of op(B)[k][j]: B [k, n] reduces over its rows, B^T (stored
+      // [n, k]) over its columns.
+      const size_t outer = trans_b ? n : 1, len = k, inner = trans_b ? 1 : n;
+      rc = lmp_k_reduce(LMP_RED_SUM, LMP_FLOAT32, dst, b, outer, len, inner);
+      if (rc == LMP_OK && colsum_accumulate) rc = lmp_k_add_inplace(LMP_FLOAT32, colsum, dst, n);
+    } else {
+      LMP_RUNTIME_OR_FAIL(rt);
+      const uint32_t grid = uint32_t(trans_b ? (n + 3) / 4 : (n + 255) / 256);
+      hipLaunchKernelGGL(colsum_strided_f32, dim3(grid), dim3(256), 0, rt->stream, colsum, b,
+                         int(k), int(n), int(ldb), trans_b ? 1 : 0, colsum_accumulate ? 1 : 0);
+      LMP_LAUNCH_CHECK("colsum_strided_f32");
+    }
+  }
+  if (dst != colsum) scratch_free(dst);  // stream-ordered: the add reads it first
   return rc;
 }
 
@@ -2046,10 +2084,12 @@ extern "C" int lmp_k_linear_backward_f32(size_t batch, size_t in, size_t out, co
   gx.accumulate = dx_accumulate ? 1 : 0;
   LMP_RUNTIME_OR_FAIL(rt);
   if (tiny16(rt, gw) && tiny16(rt, gx)) return launch_tiny_linear_backward(rt, gw, gx);
-  const int rc = lmp_k_gemm_f32(0, 1, batch, in, out, g, ldg, w, ldw, dx, lddx, dx_accumulate);
+  // dW and db first: that call refuses before it launches anything, and dX
+  // (a plain GEMM) can then only fail by running out of memory.
+  const int rc = lmp_k_gemm_colsum_f32(1, 0, in, out, batch, x, ldx, g, ldg, dw, lddw,
+                                       dw_accumulate, db, db_accumulate);
   if (rc != LMP_OK) return rc;
-  return lmp_k_gemm_colsum_f32(1, 0, in, out, batch, x, ldx, g, ldg, dw, lddw, dw_accumulate,
-                               db, db_accumulate);
+  return lmp_k_gemm_f32(0, 1, batch, in, out, g, ldg, w, ldw, dx, lddx, dx_accumulate);
 }
 
 extern "C" int lmp_k_linear_relu_f32(int trans_a, int trans_b, size_t m, size_t n,

@@ -84,6 +84,7 @@ struct FakeDevice {
   std::vector<std::pair<Arena::Addr, std::size_t>> live;
   std::vector<std::string> log;
   bool fail_sync = false;
+  Arena::Addr fail_free_of = 0;  // a release of this base fails (and keeps it)
   DeviceAlloc malloc(std::size_t bytes, Arena::Addr* base) {
     log.push_back("malloc " + std::to_string(bytes));
     if (held + bytes > capacity) return DeviceAlloc::kOutOfMemory;
@@ -99,6 +100,7 @@ struct FakeDevice {
   }
   bool free(Arena::Addr base) {
     log.push_back("free " + std::to_string(base));
+    if (base == fail_free_of) return false;
     for (auto it = live.begin(); it != live.end(); ++it)
       if (it->first == base) {
         held -= it->second;
@@ -180,6 +182,25 @@ int growth_policy_checks() {
     CHECK(lmp_hip::grow_and_allocate(eager, eager, 64, kMin, true, dev, &span, &seg) ==
           DeviceAlloc::kError);
     CHECK((dev.log == std::vector<std::string>{"malloc 1048576", "sync"}));
+  }
+  {
+    // A release that fails is an error, but every other free segment taken
+    // from the arena is still released (none is left untracked).
+    FakeDevice dev{3 * kMin};
+    Arena eager(256);
+    Arena::Addr a = 0, b = 0, c = 0;
+    CHECK(dev.malloc(kMin, &a) == DeviceAlloc::kOk && eager.add_segment(a, kMin));
+    CHECK(dev.malloc(kMin, &b) == DeviceAlloc::kOk && eager.add_segment(b, kMin));
+    CHECK(dev.malloc(kMin, &c) == DeviceAlloc::kOk && eager.add_segment(c, kMin));
+    dev.fail_free_of = a;
+    dev.log.clear();
+    Arena::Span span;
+    std::size_t seg = 0;
+    CHECK(lmp_hip::grow_and_allocate(eager, eager, 64, kMin, true, dev, &span, &seg) ==
+          DeviceAlloc::kError);
+    CHECK(eager.segment_count() == 0);
+    CHECK(dev.live.size() == 1 && dev.live[0].first == a && dev.held == kMin);
+    CHECK(dev.log.size() == 5 && dev.log[0] == "malloc 1048576" && dev.log[1] == "sync");
   }
   {
     // A request above the minimum segment gets a segment of its own size.

@@ -15,7 +15,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from _helpers import rel_err, ulp_dist
+from _helpers import assert_within_ulp, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -536,7 +536,7 @@ def test_config1_full_size_bitexact(rsl, oracle):
     del eager
     e = oracle.unary("exp", a_np)
     e_gpu = rsl.exp(a).numpy()
-    assert ulp_dist(e_gpu, e).max() <= 2
+    assert_within_ulp(e_gpu, e, 2)
     same_exp = _oracle_chain6(oracle, e_gpu, a_np, b_np)
     assert np.array_equal(fused.view(np.uint32), same_exp.view(np.uint32))
     del same_exp, e_gpu
@@ -568,22 +568,33 @@ def test_config2_backward_and_reductions(rsl, oracle):
 
 def test_config3_linear_forward_backward(rsl):
     """Linear fwd + both backward GEMMs at 4096^3 and the skinny
-    32x4096x8192 shape, checked on sampled rows against float64."""
+    32x4096x8192 shape through autograd, with a random upstream gradient:
+    loss = sum(sum(Y * G, 1), 0) with G normal(0, 0.02) makes dY = G exactly
+    (matrix_ops.cpp:8-24 then forms dX = G.W^T and dW = X^T.G).  Sampled rows
+    and columns of Y, dX and dW against float64."""
     rng = np.random.default_rng(4)
     for m, k, n in ((4096, 4096, 4096), (32, 8192, 4096)):
         x_np = (rng.standard_normal((m, k)) * 0.02).astype(np.float32)
         w_np = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+        g_np = (rng.standard_normal((m, n)) * 0.02).astype(np.float32)
         x, w = V(rsl, x_np, True), V(rsl, w_np, True)
         y = rsl.matmul(x, w)
-        y.backward()  # dY = ones
+        loss = rsl.sum(rsl.sum(y * V(rsl, g_np), 1), 0)
+        loss.backward()
         rows = rng.choice(m, min(m, 32), replace=False)
-        x64, w64 = x_np.astype(np.float64), w_np.astype(np.float64)
-        assert rel_err(y.numpy()[rows], x64[rows] @ w64) <= 1e-4
+        cols = rng.choice(n, 32, replace=False)
+        x64, w64, g64 = (t.astype(np.float64) for t in (x_np, w_np, g_np))
+        yv = y.numpy()
+        assert rel_err(yv[rows], x64[rows] @ w64) <= 1e-4
+        assert rel_err(yv[:, cols], x64 @ w64[:, cols]) <= 1e-4
         gx = x.grad.numpy()
-        assert rel_err(gx[rows], np.ones((len(rows), n)) @ w64.T) <= 1e-4
+        kcols = rng.choice(k, 32, replace=False)
+        assert rel_err(gx[rows], g64[rows] @ w64.T) <= 1e-4
+        assert rel_err(gx[:, kcols], g64 @ w64[kcols].T) <= 1e-4
         gw = w.grad.numpy()
         wrows = rng.choice(k, 32, replace=False)
-        assert rel_err(gw[wrows], x64.T[wrows] @ np.ones((m, n))) <= 1e-4
+        assert rel_err(gw[wrows], x64.T[wrows] @ g64) <= 1e-4
+        assert rel_err(gw[:, cols], x64.T @ g64[:, cols]) <= 1e-4
 
 
 @pytest.mark.parametrize("m,k,n", [(96, 80, 72), (4096, 64, 128), (2048, 256, 256)])

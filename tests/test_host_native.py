@@ -129,12 +129,15 @@ def test_sequence_constructor_shapes_and_errors():
     for data, shape, values in (([[1, 2], [3, 4]], [2, 2], [1.0, 2.0, 3.0, 4.0]),
                                 (((1, 2), (3, 4)), [2, 2], [1.0, 2.0, 3.0, 4.0]),
                                 ([1.5, True, 3], [3], [1.5, 1.0, 3.0]),
-                                (2.5, [1], [2.5]), ([], [0], []), ([[]], [1, 0], [])):
+                                (2.5, [1], [2.5]), ([], [0], []), ([[]], [1, 0], []),
+                                ([2**70, 1], [2], [float(2**70), 1.0]),
+                                ([[2**64], [-(2**65)]], [2, 1], [float(2**64), -float(2**65)])):
         v = rsl.Variable(data, device=cpu)
         assert v.shape == shape and v.data.tolist() == values, data
     for bad in ([[1, 2], [3]], [[1, 2], 3]):
         with pytest.raises(ValueError, match="Rushlite: array must be uniform"):
             rsl.Variable(bad, device=cpu)
-    for bad in ([1, "a"], [1, None], "abc", [1 + 2j]):
+    for bad in ([1, "a"], [1, None], "abc", [1 + 2j], [2**70, None], [2**70, "a"],
+                [2**70, 1 + 2j]):
         with pytest.raises(ValueError, match="Rushlite: invalid input type"):
             rsl.Variable(bad, device=cpu)

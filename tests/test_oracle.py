@@ -17,7 +17,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from _helpers import ulp_dist
+from _helpers import assert_within_ulp, ulp_dist, zero_sign_mismatches
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "lamp3_known_answers.json").read_text())
 ATOL = GOLDEN["tolerance"]["atol"]
@@ -248,7 +248,7 @@ def test_transcendentals_within_1ulp_of_correctly_rounded(oracle, op, fn):
     if op == "log":
         x = np.abs(x) + np.float32(1e-3)
     got = oracle.unary(op, x)
-    assert ulp_dist(got, correctly_rounded(fn, x)).max() <= 1
+    assert_within_ulp(got, correctly_rounded(fn, x), 1, op)
 
 
 def test_pow_within_1ulp(oracle):
@@ -256,7 +256,43 @@ def test_pow_within_1ulp(oracle):
     a = rng.uniform(0.01, 10, 5000).astype(np.float32)
     b = rng.uniform(-4, 4, 5000).astype(np.float32)
     got = oracle.binary("pow", a, b)
-    assert ulp_dist(got, correctly_rounded(np.power, a, b)).max() <= 1
+    assert_within_ulp(got, correctly_rounded(np.power, a, b), 1)
+
+
+def test_ulp_helpers_see_the_sign_of_zero():
+    """-0.0 and +0.0 are adjacent but distinct on the ulp line, distances are
+    monotone across zero, and a zero of the wrong sign is reported even though
+    it is only one ulp away."""
+    d = np.float32(1e-45)  # the smallest subnormal
+    assert ulp_dist(np.float32(-0.0), np.float32(0.0)) == 1
+    assert ulp_dist(-d, d) == 3
+    assert ulp_dist(np.float32(-1.0), np.float32(1.0)) == 2 * 0x3F800000 + 1
+    xs = np.sort(np.random.default_rng(3).standard_normal(4001).astype(np.float32))
+    xs = np.concatenate([xs[xs < 0], [np.float32(-0.0), np.float32(0.0)], xs[xs > 0]])
+    keys = ulp_dist(xs, np.full_like(xs, -np.inf))
+    assert np.all(np.diff(keys) > 0)  # strictly increasing distance from -inf
+    want = np.array([0.0, -0.0, 1.0, -0.0], np.float32)
+    assert zero_sign_mismatches(want, want) == 0
+    assert zero_sign_mismatches(np.array([0.0, 0.0, 1.0, -0.0], np.float32), want) == 1
+    assert zero_sign_mismatches(np.array([0.0, -1e-45, 1.0, -0.0], np.float32), want) == 1
+    with pytest.raises(AssertionError):
+        assert_within_ulp(np.array([0.0, 0.0], np.float32),
+                          np.array([0.0, -0.0], np.float32), 2)
+
+
+@pytest.mark.parametrize("op,fn,x,want", [
+    ("sin", math.sin, -0.0, -0.0), ("sin", math.sin, 0.0, 0.0),
+    ("tan", math.tan, -0.0, -0.0), ("tan", math.tan, 0.0, 0.0),
+    ("sqrt", math.sqrt, -0.0, -0.0), ("exp", math.exp, -0.0, 1.0),
+    ("cos", math.cos, -0.0, 1.0), ("neg", lambda v: -v, 0.0, -0.0),
+    ("abs", abs, -0.0, 0.0)])
+def test_oracle_signed_zero_results(oracle, op, fn, x, want):
+    """std::sin/tan/sqrt keep the sign of a zero argument (C99 Annex F), the
+    functors of cpu/kernels.hpp:74-113 return them unchanged; Python's math
+    module states the same values."""
+    got = oracle.unary(op, np.array([x], np.float32))
+    assert np.array_equal(got.view(np.uint32), np.array([want], np.float32).view(np.uint32))
+    assert math.copysign(1.0, fn(x)) == math.copysign(1.0, want)
 
 
 def test_reduction_order_is_sequential(oracle):
