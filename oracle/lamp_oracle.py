@@ -466,8 +466,50 @@ def matmul_f64(a, b):
     return (np.asarray(a, np.float64) @ np.asarray(b, np.float64)).astype(np.float32)
 
 
-def matmul_v(a: OVar, b: OVar, f64: bool = False):
-    mm = matmul_f64 if f64 else matmul
+def _matmul_reversed_k(a, b):
+    """The sequential fp32 order with k running backwards."""
+    a, b = _f32(a), _f32(b)
+    return matmul(np.ascontiguousarray(a[:, ::-1]), np.ascontiguousarray(b[::-1]))
+
+
+def _matmul_k_blocks(block):
+    """k cut into blocks of `block`: each block's product accumulated in
+    float64 and rounded to fp32, the blocks then summed in fp32 in order (the
+    shape of a split-K GEMM with a fold)."""
+    def mm(a, b):
+        a, b = _f32(a), _f32(b)
+        out = np.zeros((a.shape[0], b.shape[1]), np.float32)
+        for k0 in range(0, a.shape[1], block):
+            part = (a[:, k0:k0 + block].astype(np.float64)
+                    @ b[k0:k0 + block].astype(np.float64)).astype(np.float32)
+            out = out + part
+        return out
+    return mm
+
+
+def _matmul_blas(a, b):
+    """numpy's fp32 matmul (a blocked BLAS sgemm with fused multiply-adds)."""
+    return _f32(a) @ _f32(b)
+
+
+# Summation orders of an fp32 GEMM that the 1e-4 GEMM tolerance admits, to
+# size how far valid orders drift apart over a chaotic training trajectory.
+# Test infrastructure only: none restates a reference function except "seq"
+# (cpu/matrix.cpp:26-33).
+GEMM_ORDERS = {
+    "seq": matmul,
+    "f64": matmul_f64,
+    "reversed_k": _matmul_reversed_k,
+    "k_blocks_32": _matmul_k_blocks(32),
+    "k_blocks_128": _matmul_k_blocks(128),
+    "blas_sgemm": _matmul_blas,
+}
+
+
+def matmul_v(a: OVar, b: OVar, f64=False):
+    """a @ b with its backward; f64 True selects matmul_f64, a callable any
+    other GEMM order (GEMM_ORDERS)."""
+    mm = f64 if callable(f64) else (matmul_f64 if f64 else matmul)
     out = mm(a.data, b.data)
 
     def bw(node):
@@ -519,12 +561,13 @@ def mlp_step(weights, biases, x, y, f64_gemm: bool = False, relu_masks=None):
     return float(loss.data.reshape(-1)[0]), [w.grad for w in W], [b.grad for b in B]
 
 
-def mlp_train(weights, biases, x, y, steps: int, lr: float = 1e-3, f64_gemm: bool = False):
+def mlp_train(weights, biases, x, y, steps: int, lr: float = 1e-3, f64_gemm=False):
     """Train Linear-ReLU-...-Linear-Softmax with the README loop
     (README.md:116-126): loss = sum(sum(-y * log(p + 1e-3), 1), 0), full
     backward, then p <- p.data - lr * p.grad rebuilt as a fresh leaf.
     f64_gemm swaps every GEMM (forward and backward) for the float64-
-    accumulated one (matmul_f64), another valid summation order.
+    accumulated one (matmul_f64), another valid summation order, or, given a
+    callable (GEMM_ORDERS), for that one.
     Returns (per-step losses, final weights, final biases)."""
     W = [OVar(w, True) for w in weights]
     B = [OVar(b, True) for b in biases]

@@ -295,6 +295,27 @@ def test_oracle_signed_zero_results(oracle, op, fn, x, want):
     assert math.copysign(1.0, fn(x)) == math.copysign(1.0, want)
 
 
+def test_gemm_orders_are_valid_and_distinct(oracle):
+    """Every GEMM order used to size the README-MLP loss envelope is within the
+    1e-4 GEMM bar of the float64 product, and the orders really differ (each
+    pair disagrees in some bit on a product with K = 256)."""
+    rng = np.random.default_rng(12)
+    a = rng.standard_normal((64, 256)).astype(np.float32)
+    b = rng.standard_normal((256, 48)).astype(np.float32)
+    truth = a.astype(np.float64) @ b.astype(np.float64)
+    outs = {}
+    for name, mm in oracle.GEMM_ORDERS.items():
+        got = mm(a, b)
+        assert got.dtype == np.float32 and got.shape == (64, 48)
+        assert np.max(np.abs(got - truth)) / np.max(np.abs(truth)) <= 1e-4, name
+        outs[name] = got
+    assert np.array_equal(outs["seq"], oracle.matmul(a, b))
+    names = list(outs)
+    for i, p in enumerate(names):
+        for q in names[i + 1:]:
+            assert not np.array_equal(outs[p], outs[q]), (p, q)
+
+
 def test_reduction_order_is_sequential(oracle):
     """The oracle folds each output in index order from the identity: compare
     with a pure-Python float32 fold (small case, bit-exact)."""
