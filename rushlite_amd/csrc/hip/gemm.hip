@@ -905,6 +905,11 @@ int launch_tiny_linear_backward(Runtime* rt, const GemmArgs& gw, const GemmArgs&
 //             256 x 256 tiles cannot fill the CUs (K split)
 //   LdsBig    256 x 256, 8 waves of 128 x 64, 2 stages (128 KiB), whenever its
 //             tiles cover the CUs: 4096^3 130 -> 139 TFLOP/s
+//   LdsMid    128 x 64, 4 waves of 32 x 64, 3 stages (72 KiB), K split so the
+//             tiles cover the CUs, when 128 x 128 tiles would not (K >= 512):
+//             config 4's last layer 512x1000x4096 49.6 -> 45.6 us and
+//             512x4096x1000 (B transposed) 46.2 -> 42.3 us, 1024^3 30.7 ->
+//             26.3 us (medians of interleaved rounds, random operands)
 template <int WM_, int WN_, int TM_, int TN_, int STAGES_, int MINB_>
 struct LdsCfg {
   static constexpr int WM = WM_, WN = WN_, TM = TM_, TN = TN_;
@@ -921,6 +926,7 @@ struct LdsCfg {
 using LdsSmall = LdsCfg<2, 2, 2, 2, 2, 2>;
 using LdsWide = LdsCfg<4, 2, 2, 2, 3, 1>;
 using LdsBig = LdsCfg<2, 4, 4, 2, 2, 1>;
+using LdsMid = LdsCfg<4, 1, 1, 2, 3, 1>;
 
 
 __device__ __forceinline__ int kswz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
@@ -1769,6 +1775,8 @@ int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok, const 
     // tiles do better there.)
     if (big_tiles >= rt->cu_count && g.k >= 256) return launch_lds<LdsBig, TA, TB>(rt, g, ws, colsum_done);
     if (g.m >= 512 && g.n >= 2048 && g.k >= 2048) return launch_lds<LdsWide, TA, TB>(rt, g, ws, colsum_done);
+    const int64_t tiles128 = int64_t((g.m + 127) / 128) * ((g.n + 127) / 128);
+    if (tiles128 < rt->cu_count && g.k >= 512) return launch_lds<LdsMid, TA, TB>(rt, g, ws, colsum_done);
   }
   const int64_t large_tiles = int64_t((g.m + CfgLarge::BM - 1) / CfgLarge::BM) *
                               ((g.n + CfgLarge::BN - 1) / CfgLarge::BN);

@@ -55,20 +55,24 @@ def test_noalloc_gemm_matches_allocating_entry(hip, calls):
 
 
 def test_noalloc_gemm_refuses_partials_above_the_workspace(hip):
-    """1920 x 1920 x 4096 splits K three ways on 128 x 128 tiles: 44 MB of
-    partials, more than the 32 MiB workspace."""
+    """1920 x 1920 x 4096 with A's rows padded to 4097 values (no 16-byte
+    rows, so the register-staged 128 x 128 tiles) splits K three ways: 44 MB
+    of partials, more than the 32 MiB workspace."""
     L = hip.lib()
     m = n = 1920
-    k = 4096
-    da, db, ref, out, lda, ldb = _case(hip, m, n, k, 0, 0, 0, 7)
+    k, lda = 4096, 4097
+    rng = np.random.default_rng(7)
+    a = (rng.standard_normal((m, lda)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+    da, db = hip.DeviceBuffer.from_numpy(a), hip.DeviceBuffer.from_numpy(b)
+    ref, out = (hip.DeviceBuffer.from_numpy(np.zeros((m, n), np.float32)) for _ in range(2))
     before = _pool(hip)
-    st = L.lmp_k_gemm_f32_noalloc(0, 0, m, n, k, da.ptr, lda, db.ptr, ldb, out.ptr, n, 0)
+    st = L.lmp_k_gemm_f32_noalloc(0, 0, m, n, k, da.ptr, lda, db.ptr, n, out.ptr, n, 0)
     assert st == hip.ERR_UNSUPPORTED
     msg = L.lmp_rt_last_error().decode()
     assert "no-allocation workspace" in msg and str(32 << 20) in msg, msg
     assert _pool(hip) == before
-    hip.check(L.lmp_k_gemm_f32(0, 0, m, n, k, da.ptr, lda, db.ptr, ldb, ref.ptr, n, 0))
-    a64 = da.numpy().astype(np.float64)
-    want = a64[:64] @ db.numpy().astype(np.float64)
+    hip.check(L.lmp_k_gemm_f32(0, 0, m, n, k, da.ptr, lda, db.ptr, n, ref.ptr, n, 0))
+    want = a[:64, :k].astype(np.float64) @ b.astype(np.float64)
     got = ref.numpy()[:64]
     assert np.max(np.abs(got - want)) / np.max(np.abs(want)) <= 1e-4
