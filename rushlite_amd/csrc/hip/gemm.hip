@@ -956,17 +956,21 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("" ::: "memory");
 }
 
-template <int NT, int MINB, class C, bool TA, bool TB>
-__global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
+// One workgroup's tile of C (or of its split-K partial): `bid` is the tile's
+// index in launch order, `split` the K split, `partial` whether K is split
+// (the tile then goes to the partial buffer without epilogue).  `smem` holds
+// at least C::STAGES * C::STAGE floats, 1 KiB aligned.
+template <class C, bool TA, bool TB>
+__device__ __forceinline__ void gemm_f32_lds_tile(const GemmArgs& g, int bid, const int split,
+                                                  const bool partial, float* smem) {
+  constexpr int NT = C::THREADS;
   constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN, S = C::STAGES;
   constexpr int HK = kBK / 2;
   constexpr int SU = 4;           // MFMA steps per sub-step
   constexpr int NU = HK / SU;     // sub-steps per K tile
   constexpr int DPT = C::A_DMA + C::B_DMA;
-  __shared__ __attribute__((aligned(1024))) float smem[S * C::STAGE];
 
   const int ntiles = g.tiles_m * g.tiles_n;
-  int bid = blockIdx.x;
   if (ntiles % 8 == 0) bid = (bid % 8) * (ntiles / 8) + bid / 8;
   constexpr int kGroup = 8;
   const int per_group = kGroup * g.tiles_n;
@@ -978,7 +982,6 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
   const int tile_n = in_group / gsize;
   const int m0 = tile_m * BM, n0 = tile_n * BN;
 
-  const int split = blockIdx.z;
   const int k_tiles = (g.k + kBK - 1) / kBK;
   const int kt0 = split * g.k_tiles_per_split;
   const int kt1 = min(k_tiles, kt0 + g.k_tiles_per_split);
@@ -1197,7 +1200,6 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
     }
   }
 
-  const bool partial = gridDim.z > 1;
   float* out = g.c;
   int64_t ld = g.ldc;
   if (partial) {
@@ -1257,6 +1259,35 @@ __global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
         }
       }
     }
+  }
+}
+
+template <int NT, int MINB, class C, bool TA, bool TB>
+__global__ __launch_bounds__(NT, MINB) void gemm_f32_lds(GemmArgs g) {
+  static_assert(NT == C::THREADS, "one lane per thread of the configuration");
+  __shared__ __attribute__((aligned(1024))) float smem[C::STAGES * C::STAGE];
+  gemm_f32_lds_tile<C, TA, TB>(g, int(blockIdx.x), int(blockIdx.z), gridDim.z > 1, smem);
+}
+
+// Two independent products in one launch (a Linear's weight gradient A and
+// input gradient B): workgroups [0, tiles_a * splits_a) compute product A in
+// the order of its own launch (split-major, as blockIdx.z then x), the rest
+// product B, so every tile and partial holds the bits the product's own
+// launch gives.  The CUs product A frees start B's first loads while A's last
+// stores drain, where two launches would drain and refill one after the other.
+template <int NT, int MINB, class CA, bool TAA, bool TBA, class CB, bool TAB, bool TBB>
+__global__ __launch_bounds__(NT, MINB) void gemm_f32_lds_pair(GemmArgs ga, int splits_a,
+                                                              GemmArgs gb, int splits_b) {
+  static_assert(NT == CA::THREADS && NT == CB::THREADS, "one workgroup size for both");
+  constexpr int FA = CA::STAGES * CA::STAGE, FB = CB::STAGES * CB::STAGE;
+  __shared__ __attribute__((aligned(1024))) float smem[FA > FB ? FA : FB];
+  const int tiles_a = ga.tiles_m * ga.tiles_n, tiles_b = gb.tiles_m * gb.tiles_n;
+  const int i = int(blockIdx.x);
+  if (i < tiles_a * splits_a) {
+    gemm_f32_lds_tile<CA, TAA, TBA>(ga, i % tiles_a, i / tiles_a, splits_a > 1, smem);
+  } else {
+    const int j = i - tiles_a * splits_a;
+    gemm_f32_lds_tile<CB, TAB, TBB>(gb, j % tiles_b, j / tiles_b, splits_b > 1, smem);
   }
 }
 
@@ -1581,17 +1612,33 @@ int default_splits(Runtime* rt, int tiles, int k_tiles) {
   return std::max(1, std::min(splits, 64));
 }
 
+// Sets g's tile counts for BM x BN tiles and its K tiles per split for a
+// requested split count (0: default_splits); returns the split count that
+// results, no split left empty.
+int set_split(Runtime* rt, GemmArgs& g, int bm, int bn, int splits) {
+  g.tiles_m = (g.m + bm - 1) / bm;
+  g.tiles_n = (g.n + bn - 1) / bn;
+  const int k_tiles = (g.k + kBK - 1) / kBK;
+  if (splits <= 0) splits = default_splits(rt, g.tiles_m * g.tiles_n, k_tiles);
+  splits = std::max(1, std::min(splits, k_tiles));
+  g.k_tiles_per_split = (k_tiles + splits - 1) / splits;
+  return std::max(1, (k_tiles + g.k_tiles_per_split - 1) / g.k_tiles_per_split);
+}
+
+// The split of the one-workgroup-per-CU LDS configurations: K split so the
+// tiles cover the CUs once, keeping at least eight K tiles per split.
+template <class L>
+int set_split_lds(Runtime* rt, GemmArgs& g) {
+  const int tiles = ((g.m + L::BM - 1) / L::BM) * ((g.n + L::BN - 1) / L::BN);
+  const int k_tiles = (g.k + kBK - 1) / kBK;
+  return set_split(rt, g, L::BM, L::BN, std::max(1, std::min(rt->cu_count / tiles, k_tiles / 8)));
+}
+
 template <class C, bool TA, bool TB>
 int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, const Workspace& ws, int splits = 0,
                     bool* colsum_done = nullptr) {
-  g.tiles_m = (g.m + C::BM - 1) / C::BM;
-  g.tiles_n = (g.n + C::BN - 1) / C::BN;
+  splits = set_split(rt, g, C::BM, C::BN, splits);
   const int tiles = g.tiles_m * g.tiles_n;
-  const int k_tiles = (g.k + kBK - 1) / kBK;
-  if (splits <= 0) splits = default_splits(rt, tiles, k_tiles);
-  splits = std::max(1, std::min(splits, k_tiles));
-  g.k_tiles_per_split = (k_tiles + splits - 1) / splits;
-  splits = std::max(1, (k_tiles + g.k_tiles_per_split - 1) / g.k_tiles_per_split);
 
   // Column sums ride only on the LDS tiles with B untransposed and no split.
   if (g.colsum && (!(vec && std::is_same_v<C, CfgLarge>) || splits > 1 || TB)) g.colsum = nullptr;
@@ -1623,17 +1670,11 @@ int launch_gemm_cfg(Runtime* rt, GemmArgs g, bool vec, const Workspace& ws, int 
   return LMP_OK;
 }
 
-// One of the one-workgroup-per-CU LDS configurations: K split so the tiles
-// cover the CUs once, keeping at least eight K tiles per split.
+// One of the one-workgroup-per-CU LDS configurations (split by set_split_lds).
 template <class L, bool TA, bool TB>
 int launch_lds(Runtime* rt, GemmArgs g, const Workspace& ws, bool* colsum_done = nullptr) {
-  g.tiles_m = (g.m + L::BM - 1) / L::BM;
-  g.tiles_n = (g.n + L::BN - 1) / L::BN;
+  const int splits = set_split_lds<L>(rt, g);
   const int tiles = g.tiles_m * g.tiles_n;
-  const int k_tiles = (g.k + kBK - 1) / kBK;
-  int splits = std::max(1, std::min(rt->cu_count / tiles, k_tiles / 8));
-  g.k_tiles_per_split = (k_tiles + splits - 1) / splits;
-  splits = std::max(1, (k_tiles + g.k_tiles_per_split - 1) / g.k_tiles_per_split);
   // Column sums ride only with B untransposed and no split.
   if (g.colsum && (splits > 1 || TB)) g.colsum = nullptr;
   if (g.colsum && colsum_done) *colsum_done = true;
@@ -1743,13 +1784,11 @@ int launch_rows(Runtime* rt, const GemmArgs& g0) {
 // without a split (no partial round trip) win; otherwise 128x128 with split
 // K.  M <= 64 uses 32x256 tiles, and M <= 32 the register-direct kernel when
 // its alignment requirements hold.
+enum class Route { Tiny, Short, Rows, Direct, Skinny, Big, Wide, Mid, Small64, Large };
+
 template <bool TA, bool TB>
-int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok, const Workspace& ws,
-                bool* colsum_done = nullptr) {
-  if (tiny_ok(g)) {
-    if (g.colsum && colsum_done) *colsum_done = true;
-    return launch_tiny<TA, TB>(rt, g);
-  }
+Route gemm_route(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok) {
+  if (tiny_ok(g)) return Route::Tiny;
   // K <= 32 with A transposed (a Linear's weight gradient at a small batch):
   // the persistent short-K kernel, whose tiles and orders are those of the
   // 128 x 128 LDS tiles it replaces here.
@@ -1757,34 +1796,136 @@ int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok, const 
     const int64_t short_tiles = int64_t((g.m + kShortBM - 1) / kShortBM) *
                                 ((g.n + kShortBN - 1) / kShortBN);
     if (vec && g.vec_out && g.k <= kBK && !g.bias && short_tiles <= 0x7fffffff)
-      return launch_short(rt, g, colsum_done);
+      return Route::Short;
   }
   // M <= 32 with B transposed and a 32-column block for every CU: whole rows
   // of B per workgroup, no split (config 3's dX: 46 -> 31-35 us cold).
   if constexpr (!TA && TB) {
-    if (direct_ok && g.m <= 32 && (g.n + 31) / 32 >= rt->cu_count) return launch_rows(rt, g);
+    if (direct_ok && g.m <= 32 && (g.n + 31) / 32 >= rt->cu_count) return Route::Rows;
   }
-  // With B transposed a wave's loads touch more cache lines per byte, so
-  // three fragments in flight instead of two.
-  if (direct_ok && g.m <= 32) return launch_direct<TA, TB, TB ? 3 : 2>(rt, g, ws);
-  if (g.m <= 64) return launch_gemm_cfg<CfgSkinny, TA, TB>(rt, g, vec, ws);
+  if (direct_ok && g.m <= 32) return Route::Direct;
+  if (g.m <= 64) return Route::Skinny;
   if (vec) {
     const int64_t big_tiles = int64_t((g.m + LdsBig::BM - 1) / LdsBig::BM) *
                               ((g.n + LdsBig::BN - 1) / LdsBig::BN);
     // (K of a few tiles leaves the kernel bound by writing C: more, smaller
     // tiles do better there.)
-    if (big_tiles >= rt->cu_count && g.k >= 256) return launch_lds<LdsBig, TA, TB>(rt, g, ws, colsum_done);
-    if (g.m >= 512 && g.n >= 2048 && g.k >= 2048) return launch_lds<LdsWide, TA, TB>(rt, g, ws, colsum_done);
+    if (big_tiles >= rt->cu_count && g.k >= 256) return Route::Big;
+    if (g.m >= 512 && g.n >= 2048 && g.k >= 2048) return Route::Wide;
     const int64_t tiles128 = int64_t((g.m + 127) / 128) * ((g.n + 127) / 128);
-    if (tiles128 < rt->cu_count && g.k >= 512) return launch_lds<LdsMid, TA, TB>(rt, g, ws, colsum_done);
+    if (tiles128 < rt->cu_count && g.k >= 512) return Route::Mid;
   }
   const int64_t large_tiles = int64_t((g.m + CfgLarge::BM - 1) / CfgLarge::BM) *
                               ((g.n + CfgLarge::BN - 1) / CfgLarge::BN);
   const int64_t small_tiles = int64_t((g.m + CfgSmall::BM - 1) / CfgSmall::BM) *
                               ((g.n + CfgSmall::BN - 1) / CfgSmall::BN);
   if (large_tiles < rt->cu_count && g.k <= 2048 && small_tiles >= rt->cu_count)
-    return launch_gemm_cfg<CfgSmall, TA, TB>(rt, g, vec, ws, 1);
-  return launch_gemm_cfg<CfgLarge, TA, TB>(rt, g, vec, ws, 0, colsum_done);
+    return Route::Small64;
+  return Route::Large;
+}
+
+template <bool TA, bool TB>
+int launch_gemm(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok, const Workspace& ws,
+                bool* colsum_done = nullptr) {
+  switch (gemm_route<TA, TB>(rt, g, vec, direct_ok)) {
+    case Route::Tiny:
+      if (g.colsum && colsum_done) *colsum_done = true;
+      return launch_tiny<TA, TB>(rt, g);
+    case Route::Short: return launch_short(rt, g, colsum_done);
+    case Route::Rows: return launch_rows(rt, g);
+    // With B transposed a wave's loads touch more cache lines per byte, so
+    // three fragments in flight instead of two.
+    case Route::Direct: return launch_direct<TA, TB, TB ? 3 : 2>(rt, g, ws);
+    case Route::Skinny: return launch_gemm_cfg<CfgSkinny, TA, TB>(rt, g, vec, ws);
+    case Route::Big: return launch_lds<LdsBig, TA, TB>(rt, g, ws, colsum_done);
+    case Route::Wide: return launch_lds<LdsWide, TA, TB>(rt, g, ws, colsum_done);
+    case Route::Mid: return launch_lds<LdsMid, TA, TB>(rt, g, ws, colsum_done);
+    case Route::Small64: return launch_gemm_cfg<CfgSmall, TA, TB>(rt, g, vec, ws, 1);
+    case Route::Large: return launch_gemm_cfg<CfgLarge, TA, TB>(rt, g, vec, ws, 0, colsum_done);
+  }
+  return fail(LMP_ERR_RUNTIME, "gemm: no kernel for this product");
+}
+
+// ------------------------------------------------------ weight + input pair
+
+// The LDS configuration a product's own launch would use, with its tiles and
+// split set in g: 0 (not an LDS-tile launch), else the configuration's id
+// (1 Big, 2 Wide, 3 Mid, 4 the 128 x 128 LDS tiles of the Large route).
+template <bool TA, bool TB>
+int lds_config_of(Runtime* rt, GemmArgs& g, bool vec, bool direct_ok, int* splits) {
+  switch (gemm_route<TA, TB>(rt, g, vec, direct_ok)) {
+    case Route::Big: *splits = set_split_lds<LdsBig>(rt, g); return 1;
+    case Route::Wide: *splits = set_split_lds<LdsWide>(rt, g); return 2;
+    case Route::Mid: *splits = set_split_lds<LdsMid>(rt, g); return 3;
+    case Route::Large:
+      if (!vec) return 0;
+      *splits = set_split(rt, g, CfgLarge::BM, CfgLarge::BN, 0);
+      return 4;
+    default: return 0;
+  }
+}
+
+template <class CW, class CX>
+int launch_pair(Runtime* rt, GemmArgs gw, int sw, GemmArgs gx, int sx) {
+  static_assert(CW::THREADS == CX::THREADS, "one workgroup size for both");
+  const Workspace ws{};
+  float* pw = nullptr;
+  float* px = nullptr;
+  float* const cw = gw.c;
+  float* const cx = gx.c;
+  if (sw > 1) {
+    const int rc = ws.take(size_t(sw) * size_t(gw.m) * size_t(gw.n) * sizeof(float), &pw);
+    if (rc != LMP_OK) return rc;
+    gw.c = pw;
+  }
+  if (sx > 1) {
+    const int rc = ws.take(size_t(sx) * size_t(gx.m) * size_t(gx.n) * sizeof(float), &px);
+    if (rc != LMP_OK) {
+      if (pw) ws.give(pw);
+      return rc;
+    }
+    gx.c = px;
+  }
+  constexpr int kMinB = CW::MINB > CX::MINB ? CW::MINB : CX::MINB;
+  const int64_t wgs = int64_t(gw.tiles_m) * gw.tiles_n * sw + int64_t(gx.tiles_m) * gx.tiles_n * sx;
+  hipLaunchKernelGGL((gemm_f32_lds_pair<CW::THREADS, kMinB, CW, true, false, CX, false, true>),
+                     dim3(uint32_t(wgs)), dim3(CW::THREADS), 0, rt->stream, gw, sw, gx, sx);
+  LMP_LAUNCH_CHECK("gemm_f32_lds_pair");
+  int rc = LMP_OK;
+  if (sw > 1) rc = launch_fold(rt, cw, pw, gw.m, gw.n, gw.ldc, sw, gw.accumulate, nullptr, 0);
+  if (rc == LMP_OK && sx > 1)
+    rc = launch_fold(rt, cx, px, gx.m, gx.n, gx.ldc, sx, gx.accumulate, nullptr, 0);
+  if (pw) ws.give(pw);  // stream-ordered: the folds read them first
+  if (px) ws.give(px);
+  return rc;
+}
+
+// dW = X^T G (with db, the column sums of G, when gw.colsum is set) and
+// dX = G W^T in one launch when both take LDS tiles of one workgroup size,
+// each with the configuration and split of its own launch (so the same bits
+// as lmp_k_gemm_colsum_f32 and lmp_k_gemm_f32); the column sums must then ride
+// in the dW tiles (dW unsplit).  Returns false, with nothing launched, when
+// the pair does not apply.
+bool try_linear_backward_pair(Runtime* rt, GemmArgs gw, bool vec_w, bool direct_w, GemmArgs gx,
+                              bool vec_x, bool direct_x, int* rc) {
+  int sw = 1, sx = 1;
+  const int kw = lds_config_of<true, false>(rt, gw, vec_w, direct_w, &sw);
+  const int kx = lds_config_of<false, true>(rt, gx, vec_x, direct_x, &sx);
+  if (kw == 0 || kx == 0) return false;
+  if (gw.colsum && sw > 1) return false;
+  const bool wide_w = kw <= 2, wide_x = kx <= 2;  // 512-thread configurations
+  if (wide_w != wide_x) return false;
+  switch (kw * 8 + kx) {
+    case 1 * 8 + 1: *rc = launch_pair<LdsBig, LdsBig>(rt, gw, sw, gx, sx); return true;
+    case 1 * 8 + 2: *rc = launch_pair<LdsBig, LdsWide>(rt, gw, sw, gx, sx); return true;
+    case 2 * 8 + 1: *rc = launch_pair<LdsWide, LdsBig>(rt, gw, sw, gx, sx); return true;
+    case 2 * 8 + 2: *rc = launch_pair<LdsWide, LdsWide>(rt, gw, sw, gx, sx); return true;
+    case 3 * 8 + 3: *rc = launch_pair<LdsMid, LdsMid>(rt, gw, sw, gx, sx); return true;
+    case 3 * 8 + 4: *rc = launch_pair<LdsMid, LdsSmall>(rt, gw, sw, gx, sx); return true;
+    case 4 * 8 + 3: *rc = launch_pair<LdsSmall, LdsMid>(rt, gw, sw, gx, sx); return true;
+    case 4 * 8 + 4: *rc = launch_pair<LdsSmall, LdsSmall>(rt, gw, sw, gx, sx); return true;
+    default: return false;
+  }
 }
 
 bool aligned16(const void* p) {
@@ -1850,6 +1991,21 @@ using namespace lmp_hip;
 
 namespace {
 
+// Access widths a product allows: g.vec_out (C, and the bias, take 128-bit
+// stores), *vec (128-bit panel loads: 16-byte rows and a contiguous extent
+// that is a multiple of four), *direct_ok (the register-direct kernel, whose
+// float4 C stores need 16-byte C rows when B is untransposed, and a float4
+// bias read when there is a bias).
+void gemm_flags(GemmArgs& g, int trans_a, int trans_b, bool* vec, bool* direct_ok) {
+  g.vec_out = g.n % 4 == 0 && g.ldc % 4 == 0 && aligned16(g.c) && (!g.bias || aligned16(g.bias));
+  const int a_contig = trans_a ? g.m : g.k;
+  const int b_contig = trans_b ? g.k : g.n;
+  *vec = g.lda % 4 == 0 && g.ldb % 4 == 0 && a_contig % 4 == 0 && b_contig % 4 == 0 &&
+         aligned16(g.a) && aligned16(g.b);
+  *direct_ok = *vec && (trans_b || (g.ldc % 4 == 0 && aligned16(g.c) &&
+                                    (!g.bias || aligned16(g.bias))));
+}
+
 int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
                    const float* a, size_t lda, const float* b, size_t ldb,
                    const float* bias, float* c, size_t ldc, int accumulate, int relu = 0,
@@ -1886,17 +2042,8 @@ int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
   g.relu = bias && relu ? 1 : 0;
   g.colsum = colsum;
   g.colsum_acc = colsum_acc ? 1 : 0;
-  g.vec_out = n % 4 == 0 && ldc % 4 == 0 && aligned16(c) && (!bias || aligned16(bias));
-  // 128-bit panel loads need 16-byte rows and a contiguous extent that is a
-  // multiple of four.
-  const size_t a_contig = trans_a ? m : k;
-  const size_t b_contig = trans_b ? k : n;
-  const bool vec = lda % 4 == 0 && ldb % 4 == 0 && a_contig % 4 == 0 &&
-                   b_contig % 4 == 0 && aligned16(a) && aligned16(b);
-  // The direct kernel's float4 C stores (trans_b == 0) need 16-byte C rows.
-  // (and a float4 bias read when there is a bias).
-  const bool direct_ok =
-      vec && (trans_b || (ldc % 4 == 0 && aligned16(c) && (!bias || aligned16(bias))));
+  bool vec = false, direct_ok = false;
+  gemm_flags(g, trans_a, trans_b, &vec, &direct_ok);
   bool* cd = colsum_done;
   if (!trans_a && !trans_b) return launch_gemm<false, false>(rt, g, vec, direct_ok, ws, cd);
   if (!trans_a && trans_b) return launch_gemm<false, true>(rt, g, vec, direct_ok, ws, cd);
@@ -2092,6 +2239,15 @@ extern "C" int lmp_k_linear_backward_f32(size_t batch, size_t in, size_t out, co
   gx.accumulate = dx_accumulate ? 1 : 0;
   LMP_RUNTIME_OR_FAIL(rt);
   if (tiny16(rt, gw) && tiny16(rt, gx)) return launch_tiny_linear_backward(rt, gw, gx);
+  // Larger products on LDS tiles of one workgroup size: dW (with db) and dX in
+  // one launch.
+  {
+    bool vec_w = false, vec_x = false, direct_w = false, direct_x = false;
+    gemm_flags(gw, 1, 0, &vec_w, &direct_w);
+    gemm_flags(gx, 0, 1, &vec_x, &direct_x);
+    int rc = LMP_OK;
+    if (try_linear_backward_pair(rt, gw, vec_w, direct_w, gx, vec_x, direct_x, &rc)) return rc;
+  }
   // dW and db first: that call refuses before it launches anything, and dX
   // (a plain GEMM) can then only fail by running out of memory.
   const int rc = lmp_k_gemm_colsum_f32(1, 0, in, out, batch, x, ldx, g, ldg, dw, lddw,

@@ -651,10 +651,14 @@ def test_host_device_round_trip_every_byte(hip, nbytes):
 
 
 # (batch, in, out): the README MLP's two layers, odd and single-row sizes in
-# the one-launch range, then a product just past it (K > 512) and config 4's
-# last layer, which take the two separate launches.
+# the one-launch range, then a product just past it (K > 512) on two
+# launches; config 4's layers and two more shapes whose dW and dX both take
+# LDS tiles of one workgroup size, so they share one launch (dW on 128 x 128
+# and dX on 128 x 64 tiles; 256 x 256 and 256 x 128 split four ways; 128 x 64
+# both split; 256 x 128 both split).
 @pytest.mark.parametrize("batch,fan_in,fan_out", [
-    (32, 64, 10), (32, 256, 64), (7, 33, 5), (1, 3, 1), (40, 17, 600), (512, 4096, 1000)],
+    (32, 64, 10), (32, 256, 64), (7, 33, 5), (1, 3, 1), (40, 17, 600), (512, 4096, 1000),
+    (512, 4096, 4096), (768, 1024, 1000), (4096, 2048, 2048)],
     ids=str)
 @pytest.mark.parametrize("acc", [False, True], ids=["write", "accumulate"])
 def test_linear_backward_equals_separate_calls(hip, batch, fan_in, fan_out, acc):
@@ -684,8 +688,14 @@ def test_linear_backward_equals_separate_calls(hip, batch, fan_in, fan_out, acc)
                                           fan_out, int(acc), db.ptr, int(acc)))
     for got, ref in ((dx, dx_ref), (dw, dw_ref), (db, db_ref)):
         assert np.array_equal(got.numpy().view(np.uint32), ref.numpy().view(np.uint32))
-    want = x_np.T.astype(np.float64) @ g_np.astype(np.float64) + (dw0 if acc else 0.0)
-    assert rel_err(dw.numpy(), want) <= 1e-5
+    rows = np.arange(fan_in) if fan_in <= 1024 else rng.choice(fan_in, 64, replace=False)
+    want = x_np.T[rows].astype(np.float64) @ g_np.astype(np.float64) + (dw0[rows] if acc else 0.0)
+    assert rel_err(dw.numpy()[rows], want) <= 1e-5
+    xrows = np.arange(batch) if batch <= 1024 else rng.choice(batch, 64, replace=False)
+    want = g_np[xrows].astype(np.float64) @ w_np.astype(np.float64).T + (dx0[xrows] if acc else 0.0)
+    assert rel_err(dx.numpy()[xrows], want) <= 1e-4
+    want = g_np.astype(np.float64).sum(0) + (db0 if acc else 0.0)
+    assert rel_err(db.numpy(), want) <= 1e-5
     # null outputs are rejected, an empty batch is unsupported
     assert L.lmp_k_linear_backward_f32(batch, fan_in, fan_out, x.ptr, fan_in, w.ptr, fan_out,
                                        g.ptr, fan_out, None, fan_in, 0, dw.ptr, fan_out, 0,
