@@ -87,6 +87,7 @@ struct GemmArgs {
   int colsum_acc;
   const float* bmask;  // tiny kernel, B untransposed: B[k][j] counts only where
                        // 0 < bmask[k][j] < +inf (ReLU's backward mask; same layout as B)
+  int walk_a, walk_b;  // short-K kernel: 0, or the XCD-block grid walk_a x walk_b
 };
 
 // ReLU's backward mask on a gradient value: ClampBackward's strict bounds for
@@ -321,12 +322,26 @@ __global__ __launch_bounds__(256) void fold_splits(float* __restrict__ c,
 // The same fold, four adjacent columns per lane (n and ldc multiples of four,
 // C and the bias 16-byte aligned), the split loads issued four at a time; the
 // adds keep split order, so the result equals fold_splits bit for bit.
+// col_blocks == 0: lanes take consecutive float4s of C.  col_blocks > 0 (a
+// grid of col_blocks x ceil(m / 8) workgroups): workgroup b takes rows
+// 8 (b / col_blocks) .. + 7 of the 128 columns of block b % col_blocks, the
+// block a split-K workgroup of the same index mod 8 wrote, so the partials
+// are read on the XCD whose L2 holds them.
 __global__ __launch_bounds__(256) void fold_splits4(float* __restrict__ c,
                                                     const float* __restrict__ part,
                                                     int m, int n, int ldc,
                                                     int splits, int accumulate,
-                                                    const float* __restrict__ bias, int relu) {
-  const int64_t i4 = int64_t(blockIdx.x) * 256 + threadIdx.x;
+                                                    const float* __restrict__ bias, int relu,
+                                                    int col_blocks) {
+  int64_t i4;
+  if (col_blocks > 0) {
+    const int blk = int(blockIdx.x) % col_blocks, sub = int(blockIdx.x) / col_blocks;
+    const int r = sub * 8 + int(threadIdx.x >> 5), cl = blk * 128 + 4 * int(threadIdx.x & 31);
+    if (r >= m || cl >= n) return;
+    i4 = (int64_t(r) * n + cl) / 4;
+  } else {
+    i4 = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  }
   const int64_t mn4 = int64_t(m) * n / 4;
   if (i4 >= mn4) return;
   const int64_t i = 4 * i4;
@@ -375,13 +390,16 @@ struct Workspace {
 bool aligned16(const void* p);
 
 // Adds the split-K partials into C (with the epilogue of the final output).
+// col_blocks > 0: the partials come in blocks of 128 columns whose splits ran
+// on one XCD (see fold_splits4).
 int launch_fold(Runtime* rt, float* c, const float* part, int m, int n, int ldc, int splits,
-                int accumulate, const float* bias, int relu) {
+                int accumulate, const float* bias, int relu, int col_blocks = 0) {
   const int64_t mn = int64_t(m) * n;
   if (n % 4 == 0 && ldc % 4 == 0 && aligned16(c) && aligned16(part) &&
       (!bias || aligned16(bias))) {
-    hipLaunchKernelGGL(fold_splits4, dim3(uint32_t((mn / 4 + 255) / 256)), dim3(256), 0,
-                       rt->stream, c, part, m, n, ldc, splits, accumulate, bias, relu);
+    const int64_t grid = col_blocks > 0 ? int64_t(col_blocks) * ((m + 7) / 8) : (mn / 4 + 255) / 256;
+    hipLaunchKernelGGL(fold_splits4, dim3(uint32_t(grid)), dim3(256), 0, rt->stream, c, part, m,
+                       n, ldc, splits, accumulate, bias, relu, col_blocks);
   } else {
     hipLaunchKernelGGL(fold_splits, dim3(uint32_t((mn + 255) / 256)), dim3(256), 0,
                        rt->stream, c, part, m, n, ldc, splits, accumulate, bias, relu);
@@ -1515,9 +1533,28 @@ __global__ __launch_bounds__(256, 2) void gemm_tn_short(GemmArgs g) {
     }
   };
 
-  int t = int(blockIdx.x);
-  if (t < ntiles) issue(t, 0);
-  for (int it = 0; t < ntiles; ++it, t += int(gridDim.x)) {
+  // Tile (row-major index) at walk position i of this workgroup, or -1 past
+  // the end.  Plain walk: tiles blockIdx.x + i * gridDim.x.  XCD-blocked walk
+  // (walk_a x walk_b > 0, gridDim.x a multiple of 8, the tile grid split into
+  // walk_a x walk_b equal blocks): workgroup b takes block b % 8 (workgroups
+  // reach the eight XCDs round-robin), walking it row-major from b / 8 in
+  // steps of gridDim.x / 8, so each XCD's L2 sees one block's A and B panels
+  // rather than every row of A.  Either way every tile is taken exactly once.
+  auto tile_at = [&](int i) -> int {
+    if (g.walk_a == 0) {
+      const int t = int(blockIdx.x) + i * int(gridDim.x);
+      return t < ntiles ? t : -1;
+    }
+    const int bm = g.tiles_m / g.walk_a, bn = g.tiles_n / g.walk_b;
+    const int x = int(blockIdx.x) % 8;
+    const int l = int(blockIdx.x) / 8 + i * (int(gridDim.x) / 8);
+    if (l >= bm * bn) return -1;
+    const int row = (x / g.walk_b) * bm + l / bn, col = (x % g.walk_b) * bn + l % bn;
+    return row * g.tiles_n + col;
+  };
+  int t = tile_at(0);
+  if (t >= 0) issue(t, 0);
+  for (int it = 0; t >= 0; ++it) {
     const int stage = it & 1;
     const int m0 = (t / g.tiles_n) * BM, n0 = (t % g.tiles_n) * BN;
     // This tile's panels have landed (and the previous tile's stores have
@@ -1525,7 +1562,8 @@ __global__ __launch_bounds__(256, 2) void gemm_tn_short(GemmArgs g) {
     // used the other stage, so it may be refilled.
     wait_vmcnt<0>();
     asm volatile("s_barrier" ::: "memory");
-    if (t + int(gridDim.x) < ntiles) issue(t + int(gridDim.x), stage ^ 1);
+    const int t_next = tile_at(it + 1);
+    if (t_next >= 0) issue(t_next, stage ^ 1);
 
     const float* sa = smem + stage * STAGE;
     const float* sb = sa + A_PANEL;
@@ -1599,6 +1637,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tn_short(GemmArgs g) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       }
     }
+    t = t_next;
   }
 }
 
@@ -1734,8 +1773,11 @@ int launch_direct(Runtime* rt, const GemmArgs& g0, const Workspace& ws, int spli
                      d);
   LMP_LAUNCH_CHECK("gemm_direct");
   if (splits > 1) {
+    // The splits of a column block ran on one XCD when the block count is a
+    // multiple of eight (workgroups reach the XCDs round-robin).
+    const int cb = d.n_blocks % 8 == 0 && kDirectN == 128 ? d.n_blocks : 0;
     const int frc = launch_fold(rt, g0.c, part, g0.m, g0.n, g0.ldc, splits, g0.accumulate,
-                                g0.bias, g0.relu);
+                                g0.bias, g0.relu, cb);
     ws.give(part);  // stream-ordered: the fold reads it first
     if (frc != LMP_OK) return frc;
   }
@@ -1750,6 +1792,22 @@ int launch_short(Runtime* rt, GemmArgs g, bool* colsum_done) {
   const int64_t tiles = int64_t(g.tiles_m) * g.tiles_n;
   if (g.colsum && colsum_done) *colsum_done = true;
   const uint32_t grid = uint32_t(std::min<int64_t>(tiles, 2 * int64_t(rt->cu_count)));
+  // XCD-blocked walk when the tiles split into eight equal blocks: the block
+  // shape that gives each XCD the fewest A and B panels to read.
+  g.walk_a = g.walk_b = 0;
+  if (grid % 8 == 0) {
+    int64_t best = 0;
+    for (int a = 1; a <= 8; a *= 2) {
+      const int b = 8 / a;
+      if (g.tiles_m % a != 0 || g.tiles_n % b != 0) continue;
+      const int64_t panels = int64_t(g.tiles_m / a) * kShortBM + int64_t(g.tiles_n / b) * kShortBN;
+      if (best == 0 || panels < best) {
+        best = panels;
+        g.walk_a = a;
+        g.walk_b = b;
+      }
+    }
+  }
   hipLaunchKernelGGL(gemm_tn_short, dim3(grid), dim3(256), 0, rt->stream, g);
   LMP_LAUNCH_CHECK("gemm_tn_short");
   return LMP_OK;
