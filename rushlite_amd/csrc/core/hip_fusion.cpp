@@ -19,10 +19,10 @@
 // with no source text built.  On a miss the region is turned into HIP source
 // specialised to its shape: the layout is coalesced to the fewest dims, and
 // when it reduces to rows x cols with each leaf contiguous or broadcast along
-// the row, each lane of a one-shot grid produces one float4 (a workgroup owns
-// a contiguous 4 KiB output tile) from 128-bit loads and stores it with a
-// nontemporal hint; otherwise it decomposes the flat index with compile-time
-// extents.  Kernels launch on the library stream without a
+// the row, each lane of a one-shot grid produces one float4 (a one-wave
+// workgroup owns a contiguous 1 KiB output tile) from 128-bit loads and
+// stores it, with the nontemporal hint for large outputs; otherwise it
+// decomposes the flat index with compile-time extents.  Kernels launch on the library stream without a
 // device synchronisation (the reference synchronises every launch,
 // nvrtc_backend.cpp:135-141).
 #include <cstdio>
@@ -42,7 +42,13 @@ namespace {
 constexpr size_t kMaxNodes = 96;
 constexpr size_t kMaxLeaves = 16;
 constexpr size_t kMaxOutputs = 16;  // interior nodes stored beside the root
-constexpr int kBlock = 256;
+// Threads per workgroup of every fused kernel: one wave.  One-wave
+// workgroups spread a one-shot grid's tiles more finely over the CUs than
+// 256-thread ones: config 1's c = a*a + b over [8192,8192] (256 MiB read and
+// written per call, rotating inputs) 6.45-6.46 -> 6.67-6.69 TB/s on one
+// MI355X, the other fused kernels unchanged.  A row kernel then runs one row
+// per workgroup.
+constexpr int kBlock = 64;
 
 // LMP_FUSION_LOG=1 prints one line per fused region (and why nodes were cut
 // out of it) to stderr, to see how a graph splits into kernels.
@@ -531,7 +537,7 @@ constexpr size_t kStreamBytes = size_t(256) << 20;
 constexpr size_t kStreamStoreBytes = size_t(128) << 20;
 
 // The body of a float4 (vec) region: block `block` owns output float4s
-// [256 * block, 256 * block + 256) (one-shot).
+// [kBlock * block, kBlock * block + kBlock) (one-shot).
 void emit_vec_body(std::ostringstream& os, const Region& r, const Plan& p, const Names& nm,
                    const std::string& block, bool stream_stores = false) {
   const size_t nl = r.leaves.size();
@@ -622,7 +628,7 @@ std::string codegen(const Region& r, const Plan& p, const std::string& name, boo
 }
 
 // The body of an indexed region run one-shot: block `block` owns elements
-// [256 * block, 256 * block + 256), each decomposed into leaf offsets with
+// [kBlock * block, kBlock * block + kBlock), each decomposed into leaf offsets with
 // compile-time extents and strides.
 void emit_indexed_body(std::ostringstream& os, const Region& r, const Plan& p, const char* T,
                        const Names& nm, const std::string& block) {
