@@ -1836,12 +1836,17 @@ int launch_rows(Runtime* rt, const GemmArgs& g0) {
   return LMP_OK;
 }
 
-// Tile choice (measured on MI355X, fp32): the tiny kernel for small
-// latency-bound products (K <= 512, at most 2^21 multiply-adds); 128x128 whenever its tiles cover
-// the CUs; with a short K (<= 2048) and too few 128x128 tiles, 64x64 tiles
-// without a split (no partial round trip) win; otherwise 128x128 with split
-// K.  M <= 64 uses 32x256 tiles, and M <= 32 the register-direct kernel when
-// its alignment requirements hold.
+// Kernel choice (measured on MI355X, fp32), in order: the tiny kernel for
+// small latency-bound products (K <= 512, at most 2^21 multiply-adds); the
+// persistent short-K kernel (A transposed, K <= 32); whole rows of B per
+// workgroup (M <= 32, B transposed, a 32-column block per CU); the
+// register-direct kernel (M <= 32) and 32 x 256 tiles (M <= 64); then, with
+// 16-byte operand rows, the LDS-DMA configurations (256 x 256 when they cover
+// the CUs, 256 x 128 split for M >= 512, N >= 2048, K >= 2048, 128 x 64 split
+// when 128 x 128 tiles would not cover the CUs); otherwise 64 x 64 register
+// tiles without a split for a short K (<= 2048) with too few 128 x 128 tiles,
+// else 128 x 128 (on LDS-DMA tiles when the rows allow) with split K.  Single
+// and paired launches take their kernel from this one function.
 enum class Route { Tiny, Short, Rows, Direct, Skinny, Big, Wide, Mid, Small64, Large };
 
 template <bool TA, bool TB>
