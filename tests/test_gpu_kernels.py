@@ -705,6 +705,47 @@ def test_linear_backward_equals_separate_calls(hip, batch, fan_in, fan_out, acc)
                                        db.ptr, 0) == hip.ERR_UNSUPPORTED
 
 
+# Seeded random Linear shapes past the tiny range with 16-byte rows, so that
+# dW and dX both take LDS tiles (of one workgroup size or not): the paired
+# launch, or the two calls, must give the bits of the separate calls.
+_PAIR_RNG = np.random.default_rng(20260)
+PAIR_SHAPES = [(int(_PAIR_RNG.integers(130, 2700)), 4 * int(_PAIR_RNG.integers(129, 1026)),
+                4 * int(_PAIR_RNG.integers(129, 1026))) for _ in range(8)]
+
+
+@pytest.mark.parametrize("batch,fan_in,fan_out", PAIR_SHAPES, ids=str)
+def test_linear_backward_random_shapes_equal_separate_calls(hip, batch, fan_in, fan_out):
+    L = hip.lib()
+    rng = np.random.default_rng(batch + 3 * fan_in + 7 * fan_out)
+    x_np = (rng.standard_normal((batch, fan_in)) * 0.1).astype(np.float32)
+    w_np = (rng.standard_normal((fan_in, fan_out)) * 0.1).astype(np.float32)
+    g_np = (rng.standard_normal((batch, fan_out)) * 0.1).astype(np.float32)
+    x, w, g = up(hip, x_np), up(hip, w_np), up(hip, g_np)
+    for acc in (0, 1):
+        dx0 = rng.standard_normal((batch, fan_in)).astype(np.float32)
+        dw0 = rng.standard_normal((fan_in, fan_out)).astype(np.float32)
+        db0 = rng.standard_normal(fan_out).astype(np.float32)
+        dx_ref, dw_ref, db_ref = up(hip, dx0), up(hip, dw0), up(hip, db0)
+        hip.check(L.lmp_k_gemm_f32(0, 1, batch, fan_in, fan_out, g.ptr, fan_out, w.ptr, fan_out,
+                                   dx_ref.ptr, fan_in, acc))
+        hip.check(L.lmp_k_gemm_colsum_f32(1, 0, fan_in, fan_out, batch, x.ptr, fan_in, g.ptr,
+                                          fan_out, dw_ref.ptr, fan_out, acc, db_ref.ptr, acc))
+        dx, dw, db = up(hip, dx0), up(hip, dw0), up(hip, db0)
+        hip.check(L.lmp_k_linear_backward_f32(batch, fan_in, fan_out, x.ptr, fan_in, w.ptr,
+                                              fan_out, g.ptr, fan_out, dx.ptr, fan_in, acc, dw.ptr,
+                                              fan_out, acc, db.ptr, acc))
+        for got, ref in ((dx, dx_ref), (dw, dw_ref), (db, db_ref)):
+            assert np.array_equal(got.numpy().view(np.uint32), ref.numpy().view(np.uint32)), acc
+    # the last (accumulating) call against float64 on sampled rows
+    rows = rng.choice(fan_in, 48, replace=False)
+    want = x_np.T[rows].astype(np.float64) @ g_np.astype(np.float64) + dw0[rows]
+    assert rel_err(dw.numpy()[rows], want) <= 1e-5
+    xrows = rng.choice(batch, 48, replace=False)
+    want = g_np[xrows].astype(np.float64) @ w_np.astype(np.float64).T + dx0[xrows]
+    assert rel_err(dx.numpy()[xrows], want) <= 1e-5
+    assert rel_err(db.numpy(), g_np.astype(np.float64).sum(0) + db0) <= 1e-5
+
+
 # Strided B past the one-launch range: the column sums cannot ride in the
 # GEMM (B transposed, or K split for few tiles), so they take the strided
 # column-sum kernel after it.  (600, 96, 80) is a Linear's weight gradient at
