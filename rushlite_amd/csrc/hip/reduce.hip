@@ -136,7 +136,18 @@ __global__ __launch_bounds__(kBlock) void row_reduce_wave(
     a2 = R::combine(a2, x2);
     a3 = R::combine(a3, x3);
   }
-  for (; j < len; j += 64) a0 = R::combine(a0, src[j]);
+  // At most three elements per lane remain (j + 192 >= len): their loads go
+  // out together, then a0 takes them in index order as a loop would.
+  {
+    const bool t0 = j < len, t1 = j + 64 < len, t2 = j + 128 < len;
+    T y0 = a0, y1 = a0, y2 = a0;
+    if (t0) y0 = src[j];
+    if (t1) y1 = src[j + 64];
+    if (t2) y2 = src[j + 128];
+    if (t0) a0 = R::combine(a0, y0);
+    if (t1) a0 = R::combine(a0, y1);
+    if (t2) a0 = R::combine(a0, y2);
+  }
   T acc = R::combine(R::combine(a0, a1), R::combine(a2, a3));
   acc = wave_reduce<OP, T>(acc);
   if (lane == 0) out[row] = acc;
@@ -163,7 +174,18 @@ __global__ __launch_bounds__(kBlock) void row_reduce_wave_f32(
     a2 = combine4<OP>(a2, x2);
     a3 = combine4<OP>(a3, x3);
   }
-  for (; j < len4; j += 64) a0 = combine4<OP>(a0, src[j]);
+  // At most three float4 per lane remain (j + 192 >= len4): their loads go
+  // out together, then a0 takes them in index order as a loop would.
+  {
+    const bool t0 = j < len4, t1 = j + 64 < len4, t2 = j + 128 < len4;
+    v4f y0 = id, y1 = id, y2 = id;
+    if (t0) y0 = src[j];
+    if (t1) y1 = src[j + 64];
+    if (t2) y2 = src[j + 128];
+    if (t0) a0 = combine4<OP>(a0, y0);
+    if (t1) a0 = combine4<OP>(a0, y1);
+    if (t2) a0 = combine4<OP>(a0, y2);
+  }
   const v4f a = combine4<OP>(combine4<OP>(a0, a1), combine4<OP>(a2, a3));
   float v = R::combine(R::combine(a.x, a.y), R::combine(a.z, a.w));
   v = wave_reduce<OP, float>(v);
