@@ -183,9 +183,11 @@ void lcpu_reduce_f32(int op, float* out, const float* in, int ndim,
   for (int d = axis + 1; d < ndim; ++d) outer *= shape[d];
   const int64_t len = shape[axis];
   const int64_t inner = outer * len;
-  int64_t total = 1;
-  for (int d = 0; d < ndim; ++d) total *= shape[d];
-  const int64_t nout = len == 0 ? 0 : total / len;
+  /* One output per position of the other axes (reduct.cpp:26 runs over
+   * out().numel()): an empty axis leaves each output at the identity. */
+  int64_t nout = 1;
+  for (int d = 0; d < ndim; ++d)
+    if (d != axis) nout *= shape[d];
   const float id = red_identity(op);
 #pragma omp parallel for
   for (int64_t i = 0; i < nout; ++i) {

@@ -718,6 +718,29 @@ def test_captured_reductions_equal_eager(rsl, op, shape):
     assert np.array_equal(got.view(np.uint32), eager.view(np.uint32))
 
 
+@pytest.mark.parametrize("capture", [False, True])
+def test_empty_tensors(rsl, oracle, capture):
+    """Variables with a zero extent, eager and under capture_on: elementwise
+    results are empty, a reduction over the empty axis gives the identity per
+    output as the oracle (cpu/reduct.cpp:14-19), over another axis an empty
+    result, and a product with K = 0 gives zeros."""
+    e_np = np.zeros((3, 0), np.float32)
+    e = V(rsl, e_np)
+    with rsl.capture_on(capture):
+        elem = e * 2.0 + 1.0
+        reds = {op: getattr(rsl, op)(e * 2.0 + 1.0, 1) for op in ("sum", "max", "min", "prod")}
+        across = rsl.sum(e + 1.0, 0)
+        mm = rsl.matmul(e, V(rsl, np.zeros((0, 4), np.float32)))
+    assert list(elem.shape) == [3, 0] and elem.numpy().size == 0
+    for op, r in reds.items():
+        want = oracle.reduce(op, e_np, 1)
+        got = r.numpy()
+        assert got.shape == want.shape and np.array_equal(got.view(np.uint32),
+                                                          want.view(np.uint32)), op
+    assert list(across.shape) == [1, 0]
+    assert np.array_equal(mm.numpy(), np.zeros((3, 4), np.float32))
+
+
 def test_loss_row_chain_fuses(rsl):
     """The README loss's row part, sum(-y * log(p + 1e-3), 1), is one kernel."""
     rng = np.random.default_rng(8)

@@ -272,6 +272,55 @@ def test_reduce_ones_column_is_exact(hip):
     ones.free()
 
 
+@pytest.mark.parametrize("shape,axis", [((3, 0, 2), 1), ((0, 4), 0), ((4, 0), 1), ((0,), 0)],
+                         ids=str)
+def test_reduce_empty_axis_writes_identity(hip, oracle, shape, axis):
+    """A reduction over an empty axis writes the identity to every output
+    (cpu/reduct.cpp:14-19 folds nothing into kIdentity), bit for bit as the
+    oracle, sign of zero included; the input pointer may then be null."""
+    L = hip.lib()
+    outer = int(np.prod(shape[:axis], dtype=np.int64))
+    inner = int(np.prod(shape[axis + 1:], dtype=np.int64))
+    oshape = list(shape)
+    oshape[axis] = 1
+    for op in ("sum", "max", "min", "prod"):
+        out = up(hip, np.full(oshape, np.nan, np.float32))
+        hip.check(L.lmp_k_reduce(hip.RED[op], hip.FLOAT32, out.ptr, None, outer, 0, inner))
+        want = oracle.reduce(op, np.zeros(shape, np.float32), axis)
+        assert np.array_equal(out.numpy().view(np.uint32), want.view(np.uint32)), op
+
+
+def test_empty_extents_write_nothing(hip, oracle):
+    """Zero-extent calls through the C ABI succeed and leave memory as it was:
+    elementwise, fill, cast and add_inplace of 0 elements, reductions with no
+    outer or inner position, GEMMs with m or n = 0, copies of 0 bytes.  A GEMM
+    with k = 0 writes the empty product, zeros (the oracle's), or leaves C as it
+    is when accumulating."""
+    L = hip.lib()
+    pattern = np.arange(16, dtype=np.float32) + 0.5
+    g, src = up(hip, pattern), up(hip, pattern[::-1])
+    d, _ = hip.make_bcast((0, 4), (1, 4))
+    hip.check(L.lmp_k_binary(hip.BIN["add"], hip.FLOAT32, g.ptr, src.ptr, src.ptr, C.byref(d),
+                             0.0, 0.0))
+    hip.check(L.lmp_k_unary(hip.UN["exp"], hip.FLOAT32, g.ptr, src.ptr, 0, 0.0, 0.0))
+    hip.check(L.lmp_k_fill(hip.FLOAT32, g.ptr, 0, 7.0))
+    hip.check(L.lmp_k_cast(hip.FLOAT32, hip.FLOAT64, g.ptr, src.ptr, 0))
+    hip.check(L.lmp_k_add_inplace(hip.FLOAT32, g.ptr, src.ptr, 0))
+    for outer, length, inner in ((0, 5, 3), (4, 5, 0), (0, 0, 0)):
+        hip.check(L.lmp_k_reduce(hip.RED["sum"], hip.FLOAT32, g.ptr, src.ptr, outer, length,
+                                 inner))
+    for m, n in ((0, 4), (4, 0)):
+        hip.check(L.lmp_k_gemm_f32(0, 0, m, n, 3, src.ptr, 3, src.ptr, 4, g.ptr, 4, 0))
+    hip.check(L.lmp_rt_memcpy_d2d(g.ptr, src.ptr, 0))
+    hip.check(L.lmp_rt_memcpy_h2d(g.ptr, pattern[::-1].copy().ctypes.data, 0))
+    assert np.array_equal(g.numpy(), pattern)
+    hip.check(L.lmp_k_gemm_f32(0, 0, 4, 4, 0, src.ptr, 1, src.ptr, 4, g.ptr, 4, 1))
+    assert np.array_equal(g.numpy(), pattern)
+    hip.check(L.lmp_k_gemm_f32(0, 0, 4, 4, 0, src.ptr, 1, src.ptr, 4, g.ptr, 4, 0))
+    want = oracle.matmul(np.zeros((4, 0), np.float32), np.zeros((0, 4), np.float32))
+    assert np.array_equal(g.numpy().reshape(4, 4).view(np.uint32), want.view(np.uint32))
+
+
 # M <= 32 with 16-byte rows takes the register-direct kernel: (32, 132, 1028)
 # and (20, 132, 1028) split K with a ragged last split and a partial column
 # block, (4, 260, 2048) splits K eight ways, (1, 8, 8) is a single row.

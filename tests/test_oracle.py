@@ -347,6 +347,24 @@ def test_reduce_vs_numpy(oracle, axis):
     np.testing.assert_allclose(p, tp, rtol=1e-5)
 
 
+EMPTY_AXIS_CASES = [((3, 0, 2), 1), ((0, 4), 0), ((4, 0), 1), ((0,), 0), ((2, 0, 0), 1)]
+
+
+@pytest.mark.parametrize("shape,axis", EMPTY_AXIS_CASES, ids=str)
+def test_reduce_empty_axis_gives_identity(oracle, shape, axis):
+    """cpu/reduct.cpp:14-19 folds nothing into OpFn::kIdentity and writes it to
+    each of out().numel() outputs (reduct.cpp:45-46): 0, lowest(), max(), 1.
+    Every output is checked, so an unwritten (garbage) output fails."""
+    f32 = np.finfo(np.float32)
+    oshape = list(shape)
+    oshape[axis] = 1
+    for op, ident in (("sum", 0.0), ("max", -f32.max), ("min", f32.max), ("prod", 1.0)):
+        got = oracle.reduce(op, np.zeros(shape, np.float32), axis)
+        assert got.shape == tuple(oshape)
+        assert np.array_equal(got, np.full(oshape, ident, np.float32)), op
+        assert not np.signbit(got).any() or op == "max", op
+
+
 def test_matmul_order_and_value(oracle):
     rng = np.random.default_rng(4)
     a = rng.standard_normal((5, 11), dtype=np.float32)
