@@ -36,3 +36,26 @@ def rel_err(got, want) -> float:
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     return float(np.max(np.abs(got - want)) / (np.max(np.abs(want)) + 1e-30))
+
+
+def special_rows(length, rng):
+    """Rows of special values for max/min/sum/prod: all -inf, NaN among
+    values, all NaN, +inf among values, all +0, all -0, +0 and -0 both at the
+    maximum (and the minimum) among negatives (positives), random values."""
+    rows = np.empty((9, length), np.float32)
+    rows[0] = -np.inf
+    rows[1] = rng.standard_normal(length)
+    rows[1, ::5] = np.nan
+    rows[2] = np.nan
+    rows[3] = rng.standard_normal(length)
+    rows[3, length // 2] = np.inf
+    rows[4] = 0.0
+    rows[5] = -0.0
+    rows[6] = -1.0 - np.abs(rng.standard_normal(length))
+    rows[6, 1::7] = 0.0
+    rows[6, 0::11] = -0.0
+    rows[7] = 1.0 + np.abs(rng.standard_normal(length))
+    rows[7, 1::7] = 0.0
+    rows[7, 0::11] = -0.0
+    rows[8] = rng.standard_normal(length)
+    return rows

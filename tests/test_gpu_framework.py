@@ -15,7 +15,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from _helpers import assert_within_ulp, rel_err
+from _helpers import assert_within_ulp, rel_err, special_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -716,6 +716,24 @@ def test_captured_reductions_equal_eager(rsl, op, shape):
     got = r.numpy()
     assert rsl._stats()["fused_launches"] - s0["fused_launches"] == 1
     assert np.array_equal(got.view(np.uint32), eager.view(np.uint32))
+
+
+@pytest.mark.parametrize("length", [37, 1000])
+def test_captured_max_min_special_values_equal_eager(rsl, length):
+    """max/min over the last axis of rows holding infinities, NaN, signed zeros
+    (both signs tying at the extreme included) and all -inf: the fused row
+    kernel gives the eager kernel's bits, as both combine in one order."""
+    a_np = special_rows(length, np.random.default_rng(length))
+    a = V(rsl, a_np)
+    for op in ("max", "min"):
+        fn = getattr(rsl, op)
+        eager = fn(a * 1.0, 1).numpy()
+        s0 = rsl._stats()
+        with rsl.no_grad(), rsl.capture_on():
+            r = fn(a * 1.0, 1)
+        got = r.numpy()
+        assert rsl._stats()["fused_launches"] - s0["fused_launches"] == 1
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), op
 
 
 @pytest.mark.parametrize("capture", [False, True])

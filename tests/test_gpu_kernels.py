@@ -13,7 +13,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-from _helpers import assert_within_ulp, rel_err  # noqa: E402
+from _helpers import assert_within_ulp, rel_err, special_rows  # noqa: E402
 
 
 def up(hip, arr):
@@ -270,6 +270,38 @@ def test_reduce_ones_column_is_exact(hip):
     out1 = hip.reduce("sum", ones, 1).numpy()
     assert np.all(out1 == np.float32(n))
     ones.free()
+
+
+@pytest.mark.parametrize("length", [37, 1000, 4096, 16384])
+@pytest.mark.parametrize("axis", [0, 1])
+def test_reduce_special_values(hip, oracle, length, axis):
+    """max/min over rows holding infinities, NaN, signed zeros and all -inf
+    (Lamp3's std::max(acc, x) from lowest() never lets NaN in and leaves an
+    all -inf row at lowest()): bit for bit as the oracle, except the sign of a
+    zero result where +0 and -0 both attain it (row 6 for max, row 7 for min):
+    the CPU loop keeps the first in index order, the GPU's combine tree the
+    first in its order, so only the value (0) is compared there.  sum/prod:
+    NaN where the oracle has NaN (NaN inputs), equal infinities, finite
+    results within 1e-5 under max|d| / max|true|."""
+    rng = np.random.default_rng(length + 7 * axis)
+    rows = special_rows(length, rng)
+    a = np.ascontiguousarray(rows if axis == 1 else rows.T)
+    d = up(hip, a)
+    for op, tie_row in (("max", 6), ("min", 7)):
+        got = hip.reduce(op, d, axis).numpy().reshape(-1)
+        want = oracle.reduce(op, a, axis).reshape(-1)
+        keep = np.arange(want.size) != tie_row
+        assert np.array_equal(got[keep].view(np.uint32), want[keep].view(np.uint32)), op
+        assert got[tie_row] == 0.0 and want[tie_row] == 0.0, op
+    assert oracle.reduce("max", a, axis).reshape(-1)[0] == np.finfo(np.float32).min
+    for op in ("sum", "prod"):
+        src = a if op == "sum" else np.where(np.isfinite(a), 1.0 + 0.001 * a, a).astype(np.float32)
+        got = hip.reduce(op, up(hip, src), axis).numpy().reshape(-1)
+        want = oracle.reduce(op, src, axis).reshape(-1)
+        assert np.array_equal(np.isnan(got), np.isnan(want)), op
+        assert np.array_equal(got[np.isinf(want)], want[np.isinf(want)]), op
+        fin = np.isfinite(want)
+        assert rel_err(got[fin], want[fin]) <= 1e-5, op
 
 
 @pytest.mark.parametrize("shape,axis", [((3, 0, 2), 1), ((0, 4), 0), ((4, 0), 1), ((0,), 0)],
