@@ -38,6 +38,13 @@ def rel_err(got, want) -> float:
     return float(np.max(np.abs(got - want)) / (np.max(np.abs(want)) + 1e-30))
 
 
+# Signed zeros, infinities, NaN, subnormals (down to the smallest, 1e-45),
+# the smallest normal, the extremes and the neighbours of 1.
+SPECIALS = np.array([0.0, -0.0, 1.0, -1.0, 0.5, 3.0, np.inf, -np.inf, np.nan,
+                     1e-45, -1e-45, 1.5e-39, 1.1754944e-38, 1e-20, 3.4e38, -3.4e38,
+                     1.0000001, 0.99999994], np.float32)
+
+
 def special_rows(length, rng):
     """Rows of special values for max/min/sum/prod: all -inf, NaN among
     values, all NaN, +inf among values, all +0, all -0, +0 and -0 both at the

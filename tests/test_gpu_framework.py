@@ -15,7 +15,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from _helpers import assert_within_ulp, rel_err, special_rows
+from _helpers import SPECIALS, assert_within_ulp, rel_err, special_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -716,6 +716,26 @@ def test_captured_reductions_equal_eager(rsl, op, shape):
     got = r.numpy()
     assert rsl._stats()["fused_launches"] - s0["fused_launches"] == 1
     assert np.array_equal(got.view(np.uint32), eager.view(np.uint32))
+
+
+@pytest.mark.parametrize("capture", [False, True])
+def test_binary_special_values_through_variables(rsl, oracle, capture):
+    """Every pair of special values (signed zeros, infinities, NaN, subnormals,
+    extremes, neighbours of 1) through Variable binary ops, eager and inside a
+    fused kernel (a * 1 and b * 1 feed them, exact for every value), bit for
+    bit as the oracle; NaN results compare as NaN only (the sign of a NaN made
+    by 0/0 or inf - inf differs between x86 and the GPU)."""
+    col, row = SPECIALS.reshape(-1, 1), SPECIALS.reshape(1, -1)
+    a, b = V(rsl, col), V(rsl, row)
+    for op in ("add", "sub", "mul", "div", "eq", "ne", "ge", "le", "gt", "lt"):
+        fn = getattr(rsl, op)
+        with rsl.no_grad(), rsl.capture_on(capture):
+            r = fn(a * 1.0, b * 1.0)
+        got = r.numpy()
+        want = oracle.binary(op, col, row)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan), op
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)), op
 
 
 @pytest.mark.parametrize("length", [37, 1000])

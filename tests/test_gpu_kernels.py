@@ -13,7 +13,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-from _helpers import assert_within_ulp, rel_err, special_rows  # noqa: E402
+from _helpers import SPECIALS, assert_within_ulp, rel_err, special_rows  # noqa: E402
 
 
 def up(hip, arr):
@@ -46,6 +46,22 @@ def test_binary_bitexact(hip, oracle, op, sa, sb):
         got = hip.binary(op, up(hip, x), up(hip, y)).numpy()
         assert got.shape == w.shape
         assert np.array_equal(got.view(np.uint32), w.view(np.uint32)), op
+
+
+def test_binary_special_values_bitexact(hip, oracle):
+    """Every pair of special values (signed zeros, infinities, NaN, subnormals
+    down to 1e-45, the extremes, neighbours of 1) through the exact binary ops
+    against the oracle bit for bit: subnormal inputs and results are kept (no
+    flush to zero), x/0 and inf - inf as IEEE has them.  A NaN result compares
+    as NaN only: x86 and the GPU give a new NaN (0/0, inf - inf) different
+    sign bits."""
+    col, row = SPECIALS.reshape(-1, 1), SPECIALS.reshape(1, -1)
+    for op in ("add", "sub", "mul", "div", "eq", "ne", "ge", "le", "gt", "lt", "abs_backward"):
+        want = oracle.binary(op, col, row)
+        got = hip.binary(op, up(hip, col), up(hip, row)).numpy()
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan), op
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)), op
 
 
 def test_clamp_backward_strict(hip, oracle):
