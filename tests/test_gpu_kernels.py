@@ -448,6 +448,33 @@ def test_gemm_config3_square(hip, oracle):
         assert rel_err(got[rows], want) <= 1e-4, (ta, tb)
 
 
+@pytest.mark.parametrize("m,n,k", [(8, 8, 8), (64, 64, 64), (300, 260, 96), (32, 4096, 512),
+                                   (512, 512, 512), (1024, 1024, 1024)], ids=str)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_gemm_subnormal_products_and_specials(hip, m, n, k, ta, tb):
+    """Operands near 1e-20 make every product subnormal (about 1e-40): the
+    MFMA and register paths keep them (no flush to zero), within 1e-4 of the
+    float64 product under max|d| / max|true|.  An inf in A and a NaN in B put
+    NaN and inf in C where the float64 product has them."""
+    rng = np.random.default_rng(zlib.crc32(repr((m, n, k, ta, tb)).encode()))
+    a = (rng.uniform(0.5, 1.5, (k, m) if ta else (m, k)) * 1e-20).astype(np.float32)
+    b = (rng.uniform(0.5, 1.5, (n, k) if tb else (k, n)) * 1e-20).astype(np.float32)
+    got = hip.gemm(up(hip, a), up(hip, b), bool(ta), bool(tb)).numpy()
+    want = (a.T if ta else a).astype(np.float64) @ (b.T if tb else b).astype(np.float64)
+    assert np.all(got != 0.0) and rel_err(got, want) <= 1e-4
+    a2 = rng.standard_normal(a.shape).astype(np.float32)
+    b2 = rng.standard_normal(b.shape).astype(np.float32)
+    a2[0, 0] = np.inf
+    b2[(1, 0) if tb else (0, 1)] = np.nan
+    got2 = hip.gemm(up(hip, a2), up(hip, b2), bool(ta), bool(tb)).numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        want2 = (a2.T if ta else a2).astype(np.float64) @ (b2.T if tb else b2).astype(np.float64)
+    assert np.array_equal(np.isnan(got2), np.isnan(want2))
+    assert np.array_equal(got2[np.isinf(want2)], want2[np.isinf(want2)].astype(np.float32))
+    fin = np.isfinite(want2)
+    assert rel_err(got2[fin], want2[fin]) <= 1e-4
+
+
 def test_gemm_8192_cube(hip):
     """M=N=K=8192 (the north star's 8192-scale matmul) with entries
     N(0, 0.02) in the three Linear orientations: forward X.W, dX = dY.W^T and
