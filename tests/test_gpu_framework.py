@@ -738,6 +738,36 @@ def test_binary_special_values_through_variables(rsl, oracle, capture):
         assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)), op
 
 
+def test_unary_special_values_fused_and_eager(rsl, oracle):
+    """Each unary op over the special values (signed zeros, infinities, NaN,
+    subnormals, extremes, neighbours of 1): the fused kernel gives the eager
+    kernel's bits, NaN results compared as NaN (inside a fused kernel the
+    compiler may fold neg(x * 1) into x * -1, which keeps a NaN's sign where a
+    separate neg flips it; a NaN's sign carries no value); against the oracle
+    NaN at the same positions, neg / abs / sqrt / ReLU bit for bit, the
+    transcendentals within 2 ulp with the same signed zeros."""
+    x = V(rsl, SPECIALS.reshape(1, -1))
+    exact = {"neg": rsl.neg, "abs": rsl.abs, "sqrt": rsl.sqrt}
+    approx = {"exp": rsl.exp, "log": rsl.log, "sin": rsl.sin, "cos": rsl.cos, "tan": rsl.tan}
+    for name, fn in list(exact.items()) + list(approx.items()) + [("clamp", None)]:
+        call = (lambda t: rsl.clamp(t, 0, DBL_MAX)) if name == "clamp" else fn
+        eager = call(x * 1.0).numpy()
+        with rsl.no_grad(), rsl.capture_on():
+            r = call(x * 1.0)
+        fused = r.numpy()
+        fnan = np.isnan(eager)
+        assert np.array_equal(np.isnan(fused), fnan), name
+        assert np.array_equal(fused[~fnan].view(np.uint32), eager[~fnan].view(np.uint32)), name
+        p0, p1 = (0.0, DBL_MAX) if name == "clamp" else (0.0, 0.0)
+        want = oracle.unary(name, SPECIALS.reshape(1, -1), p0, p1)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(eager), nan), name
+        if name in approx:
+            assert_within_ulp(eager[~nan], want[~nan], 2, name)
+        else:
+            assert np.array_equal(eager[~nan].view(np.uint32), want[~nan].view(np.uint32)), name
+
+
 @pytest.mark.parametrize("length", [37, 1000])
 def test_captured_max_min_special_values_equal_eager(rsl, length):
     """max/min over the last axis of rows holding infinities, NaN, signed zeros

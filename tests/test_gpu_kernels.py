@@ -178,6 +178,23 @@ def test_pow_vs_correctly_rounded(hip):
     assert_within_ulp(got, want, 2)
 
 
+def test_pow_special_values(hip, oracle):
+    """pow over every pair of special values plus negative bases with integer
+    and fractional exponents: NaN where the oracle's powf has NaN, infinities
+    and zeros with its signs (C99 Annex F: pow(-0, -1) = -inf, pow(-1, inf) = 1,
+    pow(x, 0) = 1 for NaN x, ...), everything else within 2 ulp."""
+    extra = np.array([-2.0, -0.5, 2.0, 0.25, -3.0, 7.0, 1e-3, 1e30, -1e30], np.float32)
+    vals = np.concatenate([SPECIALS, extra])
+    col, row = vals.reshape(-1, 1), vals.reshape(1, -1)
+    got = hip.binary("pow", up(hip, col), up(hip, row)).numpy()
+    want = oracle.binary("pow", col, row)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    exact = ~nan & (np.isinf(want) | (want == 0.0) | (want == 1.0))
+    assert np.array_equal(got[exact].view(np.uint32), want[exact].view(np.uint32))
+    assert_within_ulp(got[~nan], want[~nan], 2)
+
+
 @pytest.mark.parametrize("shape", [(70000, 5, 4), (65536, 9, 3), (66000, 2, 7),
                                    (70000, 1, 2)], ids=str)
 def test_reduce_outer_beyond_grid_z(hip, oracle, shape):
