@@ -74,6 +74,26 @@ def test_typed_binary_exact(hip, op, dt, sa, sb):
     same(got, T.binary(op, a, b))
 
 
+SPECIALS64 = np.array([0.0, -0.0, 1.0, -1.0, 0.5, 3.0, np.inf, -np.inf, np.nan, 5e-324, -5e-324,
+                       1e-310, 2.2250738585072014e-308, 1e-160, 1.7e308, -1.7e308,
+                       1.0000000000000002, 0.9999999999999999])
+
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "eq", "ne", "ge", "le", "gt", "lt"])
+def test_float64_special_values_exact(hip, op):
+    """Every pair of float64 special values (signed zeros, infinities, NaN,
+    subnormals down to 5e-324, the extremes, the neighbours of 1) bit for bit
+    as the typed oracle; NaN results compare as NaN (x86 and the GPU create
+    NaN with different sign bits)."""
+    col, row = SPECIALS64.reshape(-1, 1), SPECIALS64.reshape(1, -1)
+    got = hip.binary(op, up(hip, col), up(hip, row)).numpy()
+    with np.errstate(all="ignore"):
+        want = T.binary(op, col, row)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.int64), want[~nan].view(np.int64))
+
+
 @pytest.mark.parametrize("dt", INTS + [np.bool_], ids=lambda d: np.dtype(d).name)
 def test_typed_pow_integers(hip, dt):
     """Integer pow is double pow truncated back: exact on exactly
