@@ -767,6 +767,48 @@ STAGE = 16 << 20  # bytes per staging chunk of lmp_rt_memcpy_h2d/d2h
 STAGED_MIN = 4 << 20
 
 
+def test_c_abi_from_several_host_threads(hip, oracle):
+    """Four host threads drive the C ABI at once (ctypes releases the GIL):
+    each allocates, uploads (staged and direct copies), runs a broadcast add,
+    a dim-1 sum and a split-K GEMM whose partials come from the shared pool,
+    downloads and frees, 6 rounds each, with shapes of its own.  Every result
+    equals the oracle's (add, exact) or float64's (sum, GEMM, 1e-5 / 1e-4):
+    the pool, the staging buffers and the one library stream are shared
+    safely."""
+    import threading
+    L = hip.lib()
+    errors = []
+
+    def work(tid):
+        try:
+            rng = np.random.default_rng(100 + tid)
+            for rnd in range(6):
+                m, n = 200 + 37 * tid + rnd, 300 + 11 * tid
+                a = rng.standard_normal((m, n), dtype=np.float32)
+                b = rng.standard_normal((1, n), dtype=np.float32)
+                da, db = up(hip, a), up(hip, b)
+                s = hip.binary("add", da, db).numpy()
+                assert np.array_equal(s.view(np.uint32), oracle.binary("add", a, b).view(np.uint32))
+                r = hip.reduce("sum", da, 1).numpy()
+                assert rel_err(r, a.astype(np.float64).sum(1, keepdims=True)) <= 1e-5
+                x = rng.standard_normal((256, 4096), dtype=np.float32)
+                w = rng.standard_normal((4096, 256), dtype=np.float32)
+                got = hip.gemm(up(hip, x), up(hip, w)).numpy()
+                assert rel_err(got, x.astype(np.float64) @ w.astype(np.float64)) <= 1e-4
+                for buf in (da, db):
+                    buf.free()
+        except Exception as e:  # noqa: BLE001 - reported by the main thread
+            errors.append((tid, repr(e)))
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    hip.check(L.lmp_rt_synchronize())
+
+
 @pytest.mark.parametrize("nbytes", [STAGED_MIN - 4, STAGED_MIN, STAGE, STAGE + 4,
                                     3 * STAGE + 12, 100 * (1 << 20) + 8])
 def test_host_device_round_trip_every_byte(hip, nbytes):
