@@ -511,21 +511,30 @@ def mlp_bench(rsl, abi, dims, batch, steps, onehot, graph=False, fused_update=Fa
         loss.realize()
         return loss
 
-    s0 = rsl._stats()
     first = step()
     first_loss = first.tolist()[0]
-    s1 = rsl._stats()
     nonzero_grads = sum(int(np.count_nonzero(g.numpy())) for g in grads_seen)
     grad_entries = sum(int(np.prod(g.shape)) for g in grads_seen)
     grads_seen.clear()
     kept = [first.data]  # keep_losses: every step's loss tensor, read after timing
+    s2 = rsl._stats()
     for _ in range(2):
         kept.append(step().data)
+    s3 = rsl._stats()
+    # Kernels of a steady-state step (steps 2 and 3; the library's own count
+    # of the kernels it launched): a pending update is launched by the next
+    # step, so the first step alone can miss it.
+    launches = round((s3["kernels"] - s2["kernels"]) / 2)
     if graph:
-        # the whole step (forward, backward, SGD) as one HIP graph launch
+        # the whole step (forward, backward, SGD) as one HIP graph launch; its
+        # kernels are those the capture records (the carried updates included)
         g = rsl.hip.Graph()
+        rsl.realize_all(p for _, p in model.named_parameters())  # the last eager step's updates
+        sg = rsl._stats()
         with g.capture(carry=model):
             loss = step()
+        sh = rsl._stats()
+        launches = sh["kernels"] - sg["kernels"]
         run = g.replay
     else:
         run = step
@@ -540,8 +549,6 @@ def mlp_bench(rsl, abi, dims, batch, steps, onehot, graph=False, fused_update=Fa
                     kept.append(out.data)
     wall = time.perf_counter() - t0
     last = loss.tolist()[0]
-    launches = (s1["eager_launches"] + s1["fused_launches"]
-                - s0["eager_launches"] - s0["fused_launches"])
     gemm_flop = 0
     for i in range(len(dims) - 1):
         f = 2 * batch * dims[i] * dims[i + 1]

@@ -149,6 +149,11 @@ int lmp_rt_free(void* ptr);
 /* Return fully free segments to the HIP runtime (allocator.cu:117-125). */
 int lmp_rt_empty_cache(void);
 int lmp_rt_pool_stats_get(lmp_rt_pool_stats* stats);
+/* Number of kernels this process has launched through the library: every
+ * kernel of every entry point, hipRTC kernels included; a launch recorded into
+ * a graph counts once, its replays do not.  No counterpart in the reference;
+ * it lets a caller count the kernels of a step (measurement only). */
+int lmp_rt_kernel_launch_count(uint64_t* count);
 
 /* Copies on the library stream.  h2d/d2h synchronise before returning so the
  * host buffer may be reused or read; from 4 MiB up they run through pinned

@@ -72,6 +72,7 @@ SIGNATURES = {
     "lmp_rt_free": (_i, [_vp]),
     "lmp_rt_empty_cache": (_i, []),
     "lmp_rt_pool_stats_get": (_i, [C.POINTER(PoolStats)]),
+    "lmp_rt_kernel_launch_count": (_i, [C.POINTER(C.c_uint64)]),
     "lmp_rt_memcpy_h2d": (_i, [_vp, _vp, _sz]),
     "lmp_rt_memcpy_d2h": (_i, [_vp, _vp, _sz]),
     "lmp_rt_memcpy_d2d": (_i, [_vp, _vp, _sz]),

@@ -421,6 +421,8 @@ PYBIND11_MODULE(_C, m) {
     d["jit_cache_hits"] = s.jit_cache_hits;
     d["fused_host_ns"] = s.fused_host_ns;
     d["gemm_host_ns"] = s.gemm_host_ns;
+    uint64_t kernels = 0;
+    if (lmp_rt_kernel_launch_count(&kernels) == LMP_OK) d["kernels"] = kernels;
     lmp_rt_pool_stats ps{};
     if (lmp_rt_pool_stats_get(&ps) == LMP_OK) {
       d["pool_reserved_bytes"] = ps.reserved_bytes;

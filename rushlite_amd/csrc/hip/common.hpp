@@ -16,6 +16,9 @@ namespace lmp_hip {
 void set_error(const std::string& msg);
 int fail(int status, const std::string& msg);
 
+// Counts every kernel the library launches (lmp_rt_kernel_launch_count).
+void count_kernel_launch();
+
 // Runtime state of the library: one device, one in-order stream.
 struct Runtime {
   int device = -1;
@@ -89,7 +92,8 @@ inline const char* dtype_name(int dtype) {
                              std::string(#expr) + ": " + hipGetErrorString(_e)); \
   } while (0)
 
-// Check the launch that was just issued.
+// Check the launch that was just issued (every launch site issues exactly
+// one launch before its check) and count it.
 #define LMP_LAUNCH_CHECK(name)                                              \
   do {                                                                      \
     hipError_t _e = hipGetLastError();                                      \
@@ -97,6 +101,7 @@ inline const char* dtype_name(int dtype) {
       return ::lmp_hip::fail(LMP_ERR_RUNTIME,                               \
                              std::string("launch of ") + (name) + ": " +    \
                                  hipGetErrorString(_e));                    \
+    ::lmp_hip::count_kernel_launch();                                       \
   } while (0)
 
 #define LMP_RUNTIME_OR_FAIL(rt)                                             \

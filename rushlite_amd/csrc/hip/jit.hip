@@ -263,6 +263,7 @@ int lmp_jit_launch(void* handle, uint32_t grid, uint32_t block, void** args) {
   JitKernel* k = static_cast<JitKernel*>(handle);
   LMP_HIP_TRY(hipModuleLaunchKernel(k->fn, grid, 1, 1, block, 1, 1, 0,
                                     rt->stream, args, nullptr));
+  count_kernel_launch();
   return LMP_OK;
 }
 

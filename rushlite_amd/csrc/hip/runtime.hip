@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -289,6 +290,12 @@ int fail(int status, const std::string& msg) {
   return status;
 }
 
+namespace {
+std::atomic<uint64_t> g_kernel_launches{0};
+}  // namespace
+
+void count_kernel_launch() { g_kernel_launches.fetch_add(1, std::memory_order_relaxed); }
+
 Runtime* runtime() {
   std::lock_guard<std::mutex> lock(g_init_mu);
   if (!g_ready && init_locked(0) != LMP_OK) return nullptr;
@@ -388,6 +395,12 @@ int lmp_rt_empty_cache(void) {
   for (const Arena::Span& s : p.arena.take_free_segments())
     LMP_HIP_TRY(hipFree(reinterpret_cast<void*>(s.addr)));
   return release_dead_pools(p);
+}
+
+int lmp_rt_kernel_launch_count(uint64_t* count) {
+  if (!count) return fail(LMP_ERR_INVALID, "null count");
+  *count = g_kernel_launches.load(std::memory_order_relaxed);
+  return LMP_OK;
 }
 
 int lmp_rt_pool_stats_get(lmp_rt_pool_stats* stats) {

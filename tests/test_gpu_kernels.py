@@ -767,6 +767,33 @@ STAGE = 16 << 20  # bytes per staging chunk of lmp_rt_memcpy_h2d/d2h
 STAGED_MIN = 4 << 20
 
 
+def test_kernel_launch_count(hip):
+    """lmp_rt_kernel_launch_count counts the kernels the library launched: one
+    for a broadcast add, a short-row reduction or a tiny GEMM, two for a
+    split-K GEMM (the product and its fold), none for an empty call."""
+    L = hip.lib()
+
+    def count():
+        c = C.c_uint64(0)
+        hip.check(L.lmp_rt_kernel_launch_count(C.byref(c)))
+        return c.value
+
+    rng = np.random.default_rng(9)
+    a = up(hip, rng.standard_normal((64, 33), dtype=np.float32))
+    b = up(hip, rng.standard_normal((64, 1), dtype=np.float32))
+    x = up(hip, rng.standard_normal((256, 4096), dtype=np.float32))
+    w = up(hip, rng.standard_normal((4096, 256), dtype=np.float32))
+    s = up(hip, rng.standard_normal((8, 8), dtype=np.float32))
+    cases = [(lambda: hip.binary("add", a, b), 1), (lambda: hip.reduce("sum", a, 1), 1),
+             (lambda: hip.gemm(s, s), 1), (lambda: hip.gemm(x, w), 2),
+             (lambda: hip.check(L.lmp_k_fill(hip.FLOAT32, a.ptr, 0, 1.0)), 0)]
+    for fn, want in cases:
+        before = count()
+        fn()
+        assert count() - before == want
+    hip.check(L.lmp_rt_synchronize())
+
+
 def test_c_abi_from_several_host_threads(hip, oracle):
     """Four host threads drive the C ABI at once (ctypes releases the GIL):
     each allocates, uploads (staged and direct copies), runs a broadcast add,

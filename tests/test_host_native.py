@@ -29,8 +29,9 @@ def declared_functions():
 
 def test_header_declares_the_abi():
     names = declared_functions()
-    assert len(names) == 43
-    for group in ("lmp_rt_malloc", "lmp_k_binary", "lmp_k_reduce", "lmp_k_gemm_f32",
+    assert len(names) == 44
+    for group in ("lmp_rt_malloc", "lmp_rt_kernel_launch_count", "lmp_k_binary", "lmp_k_reduce",
+                  "lmp_k_gemm_f32",
                   "lmp_jit_compile", "lmp_rt_graph_begin", "lmp_rt_graph_launch",
                   "lmp_k_gemm_f32_noalloc", "lmp_k_gemm_colsum_masked_f32",
                   "lmp_k_linear_backward_f32"):
