@@ -222,7 +222,7 @@ def extras(rsl, abi, a_list, b, steps, warmup, only=None):
         out["c1b_chain6_eager_unfused"] = {
             "us": round(ms * 1e3, 2),
             "GB/s_algorithmic": round(BYTES_C1 / ms / 1e6, 1),
-            "launches_per_step": (s1["eager_launches"] - s0["eager_launches"]) / (r + 2)}
+            "launches_per_step": (s1["kernels"] - s0["kernels"]) / (r + 2)}
 
         # Host <-> device around the path (the boundary takes device buffers;
         # `value` never includes these): upload of a and b from pageable
