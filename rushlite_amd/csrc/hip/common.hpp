@@ -54,6 +54,11 @@ constexpr uint64_t kStreamBytes = uint64_t(256) << 20;
 // 173 us; 256 MiB: 219 vs 227 us).
 constexpr uint64_t kStreamStoreBytes = uint64_t(128) << 20;
 
+// GEMM extents (M, N, K) and leading dimensions stay below 2^31 - 4096, so
+// that every tile origin, fragment index and K-loop step (an extent plus at
+// most a few thousand) still fits the kernels' int arithmetic.
+constexpr size_t kGemmMaxExtent = (size_t(1) << 31) - 4096;
+
 // Scratch allocation for kernels that need a workspace (split-K partials,
 // two-pass reductions).  Memory comes from the pool and is returned to it
 // by the matching release; ordering on the single stream makes reuse safe.

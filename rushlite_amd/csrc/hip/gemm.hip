@@ -2007,20 +2007,22 @@ __global__ __launch_bounds__(256) void colsum_strided_f32(float* __restrict__ ou
                                                           const float* __restrict__ b, int k,
                                                           int n, int ldb, int trans_b,
                                                           int accumulate) {
+  // Indices in 64 bits: the last workgroup's lanes reach past n (and a lane's
+  // last step past k), which for extents near 2^31 would not fit an int.
   if (!trans_b) {
-    const int j = int(blockIdx.x) * 256 + int(threadIdx.x);
+    const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (j >= n) return;
     float s = 0.0f;
-    for (int r = 0; r < k; ++r) s += b[size_t(r) * size_t(ldb) + size_t(j)];
+    for (int64_t r = 0; r < k; ++r) s += b[r * int64_t(ldb) + j];
     out[j] = accumulate ? out[j] + s : s;
     return;
   }
-  const int j = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
+  const int64_t j = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = int(threadIdx.x & 63);
   if (j >= n) return;  // the whole wave leaves together
-  const float* row = b + size_t(j) * size_t(ldb);
+  const float* row = b + j * int64_t(ldb);
   float s = 0.0f;
-  for (int r = lane; r < k; r += 64) s += row[r];
+  for (int64_t r = lane; r < k; r += 64) s += row[r];
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
   if (lane == 0) out[j] = accumulate ? out[j] + s : s;
 }
@@ -2084,9 +2086,9 @@ int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
     return lmp_k_fill(LMP_FLOAT32, c, m * n, 0.0);
   }
   if (!a || !b) return fail(LMP_ERR_INVALID, "gemm: null input");
-  const size_t lim = 0x7fffffff;
+  const size_t lim = kGemmMaxExtent - 1;
   if (m > lim || n > lim || k > lim || lda > lim || ldb > lim || ldc > lim)
-    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension above 2^31");
+    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension of 2^31 - 4096 or more");
   if ((trans_a ? lda < m : lda < k) || (trans_b ? ldb < k : ldb < n) || ldc < n)
     return fail(LMP_ERR_INVALID, "gemm: leading dimension too small");
   LMP_RUNTIME_OR_FAIL(rt);
@@ -2152,9 +2154,9 @@ extern "C" int lmp_k_gemm_colsum_f32(int trans_a, int trans_b, size_t m, size_t 
   if (!colsum) return fail(LMP_ERR_INVALID, "gemm_colsum: null column-sum output");
   if (m == 0 || n == 0 || k == 0 || !a || !b || !c)
     return fail(LMP_ERR_UNSUPPORTED, "gemm_colsum: empty or null operand");
-  const size_t lim = 0x7fffffff;
+  const size_t lim = kGemmMaxExtent - 1;
   if (m > lim || n > lim || k > lim || lda > lim || ldb > lim || ldc > lim)
-    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension above 2^31");
+    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension of 2^31 - 4096 or more");
   if ((trans_a ? lda < m : lda < k) || (trans_b ? ldb < k : ldb < n) || ldc < n)
     return fail(LMP_ERR_INVALID, "gemm: leading dimension too small");
   GemmArgs g{};
@@ -2218,9 +2220,9 @@ extern "C" int lmp_k_gemm_colsum_masked_f32(int trans_a, size_t m, size_t n, siz
     return fail(LMP_ERR_INVALID, "gemm_colsum_masked: null column sums or mask");
   if (m == 0 || n == 0 || k == 0 || !a || !b || !c)
     return fail(LMP_ERR_UNSUPPORTED, "gemm_colsum_masked: empty or null operand");
-  const size_t lim = 0x7fffffff;
+  const size_t lim = kGemmMaxExtent - 1;
   if (m > lim || n > lim || k > lim || lda > lim || ldb > lim || ldc > lim)
-    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension above 2^31");
+    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension of 2^31 - 4096 or more");
   if ((trans_a ? lda < m : lda < k) || ldb < n || ldc < n)
     return fail(LMP_ERR_INVALID, "gemm: leading dimension too small");
   GemmArgs g{};
@@ -2268,10 +2270,10 @@ extern "C" int lmp_k_linear_backward_f32(size_t batch, size_t in, size_t out, co
   if (!dx || !dw || !db) return fail(LMP_ERR_INVALID, "linear_backward: null output");
   if (batch == 0 || in == 0 || out == 0 || !x || !w || !g)
     return fail(LMP_ERR_UNSUPPORTED, "linear_backward: empty or null operand");
-  const size_t lim = 0x7fffffff;
+  const size_t lim = kGemmMaxExtent - 1;
   if (batch > lim || in > lim || out > lim || ldx > lim || ldw > lim || ldg > lim ||
       lddx > lim || lddw > lim)
-    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension above 2^31");
+    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension of 2^31 - 4096 or more");
   if (ldx < in || ldw < out || ldg < out || lddx < in || lddw < out)
     return fail(LMP_ERR_INVALID, "gemm: leading dimension too small");
   // dW [in, out] = X^T G over the batch, with db beside it.

@@ -537,9 +537,9 @@ extern "C" int lmp_k_gemm(int dtype, int trans_a, int trans_b, size_t m, size_t 
     return lmp_k_fill(dtype, c, m * n, 0.0);
   }
   if (!a || !b) return fail(LMP_ERR_INVALID, "gemm: null input");
-  const size_t lim = 0x7fffffff;
+  const size_t lim = kGemmMaxExtent - 1;
   if (m > lim || n > lim || k > lim || lda > lim || ldb > lim || ldc > lim)
-    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension above 2^31");
+    return fail(LMP_ERR_UNSUPPORTED, "gemm: dimension of 2^31 - 4096 or more");
   if ((trans_a ? lda < m : lda < k) || (trans_b ? ldb < k : ldb < n) || ldc < n)
     return fail(LMP_ERR_INVALID, "gemm: leading dimension too small");
   const uint64_t tiles = uint64_t((m + kTile - 1) / kTile) * ((n + kTile - 1) / kTile);

@@ -68,6 +68,36 @@ def test_build_recipe_imports_nothing_from_the_package():
     assert "spec_from_file_location" in entry and "from rushlite_amd import build" not in entry
 
 
+def test_gemm_entries_refuse_extents_near_2_31():
+    """Every GEMM entry point refuses an extent or leading dimension of
+    2^31 - 4096 or more (LMP_ERR_UNSUPPORTED) while validating its arguments,
+    before it touches the device: the kernels' tile, fragment and K-loop
+    indices are ints that reach a few thousand past an extent.  The operand
+    pointers are placeholders that nothing reads, so the test runs only where
+    no GPU is visible."""
+    from conftest import gpu_available
+    if gpu_available():
+        pytest.skip("placeholder pointers: argument validation is checked on a host without a GPU")
+    from rushlite_amd import abi
+    L = abi.lib()
+    big, p = (1 << 31) - 4096, 4096  # p: a non-null placeholder address
+    for ta in (0, 1):
+        for tb in (0, 1):
+            for m, n, k in ((big, 8, 8), (8, big, 8), (8, 8, big)):
+                lda = (m if ta else k)
+                ldb = (k if tb else n)
+                assert L.lmp_k_gemm_f32(ta, tb, m, n, k, p, lda, p, ldb, p, n, 0) == abi.ERR_UNSUPPORTED
+                assert L.lmp_k_gemm(abi.FLOAT64, ta, tb, m, n, k,
+                                    p, lda, p, ldb, p, n, 0) == abi.ERR_UNSUPPORTED
+    # a leading dimension alone at the limit
+    assert L.lmp_k_gemm_f32(0, 0, 8, 8, 8, p, big, p, 8, p, 8, 0) == abi.ERR_UNSUPPORTED
+    assert L.lmp_k_linear_f32(0, 0, 8, big, 8, p, 8, p, big, p, p, big) == abi.ERR_UNSUPPORTED
+    assert L.lmp_k_linear_relu_f32(0, 0, 8, big, 8, p, 8, p, big, p, p, big) == abi.ERR_UNSUPPORTED
+    assert L.lmp_k_gemm_colsum_f32(1, 0, 8, 8, big, p, 8, p, 8, p, 8, 0, p, 0) == abi.ERR_UNSUPPORTED
+    assert L.lmp_k_gemm_colsum_masked_f32(1, 8, 8, big, p, 8, p, p, 8, p, 8, 0, p, 0) == abi.ERR_UNSUPPORTED
+    assert L.lmp_k_linear_backward_f32(big, 8, 8, p, 8, p, 8, p, 8, p, 8, 0, p, 8, 0, p, 0) == abi.ERR_UNSUPPORTED
+
+
 @pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
 @pytest.mark.parametrize("sanitize", [None, "thread"], ids=["plain", "tsan"])
 def test_arena_fastdiv_and_copy_pool(tmp_path, sanitize):
