@@ -484,7 +484,7 @@ def test_mlp_trajectory_vs_torch(oracle):
         p = _torch_softmax_lamp(h @ tw[1] + tb[1], -1)
         loss = (-ty * torch.log(p + 1e-3)).sum(1, keepdim=True).sum(0, keepdim=True)
         loss.backward()
-        tl.append(float(loss))
+        tl.append(float(loss.detach()))
         tw = [(w - 1e-3 * w.grad).detach() for w in tw]
         tb = [(b - 1e-3 * b.grad).detach() for b in tb]
     np.testing.assert_allclose(losses, tl, rtol=1e-4)
