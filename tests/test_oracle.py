@@ -513,9 +513,10 @@ def test_mlp_step_gemm_orders_vs_torch(oracle):
     tl = (-ty * torch.log(p + 1e-3)).sum(1, keepdim=True).sum(0, keepdim=True)
     tl.backward()
     want = [t.grad.numpy() for t in (tw[0], tb[0], tw[1], tb[1])]
+    tlv = float(tl.detach())
     for f64 in (False, True):
         loss, gw, gb = oracle.mlp_step(ws, bs, x, y, f64_gemm=f64)
-        assert abs(loss - float(tl)) <= 1e-5 * abs(float(tl))
+        assert abs(loss - tlv) <= 1e-5 * abs(tlv)
         got = [gw[0], gb[0], gw[1], gb[1]]
         for g, w in zip(got, want):
             assert np.max(np.abs(g - w)) / np.max(np.abs(w)) < 1e-5
