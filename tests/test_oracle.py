@@ -556,7 +556,7 @@ def test_mlp_step_with_relu_masks_vs_torch(oracle):
     tl.backward()
     want = [t_.grad.numpy() for t_ in (tw[0], tb[0], tw[1], tb[1])]
     loss, gw, gb = oracle.mlp_step(ws, bs, x, y, f64_gemm=True, relu_masks=[mask])
-    assert abs(loss - float(tl)) <= 1e-5 * abs(float(tl))
+    assert abs(loss - float(tl.detach())) <= 1e-5 * abs(float(tl.detach()))
     for g, w in zip([gw[0], gb[0], gw[1], gb[1]], want):
         assert np.max(np.abs(g - w)) / np.max(np.abs(w)) < 1e-5
     # the flips are visible: the first layer's gradients move
