@@ -72,6 +72,49 @@ def _params(model):
 CASES = [((256, 64, 10), 32), ((1024, 512, 256, 10), 32)]
 
 
+def test_graph_replays_equal_eager_steps_at_config4_size(rsl):
+    """Config 4 (batch 512, 4096-4096-4096-1000, x normal(0, 1), one-hot y):
+    the captured step replays the LDS-tile GEMMs with their split-K folds, the
+    paired weight and input gradient launches and the grouped update.
+    Parameters at a 1/64 scale, so the gradients are dense (at randn(0, 1) the
+    softmax is one-hot and every gradient is zero); the loss must equal the
+    eager twin's at every replay and the parameters after the last."""
+    dims, batch = (4096, 4096, 4096, 1000), 512
+    rng = np.random.default_rng(5)
+    x_np = rng.standard_normal((batch, dims[0]), dtype=np.float32)
+    y_np = np.zeros((batch, dims[-1]), np.float32)
+    y_np[np.arange(batch), rng.integers(0, dims[-1], batch)] = 1.0
+    ws = [rng.standard_normal((dims[i], dims[i + 1]), dtype=np.float32) / np.float32(64)
+          for i in range(len(dims) - 1)]
+    bs = [rng.standard_normal(dims[i + 1], dtype=np.float32) / np.float32(64)
+          for i in range(len(dims) - 1)]
+    eager = _mlp(rsl, ws, bs)
+    graphed = _mlp(rsl, ws, bs)
+    xe, ye = rsl.Variable(x_np), rsl.Variable(y_np)
+    xg, yg = rsl.Variable(x_np), rsl.Variable(y_np)
+    step_e = _stepper(rsl, eager, xe, ye, fused_update=True)
+    step_g = _stepper(rsl, graphed, xg, yg, fused_update=True)
+    l_e, l_g = step_e(), step_g()
+    rsl.realize_all(p for _, p in eager.named_parameters())
+    rsl.realize_all(p for _, p in graphed.named_parameters())
+    assert np.array_equal(l_e.numpy(), l_g.numpy())
+    graph = rsl.hip.Graph()
+    with graph.capture(carry=graphed):
+        loss_g = step_g()
+    losses = []
+    for i in range(4):
+        graph.replay()
+        l_e = step_e()
+        rsl.realize_all(p for _, p in eager.named_parameters())
+        got, want = loss_g.numpy(), l_e.numpy()
+        assert np.array_equal(got, want), (i, got, want)
+        losses.append(float(want.ravel()[0]))
+    assert losses[-1] < losses[0]  # the dense gradients move the loss
+    pg, pe = _params(graphed), _params(eager)
+    for name in pe:
+        assert np.array_equal(pg[name], pe[name]), name
+
+
 @pytest.mark.parametrize("fused_update", [False, True], ids=["eager_sgd", "fused_sgd"])
 @pytest.mark.parametrize("dims,batch", CASES)
 def test_graph_replays_equal_eager_steps(rsl, dims, batch, fused_update):
