@@ -191,10 +191,36 @@ def rsl(hip):
     return rushlite_amd
 
 
+def _torch_eval(evaluate, arrs):
+    tv = [torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in arrs]
+    out = evaluate(tv)
+    out.backward()
+    return (out.detach().numpy().reshape(-1),
+            [np.zeros(a.shape) if t.grad is None else t.grad.numpy() for t, a in zip(tv, arrs)])
+
+
+def skip_if_ill_conditioned(evaluate, arrs, dtype, tol):
+    """Skips a program whose torch float64 value or input gradients move by
+    more than `tol` when its inputs move by one ulp of `dtype` (two random
+    perturbations): a max/min tie that one rounding breaks, or a cancelling
+    sum, where two correct evaluation orders may differ by more than the bar."""
+    base_out, base_grads = _torch_eval(evaluate, arrs)
+    eps = float(np.finfo(dtype).eps)
+    for trial in range(2):
+        rng = np.random.default_rng(77 + trial)
+        moved = [(a * (1 + eps * rng.uniform(-1, 1, a.shape))).astype(dtype) for a in arrs]
+        out, grads = _torch_eval(evaluate, moved)
+        errs = [rel_err(out, base_out)]
+        errs += [rel_err(g.reshape(b.shape), b) for g, b in zip(grads, base_grads)]
+        if max(errs) > tol:
+            pytest.skip(f"ill-conditioned: a one-ulp input change moves torch float64 by {max(errs):.2g}")
+
+
 def check_graph(rsl, seed, capture, dtype, tol):
     leaves, steps, shapes = make_program(seed)
     rng = np.random.default_rng(1000 + seed)
     arrs = [rng.uniform(-1.0, 1.0, s).astype(dtype) for s in leaves]
+    skip_if_ill_conditioned(lambda tv: run(TorchOps, tv, steps, shapes), arrs, dtype, tol)
     tv = [torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in arrs]
     t_out = run(TorchOps, tv, steps, shapes)
     t_out.backward()
@@ -412,6 +438,12 @@ def test_random_graph_3d(rsl, oracle, seed, shape, capture):
         if dtype == np.float64:
             want, want_grads, tol = t_out.detach().numpy(), t_grads, 1e-9
             kind = rsl.dtype.float64
+            try:
+                skip_if_ill_conditioned(
+                    lambda v: _sum_all(TorchOps, _run_steps(TorchOps, v, steps), shapes), a,
+                    dtype, tol)
+            except pytest.skip.Exception:
+                continue  # ill-conditioned in float64: the float32 check below still runs
         else:
             ov = [oracle.OVar(x.copy(), requires_grad=True) for x in a]
             o_ops = oracle_ops(oracle)
