@@ -1631,6 +1631,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tn_short(GemmArgs g) {
           if (row < g.m && col < g.n) {
             v4f* p = reinterpret_cast<v4f*>(g.c + int64_t(row) * g.ldc + col);
             if (g.accumulate) *p = *p + v;
+            else if (g.bias) *p = lin_epi4(v, *reinterpret_cast<const v4f*>(g.bias + col), g.relu);
             else *p = v;
           }
         }
@@ -1858,7 +1859,7 @@ Route gemm_route(Runtime* rt, const GemmArgs& g, bool vec, bool direct_ok) {
   if constexpr (TA && !TB) {
     const int64_t short_tiles = int64_t((g.m + kShortBM - 1) / kShortBM) *
                                 ((g.n + kShortBN - 1) / kShortBN);
-    if (vec && g.vec_out && g.k <= kBK && !g.bias && short_tiles <= 0x7fffffff)
+    if (vec && g.vec_out && g.k <= kBK && short_tiles <= 0x7fffffff)
       return Route::Short;
   }
   // M <= 32 with B transposed and a 32-column block for every CU: whole rows
@@ -2092,6 +2093,22 @@ int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
   if ((trans_a ? lda < m : lda < k) || (trans_b ? ldb < k : ldb < n) || ldc < n)
     return fail(LMP_ERR_INVALID, "gemm: leading dimension too small");
   LMP_RUNTIME_OR_FAIL(rt);
+  // The kernel choice must not depend on the bias (a Linear equals the GEMM
+  // followed by the bias add bit for bit only if both run the same kernel),
+  // and the kernels read the bias four columns at a time: a bias that is not
+  // 16-byte aligned is first copied to one that is.
+  float* bias_copy = nullptr;
+  if (bias && !aligned16(bias)) {
+    bias_copy = static_cast<float*>(scratch_alloc(n * sizeof(float)));
+    if (!bias_copy) return LMP_ERR_OOM;
+    const hipError_t e = hipMemcpyAsync(bias_copy, bias, n * sizeof(float),
+                                        hipMemcpyDeviceToDevice, rt->stream);
+    if (e != hipSuccess) {
+      scratch_free(bias_copy);
+      return fail(LMP_ERR_RUNTIME, std::string("linear: bias copy: ") + hipGetErrorString(e));
+    }
+    bias = bias_copy;
+  }
   GemmArgs g{};
   g.a = a;
   g.b = b;
@@ -2110,10 +2127,13 @@ int gemm_f32_entry(int trans_a, int trans_b, size_t m, size_t n, size_t k,
   bool vec = false, direct_ok = false;
   gemm_flags(g, trans_a, trans_b, &vec, &direct_ok);
   bool* cd = colsum_done;
-  if (!trans_a && !trans_b) return launch_gemm<false, false>(rt, g, vec, direct_ok, ws, cd);
-  if (!trans_a && trans_b) return launch_gemm<false, true>(rt, g, vec, direct_ok, ws, cd);
-  if (trans_a && !trans_b) return launch_gemm<true, false>(rt, g, vec, direct_ok, ws, cd);
-  return launch_gemm<true, true>(rt, g, vec, direct_ok, ws, cd);
+  int rc;
+  if (!trans_a && !trans_b) rc = launch_gemm<false, false>(rt, g, vec, direct_ok, ws, cd);
+  else if (!trans_a && trans_b) rc = launch_gemm<false, true>(rt, g, vec, direct_ok, ws, cd);
+  else if (trans_a && !trans_b) rc = launch_gemm<true, false>(rt, g, vec, direct_ok, ws, cd);
+  else rc = launch_gemm<true, true>(rt, g, vec, direct_ok, ws, cd);
+  if (bias_copy) scratch_free(bias_copy);  // stream-ordered: the kernels read it first
+  return rc;
 }
 
 }  // namespace

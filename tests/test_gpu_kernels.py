@@ -688,7 +688,10 @@ def test_gemm_short_k_large_c(hip, m, n, k, ta, tb):
 # split-K fold, the 128/256-wide LDS tiles), so C must equal the plain GEMM
 # followed by a float32 bias add, bit for bit.
 LINEAR_SHAPES = [(32, 64, 256), (20, 132, 1028), (48, 96, 64), (200, 130, 70),
-                 (256, 1000, 128), (512, 2048, 2048), (4096, 4096, 256)]
+                 (256, 1000, 128), (512, 2048, 2048), (4096, 4096, 256),
+                 # K <= 32 past the tiny kernel's range: A transposed takes the
+                 # short-K kernel, with or without a bias
+                 (28, 3272, 28), (32, 4072, 20), (640, 2048, 32)]
 
 
 @pytest.mark.parametrize("m,n,k", LINEAR_SHAPES, ids=str)
@@ -711,6 +714,12 @@ def test_linear_bias_epilogue_equals_gemm_then_add(hip, m, n, k, ta, tb):
     hip.check(hip.lib().lmp_k_linear_relu_f32(ta, tb, m, n, k, da.ptr, da.shape[1], db.ptr,
                                               db.shape[1], dbias.ptr, out.ptr, n))
     relu = np.where(want < 0, np.float32(0), want)
+    assert np.array_equal(out.numpy().view(np.uint32), relu.view(np.uint32))
+    # a bias that is not 16-byte aligned (one float into a buffer) gives the
+    # same bits: the kernel choice does not depend on where the bias lies
+    shifted = up(hip, np.concatenate([[np.float32(7)], bias]).astype(np.float32))
+    hip.check(hip.lib().lmp_k_linear_relu_f32(ta, tb, m, n, k, da.ptr, da.shape[1], db.ptr,
+                                              db.shape[1], shifted.ptr + 4, out.ptr, n))
     assert np.array_equal(out.numpy().view(np.uint32), relu.view(np.uint32))
 
 
@@ -735,7 +744,8 @@ def _random_gemm_shapes(count, seed):
     return shapes
 
 
-@pytest.mark.parametrize("m,n,k", _random_gemm_shapes(24, 2026) + [(20, 8200, 100), (600, 2100, 2100)],
+@pytest.mark.parametrize("m,n,k", _random_gemm_shapes(24, 2026) + [(20, 8200, 100), (600, 2100, 2100),
+                                                   (28, 3272, 28), (28, 4048, 20)],
                          ids=str)
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_gemm_random_shapes_every_path(hip, m, n, k, ta, tb):
