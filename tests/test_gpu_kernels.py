@@ -283,8 +283,12 @@ def test_reduce(hip, oracle, shape, axis):
     want = oracle.reduce("sum", a, axis)
     assert got.shape == want.shape
     truth = a.astype(np.float64).sum(axis=axis, keepdims=True)
-    assert rel_err(got, want) <= 1e-5
     assert rel_err(got, truth) <= 1e-5
+    # Against the oracle's sequential float32 sum at 1e-5, or twice the
+    # oracle's own distance from float64 where that is larger: a cancelling
+    # sum (a 1754-value row summing to -2.89 from terms up to 4 in size) puts
+    # the sequential order 1.3e-5 from the truth, and the tree order 6e-7.
+    assert rel_err(got, want) <= max(1e-5, 2 * rel_err(want, truth))
     small = (1.0 + 0.01 * a).astype(np.float32)
     got = hip.reduce("prod", up(hip, small), axis).numpy()
     assert rel_err(got, oracle.reduce("prod", small, axis)) <= 1e-5
