@@ -1,0 +1,232 @@
+"""Wider randomized runs of the GPU parity checks (a GPU box; not collected by
+pytest).  Each suite draws many more cases than the committed tests from the
+same generators and checks them to the same bars, printing a progress line
+every few dozen cases and every mismatch:
+
+    python tests/fuzz_wide.py programs 100 200   # random programs, seeds 100..199
+    python tests/fuzz_wide.py gemm 888 3000      # random GEMM shapes (+ 100 Linear backward pairs)
+    python tests/fuzz_wide.py strided 51 1500    # strided, offset operands; padding poisoned
+    python tests/fuzz_wide.py ops 31 600         # reductions (and 2000 broadcast binaries)
+    python tests/fuzz_wide.py typed 41 400       # bool / int / float64 GEMM, reduce, binary
+
+The generators and checks are the committed tests' own (test_gpu_graphs,
+test_gpu_hip_graph, test_gpu_kernels, test_gpu_typed); `strided` adds GEMMs
+whose operands sit at odd offsets inside wider rows filled with NaN, whose
+output rows are wider than N and prefilled with a sentinel: no NaN may reach
+C and no element outside C may change.
+"""
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parent))
+sys.path.insert(0, str(HERE))
+
+from rushlite_amd import abi  # noqa: E402
+from _helpers import rel_err  # noqa: E402
+
+T0 = time.time()
+COUNTS = {"ok": 0, "skip": 0, "fail": 0}
+
+
+def attempt(name, fn, *args):
+    try:
+        fn(*args)
+        COUNTS["ok"] += 1
+    except pytest.skip.Exception:
+        COUNTS["skip"] += 1
+    except AssertionError as e:
+        COUNTS["fail"] += 1
+        print("FAIL", name, [a for a in args if not hasattr(a, "__dict__")], str(e)[:300],
+              flush=True)
+
+
+def progress(what):
+    print(f"{what}: {COUNTS} {time.time() - T0:.0f} s", flush=True)
+
+
+def programs(lo, hi):
+    import rushlite_amd as rsl
+    from oracle import lamp_oracle
+    lamp_oracle.load()
+    import test_gpu_graphs as TG
+    import test_gpu_hip_graph as TH
+    for seed in range(lo, hi):
+        for cap in (False, True):
+            attempt("f64", TG.check_graph, rsl, seed, cap, np.float64, TG.TOL)
+            attempt("f32", TG.check_graph, rsl, seed, cap, np.float32, 1e-4)
+            for shape in TG.RC_SHAPES:
+                attempt("rc", TG.test_random_graph_float32_shapes_vs_oracle, rsl, lamp_oracle,
+                        seed, shape, cap)
+            for shape in TG.D3_SHAPES:
+                attempt("3d", TG.test_random_graph_3d, rsl, lamp_oracle, seed, shape, cap)
+            for shape in [(64, 128), (33, 7)]:
+                attempt("graph", TH.test_random_program_graph_replays_equal_eager, rsl, seed,
+                        shape, cap)
+        if seed % 10 == 0:
+            progress(f"seed {seed}")
+
+
+def gemm(seed, count, pairs=100):
+    import test_gpu_kernels as TK
+    for i, (m, n, k) in enumerate(TK._random_gemm_shapes(count, seed)):
+        for ta, tb in ((0, 0), (0, 1), (1, 0), (1, 1)):
+            attempt("gemm", TK.test_gemm_random_shapes_every_path, abi, m, n, k, ta, tb)
+        if i % 100 == 0:
+            progress(f"gemm shape {i}")
+    rng = np.random.default_rng(seed + 1)
+    for i in range(pairs):
+        shape = (int(rng.integers(130, 2700)), 4 * int(rng.integers(129, 1026)),
+                 4 * int(rng.integers(129, 1026)))
+        attempt("pair", TK.test_linear_backward_random_shapes_equal_separate_calls, abi, *shape)
+        if i % 20 == 0:
+            progress(f"pair {i}")
+
+
+def _strided_case(L, rng):
+    c = rng.random()
+    m = int(rng.integers(1, 33) if c < 0.25 else rng.integers(33, 300) if c < 0.6
+            else rng.integers(300, 1500))
+    n = int(rng.integers(1, 130) if rng.random() < 0.3 else rng.integers(130, 2500))
+    k = int(rng.integers(1, 33) if rng.random() < 0.3 else rng.integers(33, 1500))
+    if m * n * k > (1 << 30):
+        return
+    ta, tb = int(rng.integers(0, 2)), int(rng.integers(0, 2))
+    kind = str(rng.choice(["gemm", "acc", "relu", "colsum"]))
+    if kind == "colsum":
+        tb = 0
+    ar, ac = (k, m) if ta else (m, k)
+    br, bc = (n, k) if tb else (k, n)
+    lda, ldb, ldc = (ac + int(rng.integers(0, 10)), bc + int(rng.integers(0, 10)),
+                     n + int(rng.integers(0, 10)))
+    oa, ob, oc = (int(rng.integers(0, 4)) for _ in range(3))
+    a = rng.standard_normal((ar, ac)).astype(np.float32)
+    b = rng.standard_normal((br, bc)).astype(np.float32)
+    sentinel = np.float32(12345.0)
+    ha = np.full(oa + ar * lda + 8, np.nan, np.float32)
+    hb = np.full(ob + br * ldb + 8, np.nan, np.float32)
+    hc = np.full(oc + m * ldc + 8, sentinel, np.float32)
+    for r in range(ar):
+        ha[oa + r * lda: oa + r * lda + ac] = a[r]
+    for r in range(br):
+        hb[ob + r * ldb: ob + r * ldb + bc] = b[r]
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    if kind == "acc":
+        for r in range(m):
+            hc[oc + r * ldc: oc + r * ldc + n] = c0[r]
+    da, db, dc = (abi.DeviceBuffer.from_numpy(x) for x in (ha, hb, hc))
+    pa, pb, pc = da.ptr + 4 * oa, db.ptr + 4 * ob, dc.ptr + 4 * oc
+    want = (a.T if ta else a).astype(np.float64) @ (b.T if tb else b).astype(np.float64)
+    bias = rng.standard_normal(n).astype(np.float32)
+    dbias = abi.DeviceBuffer.from_numpy(bias)
+    dcs = abi.DeviceBuffer((n,), np.float32)
+    if kind in ("gemm", "acc"):
+        st = L.lmp_k_gemm_f32(ta, tb, m, n, k, pa, lda, pb, ldb, pc, ldc, int(kind == "acc"))
+        if kind == "acc":
+            want = want + c0
+    elif kind == "relu":
+        st = L.lmp_k_linear_relu_f32(ta, tb, m, n, k, pa, lda, pb, ldb, dbias.ptr, pc, ldc)
+        want = np.maximum(want + bias, 0.0)
+    else:
+        st = L.lmp_k_gemm_colsum_f32(ta, 0, m, n, k, pa, lda, pb, ldb, pc, ldc, 0, dcs.ptr, 0)
+    case = (kind, m, n, k, ta, tb, lda, ldb, ldc, oa, ob, oc)
+    if st == abi.ERR_UNSUPPORTED:
+        return
+    assert st == abi.OK, (case, st, L.lmp_rt_last_error())
+    got = dc.numpy()
+    inner = np.stack([got[oc + r * ldc: oc + r * ldc + n] for r in range(m)])
+    mask = np.ones(got.shape, bool)
+    for r in range(m):
+        mask[oc + r * ldc: oc + r * ldc + n] = False
+    assert np.all(np.isfinite(inner)), (case, "NaN from the padding reached C")
+    assert rel_err(inner, want) <= 1e-5, (case, rel_err(inner, want))
+    assert np.array_equal(got[mask], hc[mask]), (case, "an element outside C changed")
+    if kind == "colsum":
+        assert rel_err(dcs.numpy(), b.astype(np.float64).sum(0)) <= 1e-5, case
+
+
+def strided(seed, count):
+    L = abi.lib()
+    rng = np.random.default_rng(seed)
+    for i in range(count):
+        attempt("strided", _strided_case, L, rng)
+        if i % 100 == 0:
+            progress(f"strided {i}")
+
+
+def _random_shape(rng):
+    dims = []
+    for _ in range(int(rng.integers(1, 4))):
+        c = rng.random()
+        dims.append(int(rng.integers(1, 8) if c < 0.3 else rng.integers(8, 300) if c < 0.8
+                        else rng.integers(300, 5000)))
+    while np.prod(dims) > (1 << 24):
+        dims[int(np.argmax(dims))] //= 2
+    return tuple(max(1, d) for d in dims)
+
+
+def ops(seed, nred, nbin=2000):
+    from oracle import lamp_oracle as oracle
+    oracle.load()
+    import test_gpu_kernels as TK
+    rng = np.random.default_rng(seed)
+    for i in range(nred):
+        shape = _random_shape(rng)
+        attempt("reduce", TK.test_reduce, abi, oracle, shape, int(rng.integers(0, len(shape))))
+        if i % 100 == 0:
+            progress(f"reduce {i}")
+    for i in range(nbin):
+        sa = _random_shape(rng)
+        sb = tuple(1 if rng.random() < 0.4 else d for d in sa[int(rng.integers(0, len(sa))):])
+        if rng.random() < 0.5:
+            sa, sb = sb, sa
+        attempt("binary", TK.test_binary_bitexact, abi, oracle, str(rng.choice(TK.EXACT_BIN)), sa,
+                sb)
+        if i % 200 == 0:
+            progress(f"binary {i}")
+
+
+def typed(seed, ngemm, nred=300, nbin=1500):
+    import test_gpu_typed as TT
+    rng = np.random.default_rng(seed)
+    dims = lambda lo, hi: int(rng.integers(lo, hi))  # noqa: E731
+    pick = lambda: TT.TYPED[int(rng.integers(0, len(TT.TYPED)))]  # noqa: E731
+    for i in range(ngemm):
+        attempt("typed gemm", TT.test_typed_gemm, abi, pick(), dims(1, 300), dims(1, 300),
+                dims(1, 300), dims(0, 2), dims(0, 2))
+        if i % 100 == 0:
+            progress(f"typed gemm {i}")
+    for i in range(nred):
+        nd = dims(1, 4)
+        shape = tuple(dims(1, 400 if nd < 3 else 120) for _ in range(nd))
+        attempt("typed reduce", TT.test_typed_reduce, abi, pick(), shape, dims(0, nd))
+        if i % 100 == 0:
+            progress(f"typed reduce {i}")
+    names = ["add", "sub", "mul", "div", "eq", "ne", "ge", "le", "gt", "lt"]
+    for i in range(nbin):
+        nd = dims(1, 4)
+        sa = tuple(dims(1, 200) for _ in range(nd))
+        sb = tuple(1 if rng.random() < 0.4 else d for d in sa[dims(0, nd):])
+        if rng.random() < 0.5:
+            sa, sb = sb, sa
+        attempt("typed binary", TT.test_typed_binary_exact, abi, str(rng.choice(names)), pick(),
+                sa, sb)
+        if i % 200 == 0:
+            progress(f"typed binary {i}")
+
+
+def main():
+    suite, a, b = sys.argv[1], int(sys.argv[2]), int(sys.argv[3])
+    abi.check(abi.lib().lmp_rt_init(0))
+    {"programs": programs, "gemm": gemm, "strided": strided, "ops": ops,
+     "typed": typed}[suite](a, b)
+    print("DONE", suite, COUNTS, flush=True)
+    sys.exit(1 if COUNTS["fail"] else 0)
+
+
+if __name__ == "__main__":
+    main()
