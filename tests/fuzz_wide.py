@@ -8,6 +8,7 @@ every few dozen cases and every mismatch:
     python tests/fuzz_wide.py strided 51 1500    # strided, offset operands; padding poisoned
     python tests/fuzz_wide.py ops 31 600         # reductions (and 2000 broadcast binaries)
     python tests/fuzz_wide.py typed 41 400       # bool / int / float64 GEMM, reduce, binary
+    python tests/fuzz_wide.py noalloc 61 400     # the no-allocation GEMM against the allocating one
 
 The generators and checks are the committed tests' own (test_gpu_graphs,
 test_gpu_hip_graph, test_gpu_kernels, test_gpu_typed); `strided` adds GEMMs
@@ -219,11 +220,43 @@ def typed(seed, ngemm, nred=300, nbin=1500):
             progress(f"typed binary {i}")
 
 
+def _noalloc_case(L, rng):
+    m, n, k = (int(rng.integers(1, 2100)), int(rng.integers(1, 4200)), int(rng.integers(1, 4200)))
+    if m * n * k > (1 << 32):
+        return
+    ta, tb, acc = int(rng.integers(0, 2)), int(rng.integers(0, 2)), int(rng.integers(0, 2))
+    a = (rng.standard_normal((k, m) if ta else (m, k)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal((n, k) if tb else (k, n)) * 0.02).astype(np.float32)
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    da, db = abi.DeviceBuffer.from_numpy(a), abi.DeviceBuffer.from_numpy(b)
+    ref, out = abi.DeviceBuffer.from_numpy(c0), abi.DeviceBuffer.from_numpy(c0)
+    abi.check(L.lmp_k_gemm_f32(ta, tb, m, n, k, da.ptr, a.shape[1], db.ptr, b.shape[1], ref.ptr,
+                               n, acc))
+    st = L.lmp_k_gemm_f32_noalloc(ta, tb, m, n, k, da.ptr, a.shape[1], db.ptr, b.shape[1],
+                                  out.ptr, n, acc)
+    if st == abi.ERR_UNSUPPORTED:  # partials above the fixed workspace
+        return
+    assert st == abi.OK, ((m, n, k, ta, tb, acc), st)
+    assert np.array_equal(out.numpy().view(np.uint32), ref.numpy().view(np.uint32)), \
+        (m, n, k, ta, tb, acc)
+
+
+def noalloc(seed, count):
+    """lmp_k_gemm_f32_noalloc against lmp_k_gemm_f32 on random products, one
+    after another on the shared workspace: the same bits."""
+    L = abi.lib()
+    rng = np.random.default_rng(seed)
+    for i in range(count):
+        attempt("noalloc", _noalloc_case, L, rng)
+        if i % 50 == 0:
+            progress(f"noalloc {i}")
+
+
 def main():
     suite, a, b = sys.argv[1], int(sys.argv[2]), int(sys.argv[3])
     abi.check(abi.lib().lmp_rt_init(0))
     {"programs": programs, "gemm": gemm, "strided": strided, "ops": ops,
-     "typed": typed}[suite](a, b)
+     "typed": typed, "noalloc": noalloc}[suite](a, b)
     print("DONE", suite, COUNTS, flush=True)
     sys.exit(1 if COUNTS["fail"] else 0)
 
