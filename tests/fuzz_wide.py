@@ -9,6 +9,7 @@ every few dozen cases and every mismatch:
     python tests/fuzz_wide.py ops 31 600         # reductions (and 2000 broadcast binaries)
     python tests/fuzz_wide.py typed 41 400       # bool / int / float64 GEMM, reduce, binary
     python tests/fuzz_wide.py noalloc 61 400     # the no-allocation GEMM against the allocating one
+    python tests/fuzz_wide.py mlp 71 300         # one training step of random MLPs against the oracle
 
 The generators and checks are the committed tests' own (test_gpu_graphs,
 test_gpu_hip_graph, test_gpu_kernels, test_gpu_typed); `strided` adds GEMMs
@@ -252,11 +253,90 @@ def noalloc(seed, count):
             progress(f"noalloc {i}")
 
 
+def _mlp_case(rsl, oracle, rng):
+    from rushlite_amd.nets import layers
+    nl = int(rng.integers(1, 4))
+    widths = [int(rng.choice([rng.integers(1, 80), rng.integers(80, 700)])) for _ in range(nl + 1)]
+    batch = int(rng.choice([rng.integers(1, 40), rng.integers(40, 600)]))
+    x = rng.random((batch, widths[0]), dtype=np.float32)
+    y = rng.random((batch, widths[-1]), dtype=np.float32)
+    ws = [(rng.standard_normal((widths[i], widths[i + 1])) / np.sqrt(widths[i])).astype(np.float32)
+          for i in range(nl)]
+    bs = [(rng.standard_normal(widths[i + 1]) * 0.1).astype(np.float32) for i in range(nl)]
+    mods = []
+    for i in range(nl):
+        mods.append(layers.Linear(widths[i], widths[i + 1]))
+        if i < nl - 1:
+            mods.append(layers.ReLU())
+    mods.append(layers.Softmax(dim=-1))
+    model = layers.Sequential(mods)
+    li = 0
+    for i, m in enumerate(mods):
+        if isinstance(m, layers.Linear):
+            model.params[f"{i}.weights"] = rsl.Variable(ws[li], requires_grad=True)
+            model.params[f"{i}.bias"] = rsl.Variable(bs[li], requires_grad=True)
+            li += 1
+    capture = bool(rng.integers(0, 2))
+    xv, yv = rsl.Variable(x), rsl.Variable(y)
+    with rsl.capture_on(capture):
+        probs = model(xv)
+        loss = (-yv * rsl.log(probs + 1e-3)).sum(1).sum(0)
+    loss.backward()
+    ref_loss, ref_gw, ref_gb = oracle.mlp_step(ws, bs, x, y)
+    _, r64_gw, r64_gb = oracle.mlp_step(ws, bs, x, y, f64_gemm=True)
+    case = (widths, batch, capture)
+    # Skip a step that is ill-conditioned in float32: both oracle orders more
+    # than half the bar from torch float64 (a cancelling column sum of a
+    # saturated softmax's gradient, say), where valid float32 orders disagree.
+    import torch
+    from test_oracle import _torch_softmax_lamp
+    tw = [torch.tensor(w, dtype=torch.float64, requires_grad=True) for w in ws]
+    tb = [torch.tensor(b, dtype=torch.float64, requires_grad=True) for b in bs]
+    h = torch.tensor(x, dtype=torch.float64)
+    for i in range(nl):
+        h = h @ tw[i] + tb[i]
+        if i < nl - 1:
+            # a pre-activation within float32 GEMM rounding of zero: the ReLU
+            # mask there depends on the summation order
+            hv = h.detach().abs()
+            if float(hv.min()) < 2e-6 * float(hv.max()):
+                pytest.skip(f"a ReLU input within rounding of zero: {case}")
+            h = torch.clamp(h, min=0.0)
+    tl = (-torch.tensor(y, dtype=torch.float64) * torch.log(_torch_softmax_lamp(h, -1) + 1e-3))
+    tl.sum(1, keepdim=True).sum(0, keepdim=True).backward()
+    truth = [t.grad.numpy() for pair in zip(tw, tb) for t in pair]
+    refs_all = [t for pair in zip(ref_gw, ref_gb) for t in pair]
+    refs64_all = [t for pair in zip(r64_gw, r64_gb) for t in pair]
+    for r, r64, t in zip(refs_all, refs64_all, truth):
+        if min(rel_err(r, t), rel_err(r64, t)) > 5e-5:
+            pytest.skip(f"ill-conditioned in float32: {case}")
+    assert abs(loss.tolist()[0] - ref_loss) <= 1e-4 * max(abs(ref_loss), 1e-30), case
+    grads = [p.grad.numpy() for _, p in model.named_parameters()]
+    refs = [t for pair in zip(ref_gw, ref_gb) for t in pair]
+    refs64 = [t for pair in zip(r64_gw, r64_gb) for t in pair]
+    for i, (g, r, r64) in enumerate(zip(grads, refs, refs64)):
+        assert min(rel_err(g, r), rel_err(g, r64)) <= 1e-4, (case, i)
+
+
+def mlp(seed, count):
+    """One training step of random Linear-ReLU-...-Softmax nets (1-3 layers,
+    widths and batches across the GEMM kernels' thresholds, the forward
+    captured or eager) against the oracle's step in two GEMM orders."""
+    import rushlite_amd as rsl
+    from oracle import lamp_oracle as oracle
+    oracle.load()
+    rng = np.random.default_rng(seed)
+    for i in range(count):
+        attempt("mlp", _mlp_case, rsl, oracle, rng)
+        if i % 25 == 0:
+            progress(f"mlp {i}")
+
+
 def main():
     suite, a, b = sys.argv[1], int(sys.argv[2]), int(sys.argv[3])
     abi.check(abi.lib().lmp_rt_init(0))
     {"programs": programs, "gemm": gemm, "strided": strided, "ops": ops,
-     "typed": typed, "noalloc": noalloc}[suite](a, b)
+     "typed": typed, "noalloc": noalloc, "mlp": mlp}[suite](a, b)
     print("DONE", suite, COUNTS, flush=True)
     sys.exit(1 if COUNTS["fail"] else 0)
 
