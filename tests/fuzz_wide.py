@@ -10,6 +10,7 @@ every few dozen cases and every mismatch:
     python tests/fuzz_wide.py typed 41 400       # bool / int / float64 GEMM, reduce, binary
     python tests/fuzz_wide.py noalloc 61 400     # the no-allocation GEMM against the allocating one
     python tests/fuzz_wide.py mlp 71 300         # one training step of random MLPs against the oracle
+    python tests/fuzz_wide.py graphs 81 100      # random MLP steps in HIP graphs against eager twins
 
 The generators and checks are the committed tests' own (test_gpu_graphs,
 test_gpu_hip_graph, test_gpu_kernels, test_gpu_typed); `strided` adds GEMMs
@@ -332,11 +333,28 @@ def mlp(seed, count):
             progress(f"mlp {i}")
 
 
+def graphs(seed, count):
+    """Random MLP training steps captured in a HIP graph (the update eager or
+    captured), every replay against an eager twin bit for bit."""
+    import rushlite_amd as rsl
+    import test_gpu_hip_graph as TH
+    rng = np.random.default_rng(seed)
+    for i in range(count):
+        nl = int(rng.integers(1, 4))
+        dims = tuple(int(rng.choice([rng.integers(1, 80), rng.integers(80, 1100)]))
+                     for _ in range(nl + 1))
+        batch = int(rng.choice([rng.integers(1, 40), rng.integers(40, 600)]))
+        attempt("graph", TH.test_graph_replays_equal_eager_steps, rsl, dims, batch,
+                bool(rng.integers(0, 2)))
+        if i % 10 == 0:
+            progress(f"graphs {i}")
+
+
 def main():
     suite, a, b = sys.argv[1], int(sys.argv[2]), int(sys.argv[3])
     abi.check(abi.lib().lmp_rt_init(0))
     {"programs": programs, "gemm": gemm, "strided": strided, "ops": ops,
-     "typed": typed, "noalloc": noalloc, "mlp": mlp}[suite](a, b)
+     "typed": typed, "noalloc": noalloc, "mlp": mlp, "graphs": graphs}[suite](a, b)
     print("DONE", suite, COUNTS, flush=True)
     sys.exit(1 if COUNTS["fail"] else 0)
 
