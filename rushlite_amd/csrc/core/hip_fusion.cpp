@@ -813,7 +813,9 @@ std::string codegen_rows(const Region& r, const RowPlan& rp, const std::string& 
     for (int off = 1; off <= 32; off <<= 1)
       os << "    { const " << T << " o = lmp_swap<" << off << ">(" << P << "v); " << P
          << "v = " << comb(P + "v", "o") << "; }\n";
-    os << "    v" << m << " = " << P << "v;\n  }\n";
+    // Every lane goes on with lane 0's result, the value the eager kernel
+    // stores (the lanes can differ where max/min tie +0 and -0).
+    os << "    v" << m << " = lmp_lane0(" << P << "v);\n  }\n";
   }
   os << "  // stores\n";
   const auto store = [&](size_t m, const std::string& ptr) {

@@ -11,6 +11,7 @@ every few dozen cases and every mismatch:
     python tests/fuzz_wide.py noalloc 61 400     # the no-allocation GEMM against the allocating one
     python tests/fuzz_wide.py mlp 71 300         # one training step of random MLPs against the oracle
     python tests/fuzz_wide.py graphs 81 100      # random MLP steps in HIP graphs against eager twins
+    python tests/fuzz_wide.py specials 91 600    # fused against eager on special-value inputs
 
 The generators and checks are the committed tests' own (test_gpu_graphs,
 test_gpu_hip_graph, test_gpu_kernels, test_gpu_typed); `strided` adds GEMMs
@@ -350,11 +351,57 @@ def graphs(seed, count):
             progress(f"graphs {i}")
 
 
+def _same_or_both_nan(got, want):
+    got, want = np.asarray(got), np.asarray(want)
+    nan = np.isnan(want)
+    return (got.shape == want.shape and np.array_equal(np.isnan(got), nan)
+            and np.array_equal(got[~nan].view(np.uint8), want[~nan].view(np.uint8)))
+
+
+def _specials_case(rsl, rng, seed, shape, dtype):
+    import test_gpu_graphs as TG
+    from _helpers import SPECIALS
+    leaves, steps, shapes = TG.make_program_3d(seed, *shape)
+    arrs = []
+    for s in leaves:
+        v = rng.uniform(-1.0, 1.0, s)
+        pick = rng.random(s) < 0.3
+        v[pick] = rng.choice(SPECIALS.astype(np.float64), int(pick.sum()))
+        arrs.append(v.astype(dtype))
+    kind = rsl.dtype.float64 if dtype == np.float64 else rsl.dtype.float32
+    ops = TG.lamp_ops(rsl, kind)
+    outs = []
+    for capture in (False, True):
+        lv = [rsl.Variable(a, dtype=kind) for a in arrs]
+        with rsl.capture_on(capture):
+            out = TG._run_steps(ops, lv, steps)
+        outs.append(out.numpy())
+    assert _same_or_both_nan(outs[1], outs[0]), (seed, shape, np.dtype(dtype).name, steps)
+
+
+def specials(seed, count):
+    """Random elementwise and reduction programs (the 3-d generator: every
+    broadcast kind, reductions over any axis) on inputs 30% special values
+    (signed zeros, infinities, NaN, subnormals, extremes): the fused kernels
+    against the eager ones, bit for bit, NaN by position."""
+    import rushlite_amd as rsl
+    import test_gpu_graphs as TG
+    rng = np.random.default_rng(seed)
+    shapes = TG.D3_SHAPES + [(1, 64, 128), (2, 33, 7)]
+    for i in range(count):
+        shape = shapes[int(rng.integers(0, len(shapes)))]
+        dt = np.float64 if rng.random() < 0.3 else np.float32
+        attempt("specials", _specials_case, rsl, rng, int(rng.integers(0, 1 << 30)), shape, dt)
+        if i % 50 == 0:
+            progress(f"specials {i}")
+
+
 def main():
     suite, a, b = sys.argv[1], int(sys.argv[2]), int(sys.argv[3])
     abi.check(abi.lib().lmp_rt_init(0))
     {"programs": programs, "gemm": gemm, "strided": strided, "ops": ops,
-     "typed": typed, "noalloc": noalloc, "mlp": mlp, "graphs": graphs}[suite](a, b)
+     "typed": typed, "noalloc": noalloc, "mlp": mlp, "graphs": graphs,
+     "specials": specials}[suite](a, b)
     print("DONE", suite, COUNTS, flush=True)
     sys.exit(1 if COUNTS["fail"] else 0)
 

@@ -786,6 +786,40 @@ def test_captured_max_min_special_values_equal_eager(rsl, length):
         assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), op
 
 
+@pytest.mark.parametrize("dtype", ["float32", "float64"])
+def test_captured_reduction_used_elementwise_after_signed_zero_tie(rsl, dtype):
+    """A max/min whose +0 and -0 tie at the extreme, used by elementwise ops in
+    the same fused row kernel: every lane must go on with the value the eager
+    kernel stores (lane 0's after the butterfly; other lanes can hold the
+    other zero), so min(x) / (1 + x*x) keeps one zero sign along the row, as
+    eager.  Found by a wider random run (a float64 row of 103 -0 and 7 +0)."""
+    dt = np.float64 if dtype == "float64" else np.float32
+    kind = getattr(rsl.dtype, dtype)
+    rows = np.ones((6, 128), dt)
+    rows[0, 0:64:2] = -0.0
+    rows[0, 1:64:2] = 0.0                       # -0 in even lanes, +0 in odd
+    rows[1, :64] = 0.0
+    rows[1, 5] = -0.0                           # one -0 among +0
+    rows[2, :] = -0.0
+    rows[2, 77] = 0.0                           # one +0 in the second half
+    rows[3, 64:] = 0.0
+    rows[3, 100:128:3] = -0.0                   # the tie in the second half
+    rows[4, ::5] = -0.0
+    rows[4, 1::5] = 0.0
+    rows[5, :] = -1.0                           # no zero at the minimum
+    for op in ("max", "min"):
+        src = -rows if op == "max" else rows
+        a = rsl.Variable(src, dtype=kind)
+        fn = getattr(rsl, op)
+        eager = (fn(a, 1) / (a * a + 1.0)).numpy()
+        with rsl.no_grad(), rsl.capture_on():
+            r = fn(a, 1) / (a * a + 1.0)
+        got = r.numpy()
+        assert np.array_equal(got.view(np.uint8), eager.view(np.uint8)), op
+        for i in range(5):  # one zero sign along each tying row
+            assert len(set(np.signbit(got[i]).tolist())) == 1, (op, i)
+
+
 @pytest.mark.parametrize("capture", [False, True])
 def test_empty_tensors(rsl, oracle, capture):
     """Variables with a zero extent, eager and under capture_on: elementwise
