@@ -12,6 +12,7 @@ every few dozen cases and every mismatch:
     python tests/fuzz_wide.py mlp 71 300         # one training step of random MLPs against the oracle
     python tests/fuzz_wide.py graphs 81 100      # random MLP steps in HIP graphs against eager twins
     python tests/fuzz_wide.py specials 91 600    # fused against eager on special-value inputs
+    python tests/fuzz_wide.py bits 101 600       # captured programs against eager, bit for bit
 
 The generators and checks are the committed tests' own (test_gpu_graphs,
 test_gpu_hip_graph, test_gpu_kernels, test_gpu_typed); `strided` adds GEMMs
@@ -379,6 +380,41 @@ def _specials_case(rsl, rng, seed, shape, dtype):
     assert _same_or_both_nan(outs[1], outs[0]), (seed, shape, np.dtype(dtype).name, steps)
 
 
+def _bits_case(rsl, rng, seed, shape, dtype):
+    import test_gpu_graphs as TG
+    leaves, steps, shapes = TG.make_program_rc(seed, *shape)
+    arrs = [rng.uniform(-1.0, 1.0, s).astype(dtype) for s in leaves]
+    kind = rsl.dtype.float64 if dtype == np.float64 else rsl.dtype.float32
+    ops = TG.lamp_ops(rsl, kind)
+    outs, grads = [], []
+    for capture in (False, True):
+        lv = [rsl.Variable(a, requires_grad=True, dtype=kind) for a in arrs]
+        with rsl.capture_on(capture):
+            out = TG._run_steps(ops, lv, steps)
+            total = TG.run(ops, lv, steps, shapes)
+        outs.append(out.numpy())
+        total.backward()
+        grads.append([v.grad.numpy() for v in lv])
+    assert _same_or_both_nan(outs[1], outs[0]), (seed, shape, "value", steps)
+    for i, (g1, g0) in enumerate(zip(grads[1], grads[0])):
+        assert _same_or_both_nan(g1, g0), (seed, shape, "grad", i, steps)
+
+
+def bits(seed, count):
+    """Random programs over [R, C] leaves (matmul and transpose included),
+    captured against eager: values and every input gradient bit for bit."""
+    import rushlite_amd as rsl
+    import test_gpu_graphs as TG
+    rng = np.random.default_rng(seed)
+    shapes = TG.RC_SHAPES + [(512, 1000), (7, 5)]
+    for i in range(count):
+        shape = shapes[int(rng.integers(0, len(shapes)))]
+        dt = np.float64 if rng.random() < 0.3 else np.float32
+        attempt("bits", _bits_case, rsl, rng, int(rng.integers(0, 1 << 30)), shape, dt)
+        if i % 50 == 0:
+            progress(f"bits {i}")
+
+
 def specials(seed, count):
     """Random elementwise and reduction programs (the 3-d generator: every
     broadcast kind, reductions over any axis) on inputs 30% special values
@@ -401,7 +437,7 @@ def main():
     abi.check(abi.lib().lmp_rt_init(0))
     {"programs": programs, "gemm": gemm, "strided": strided, "ops": ops,
      "typed": typed, "noalloc": noalloc, "mlp": mlp, "graphs": graphs,
-     "specials": specials}[suite](a, b)
+     "specials": specials, "bits": bits}[suite](a, b)
     print("DONE", suite, COUNTS, flush=True)
     sys.exit(1 if COUNTS["fail"] else 0)
 
