@@ -13,6 +13,7 @@ every few dozen cases and every mismatch:
     python tests/fuzz_wide.py graphs 81 100      # random MLP steps in HIP graphs against eager twins
     python tests/fuzz_wide.py specials 91 600    # fused against eager on special-value inputs
     python tests/fuzz_wide.py bits 101 600       # captured programs against eager, bit for bit
+    python tests/fuzz_wide.py copies 111 400     # host-device copies of random sizes and offsets
 
 The generators and checks are the committed tests' own (test_gpu_graphs,
 test_gpu_hip_graph, test_gpu_kernels, test_gpu_typed); `strided` adds GEMMs
@@ -415,6 +416,42 @@ def bits(seed, count):
             progress(f"bits {i}")
 
 
+def _copies_case(L, rng):
+    nbytes = int(np.exp(rng.uniform(0, np.log(96 << 20))))
+    so, do = int(rng.integers(0, 64)), int(rng.integers(0, 64))
+    src = rng.integers(0, 256, so + nbytes + 64, dtype=np.uint8)
+    dev = abi.DeviceBuffer((do + nbytes + 64,), np.uint8)
+    guard = rng.integers(0, 256, do + nbytes + 64, dtype=np.uint8)
+    abi.check(L.lmp_rt_memcpy_h2d(dev.ptr, guard.ctypes.data, guard.nbytes))
+    abi.check(L.lmp_rt_memcpy_h2d(dev.ptr + do, src.ctypes.data + so, nbytes))
+    back = np.empty(do + nbytes + 64, np.uint8)
+    abi.check(L.lmp_rt_memcpy_d2h(back.ctypes.data, dev.ptr, back.nbytes))
+    want = guard.copy()
+    want[do:do + nbytes] = src[so:so + nbytes]
+    assert np.array_equal(back, want), ("h2d", nbytes, so, do)
+    # device to device into another offset, then a partial download
+    dev2 = abi.DeviceBuffer((nbytes + 128,), np.uint8)
+    o2 = int(rng.integers(0, 64))
+    abi.check(L.lmp_rt_memcpy_d2d(dev2.ptr + o2, dev.ptr + do, nbytes))
+    part = np.empty(nbytes + 8, np.uint8)
+    part[-8:] = 7
+    abi.check(L.lmp_rt_memcpy_d2h(part.ctypes.data, dev2.ptr + o2, nbytes))
+    assert np.array_equal(part[:nbytes], src[so:so + nbytes]), ("d2d/d2h", nbytes, so, do, o2)
+    assert np.all(part[-8:] == 7), ("d2h wrote past its end", nbytes)
+
+
+def copies(seed, count):
+    """Host-device copies of random sizes (1 byte to 96 MiB, across the staging
+    threshold and chunk boundaries) at random byte offsets on both sides: the
+    bytes arrive, nothing around them changes."""
+    L = abi.lib()
+    rng = np.random.default_rng(seed)
+    for i in range(count):
+        attempt("copies", _copies_case, L, rng)
+        if i % 50 == 0:
+            progress(f"copies {i}")
+
+
 def specials(seed, count):
     """Random elementwise and reduction programs (the 3-d generator: every
     broadcast kind, reductions over any axis) on inputs 30% special values
@@ -437,7 +474,7 @@ def main():
     abi.check(abi.lib().lmp_rt_init(0))
     {"programs": programs, "gemm": gemm, "strided": strided, "ops": ops,
      "typed": typed, "noalloc": noalloc, "mlp": mlp, "graphs": graphs,
-     "specials": specials, "bits": bits}[suite](a, b)
+     "specials": specials, "bits": bits, "copies": copies}[suite](a, b)
     print("DONE", suite, COUNTS, flush=True)
     sys.exit(1 if COUNTS["fail"] else 0)
 
