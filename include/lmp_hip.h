@@ -273,7 +273,10 @@ int lmp_k_gemm_f32_noalloc(int trans_a, int trans_b, size_t m, size_t n, size_t 
  * of the finished fp32 product (after any split-K fold): one pass instead of
  * the reference's matmul followed by a broadcast add (LinearImpl::forward,
  * layers/linear.cpp:21-26; linear.py:31-34).  Same rounding as the two-step
- * form: the product is complete before the bias is added. */
+ * form: the product is complete before the bias is added, and it is the
+ * product lmp_k_gemm_f32 computes (the same kernel whatever the bias; a bias
+ * that is not 16-byte aligned is first copied to one that is), so the result
+ * equals lmp_k_gemm_f32 then the add bit for bit. */
 int lmp_k_linear_f32(int trans_a, int trans_b, size_t m, size_t n, size_t k,
                      const float* a, size_t lda, const float* b, size_t ldb,
                      const float* bias, float* c, size_t ldc);
