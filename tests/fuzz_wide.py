@@ -14,6 +14,7 @@ every few dozen cases and every mismatch:
     python tests/fuzz_wide.py specials 91 600    # fused against eager on special-value inputs
     python tests/fuzz_wide.py bits 101 600       # captured programs against eager, bit for bit
     python tests/fuzz_wide.py copies 111 400     # host-device copies of random sizes and offsets
+    python tests/fuzz_wide.py held 121 500       # captured programs with intermediates held, bit for bit
 
 The generators and checks are the committed tests' own (test_gpu_graphs,
 test_gpu_hip_graph, test_gpu_kernels, test_gpu_typed); `strided` adds GEMMs
@@ -401,6 +402,48 @@ def _bits_case(rsl, rng, seed, shape, dtype):
         assert _same_or_both_nan(g1, g0), (seed, shape, "grad", i, steps)
 
 
+def _held_case(rsl, rng, seed, shape, dtype):
+    import test_gpu_graphs as TG
+    leaves, steps, shapes = TG.make_program_rc(seed, *shape)
+    arrs = [rng.uniform(-1.0, 1.0, s).astype(dtype) for s in leaves]
+    kind = rsl.dtype.float64 if dtype == np.float64 else rsl.dtype.float32
+    ops = TG.lamp_ops(rsl, kind)
+    first = len(leaves)
+    keep = sorted(set(int(i) for i in rng.integers(first, first + len(steps), int(rng.integers(1, 24)))))
+    results = []
+    for capture in (False, True):
+        # one step at a time over a growing pool (the step's operands index
+        # it), so every intermediate has a Python owner while the rest of the
+        # program is recorded; those in `keep` outlive the region
+        pool = [rsl.Variable(a, dtype=kind) for a in arrs]
+        with rsl.capture_on(capture):
+            for st in steps:
+                pool.append(TG._run_steps(ops, pool, [st]))
+        held = {i: pool[i] for i in keep}
+        held[-1] = pool[-1]
+        del pool
+        results.append({i: v.numpy() for i, v in held.items()})
+    for i in results[0]:
+        assert _same_or_both_nan(results[1][i], results[0][i]), (seed, shape, "value", i, keep, steps)
+
+
+def held(seed, count):
+    """Random programs run with some intermediates held by the caller (so the
+    fused regions store them as extra outputs, split at the output limit, or
+    cut there), captured against eager: every held value and the result bit
+    for bit."""
+    import rushlite_amd as rsl
+    import test_gpu_graphs as TG
+    rng = np.random.default_rng(seed)
+    shapes = TG.RC_SHAPES + [(512, 1000), (7, 5)]
+    for i in range(count):
+        shape = shapes[int(rng.integers(0, len(shapes)))]
+        dt = np.float64 if rng.random() < 0.3 else np.float32
+        attempt("held", _held_case, rsl, rng, int(rng.integers(0, 1 << 30)), shape, dt)
+        if i % 50 == 0:
+            progress(f"held {i}")
+
+
 def bits(seed, count):
     """Random programs over [R, C] leaves (matmul and transpose included),
     captured against eager: values and every input gradient bit for bit."""
@@ -474,7 +517,7 @@ def main():
     abi.check(abi.lib().lmp_rt_init(0))
     {"programs": programs, "gemm": gemm, "strided": strided, "ops": ops,
      "typed": typed, "noalloc": noalloc, "mlp": mlp, "graphs": graphs,
-     "specials": specials, "bits": bits, "copies": copies}[suite](a, b)
+     "specials": specials, "bits": bits, "copies": copies, "held": held}[suite](a, b)
     print("DONE", suite, COUNTS, flush=True)
     sys.exit(1 if COUNTS["fail"] else 0)
 
