@@ -15,6 +15,7 @@ every few dozen cases and every mismatch:
     python tests/fuzz_wide.py bits 101 600       # captured programs against eager, bit for bit
     python tests/fuzz_wide.py copies 111 400     # host-device copies of random sizes and offsets
     python tests/fuzz_wide.py held 121 500       # captured programs with intermediates held, bit for bit
+    python tests/fuzz_wide.py large 131 100      # GEMMs of 2^30+ multiply-adds, sampled rows and columns
 
 The generators and checks are the committed tests' own (test_gpu_graphs,
 test_gpu_hip_graph, test_gpu_kernels, test_gpu_typed); `strided` adds GEMMs
@@ -163,6 +164,55 @@ def strided(seed, count):
         attempt("strided", _strided_case, L, rng)
         if i % 100 == 0:
             progress(f"strided {i}")
+
+
+def _large_case(L, rng):
+    # extents log-uniform in [1, 9000], redrawn until the product has at
+    # least 2^30 multiply-adds: large tile walks, ragged edges, split K
+    while True:
+        m, n, k = (int(np.exp(rng.uniform(0.0, np.log(9000.0)))) for _ in range(3))
+        if m * n * k >= (1 << 30):
+            break
+    ta, tb = int(rng.integers(0, 2)), int(rng.integers(0, 2))
+    kind = str(rng.choice(["gemm", "acc", "relu"]))
+    ar, ac = (k, m) if ta else (m, k)
+    br, bc = (n, k) if tb else (k, n)
+    a = rng.standard_normal((ar, ac), dtype=np.float32) * np.float32(0.02)
+    b = rng.standard_normal((br, bc), dtype=np.float32) * np.float32(0.02)
+    bias = rng.standard_normal(n, dtype=np.float32) * np.float32(0.01)
+    c0 = rng.standard_normal((m, n), dtype=np.float32) * np.float32(0.01)
+    da, db, dbias = (abi.DeviceBuffer.from_numpy(x) for x in (a, b, bias))
+    dc = abi.DeviceBuffer.from_numpy(c0)
+    if kind == "relu":
+        st = L.lmp_k_linear_relu_f32(ta, tb, m, n, k, da.ptr, ac, db.ptr, bc, dbias.ptr, dc.ptr, n)
+    else:
+        st = L.lmp_k_gemm_f32(ta, tb, m, n, k, da.ptr, ac, db.ptr, bc, dc.ptr, n, int(kind == "acc"))
+    abi.check(st)
+    got = dc.numpy()
+    del da, db, dc
+    A = (a.T if ta else a).astype(np.float64)
+    B = (b.T if tb else b).astype(np.float64)
+    rows = np.concatenate([rng.choice(m, min(m, 24), replace=False), [0, m - 1]])
+    cols = np.concatenate([rng.choice(n, min(n, 24), replace=False), [0, n - 1]])
+    for part, g, want, base, bb in (("rows", got[rows], A[rows] @ B, c0[rows], bias),
+                                    ("cols", got[:, cols], A @ B[:, cols], c0[:, cols], bias[cols])):
+        if kind == "acc":
+            want = want + base
+        elif kind == "relu":
+            want = np.maximum(want + bb, 0.0)
+        assert rel_err(g, want) <= 1e-4, (m, n, k, ta, tb, kind, part)
+
+
+def large(seed, count):
+    """Random GEMMs of 2^30 to 7.3e11 multiply-adds (extents up to 9000, every
+    orientation, plain, accumulating and bias + ReLU): 26 sampled rows and 26
+    sampled columns of each against float64 at 1e-4."""
+    L = abi.lib()
+    rng = np.random.default_rng(seed)
+    for i in range(count):
+        attempt("large", _large_case, L, rng)
+        if i % 10 == 0:
+            progress(f"large {i}")
 
 
 def _random_shape(rng):
@@ -517,7 +567,7 @@ def main():
     abi.check(abi.lib().lmp_rt_init(0))
     {"programs": programs, "gemm": gemm, "strided": strided, "ops": ops,
      "typed": typed, "noalloc": noalloc, "mlp": mlp, "graphs": graphs,
-     "specials": specials, "bits": bits, "copies": copies, "held": held}[suite](a, b)
+     "specials": specials, "bits": bits, "copies": copies, "held": held, "large": large}[suite](a, b)
     print("DONE", suite, COUNTS, flush=True)
     sys.exit(1 if COUNTS["fail"] else 0)
 
