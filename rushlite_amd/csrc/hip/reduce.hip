@@ -401,10 +401,16 @@ bool aligned16(const void* p) {
 
 uint32_t blocks_for(uint64_t n) { return uint32_t((n + kBlock - 1) / kBlock); }
 
+// The float4 row and column kernels index within a row or a column with
+// 32-bit counters that run up to a few hundred past the extent (and a chunk
+// start plus a chunk length): extents of 2^31 float4 (rows) or 2^31 rows
+// (columns) or more take the 64-bit kernels instead.
+constexpr uint64_t kMaxU32Extent = 0x7fffffffull;
+
 template <int OP, typename T>
 int reduce_rows(Runtime* rt, T* out, const T* in, uint64_t rows, uint64_t len) {
   if constexpr (std::is_same_v<T, float>) {
-    if (len >= 2048 && len % 4 == 0 && aligned16(in) && len / 4 <= 0xffffffffull) {
+    if (len >= 2048 && len % 4 == 0 && aligned16(in) && len / 4 <= kMaxU32Extent) {
       const uint64_t len4 = len / 4;
       // Enough workgroups to fill the chip twice over; split long rows only
       // when rows alone cannot.
@@ -445,7 +451,7 @@ int reduce_rows(Runtime* rt, T* out, const T* in, uint64_t rows, uint64_t len) {
   const uint64_t blocks = (rows + kWaves - 1) / kWaves;
   if (blocks > 0x7fffffffull) return fail(LMP_ERR_UNSUPPORTED, "reduce: too many rows");
   if constexpr (std::is_same_v<T, float>) {
-    if (len % 4 == 0 && aligned16(in) && len / 4 <= 0xffffffffull) {
+    if (len % 4 == 0 && aligned16(in) && len / 4 <= kMaxU32Extent) {
       hipLaunchKernelGGL((row_reduce_wave_f32<OP>), dim3(uint32_t(blocks)), dim3(kBlock), 0,
                          rt->stream, out, in, rows, uint32_t(len / 4));
       LMP_LAUNCH_CHECK("row_reduce_wave_f32");
@@ -463,7 +469,7 @@ int reduce_cols(Runtime* rt, T* out, const T* in, uint64_t outer, uint64_t len,
                 uint64_t inner) {
   const bool vec = std::is_same_v<T, float> && inner % 4 == 0 && aligned16(in) &&
                    aligned16(out) && inner / 4 <= 0x7fffffffull &&
-                   len <= 0xffffffffull;
+                   len <= kMaxU32Extent;
   // Lanes per workgroup along the columns: 64 float4 lanes (4 waves share a
   // strip) on the vector path, 256 scalar lanes otherwise.
   const uint64_t lanes = vec ? inner / 4 : inner;

@@ -239,6 +239,40 @@ def test_binary_extent_beyond_32_bits(hip):
     hip.check(L.lmp_rt_empty_cache())
 
 
+def _plant(hip, buf, cols, marks):
+    for (r, c), v in marks.items():
+        x = np.array([v], np.float32)
+        hip.check(hip.lib().lmp_rt_memcpy_h2d(C.c_void_p(buf.ptr + 4 * (r * cols + c)),
+                                              x.ctypes.data_as(C.c_void_p), 4))
+
+
+def test_reduce_offsets_beyond_32_bits(hip):
+    """Sum and max over dim 1 of [2, 2^31 + 8] (16 GiB: row 1 starts past 2^31
+    floats, each row split over 1024 workgroups) and over dim 0 of
+    [2^21 + 3, 1024] (2.1e9 elements, the column kernel's chunks ending past
+    2^31 floats): a background of 0 (sum) or -1 (max) with values planted at
+    the ends and around 2^30 / 2^31, so every result is exact."""
+    L = hip.lib()
+    for (rows, cols, axis, marks) in (
+            (2, (1 << 31) + 8, 1, {(0, 0): 1.0, (0, (1 << 31) + 7): 2.0, (1, 0): 4.0,
+                                   (1, 1 << 30): 16.0, (1, (1 << 31) + 7): 8.0}),
+            ((1 << 21) + 3, 1024, 0, {(0, 0): 1.0, ((1 << 21) + 2, 0): 2.0,
+                                      ((1 << 21) + 2, 1023): 4.0, (1 << 21, 517): 8.0,
+                                      (1 << 20, 3): 32.0})):
+        a = hip.DeviceBuffer((rows, cols), np.float32)
+        for op, background in (("sum", 0.0), ("max", -1.0)):
+            hip.check(L.lmp_k_fill(hip.FLOAT32, a.ptr, rows * cols, background))
+            _plant(hip, a, cols, marks)
+            want = np.full(rows if axis == 1 else cols, background, np.float32)
+            for (r, c), v in marks.items():
+                i = r if axis == 1 else c
+                want[i] = want[i] + v if op == "sum" else max(want[i], v)
+            got = hip.reduce(op, a, axis).numpy().ravel()
+            assert np.array_equal(got, want), (rows, cols, op)
+        a.free()
+        hip.check(L.lmp_rt_empty_cache())
+
+
 def test_fill_cast_add_inplace(hip):
     L = hip.lib()
     buf = hip.DeviceBuffer((1001,), np.float32)
