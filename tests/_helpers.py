@@ -66,3 +66,22 @@ def special_rows(length, rng):
     rows[7, 0::11] = -0.0
     rows[8] = rng.standard_normal(length)
     return rows
+
+
+def assert_sum_close(got, want, a, axis):
+    """A float32 sum against the oracle's sequential sum `want` at 1e-5
+    under max|diff|/max|want|.  A cancelling sum (one far smaller than the sum
+    of its terms' magnitudes) has no order-independent result at that bar:
+    there each output of both orders must lie within 1e-6 of the sum of
+    |terms| of the float64 sum, a band that a dropped or doubled term of
+    typical size still leaves.  Examples: 1995 terms up to 3.8 summing to
+    -0.129 put the sequential order 2.4e-4 (relative) from float64 and the
+    tree order 2.0e-5; 2506 terms up to 3.4 summing to -0.454 put them 4.1e-6
+    and 1.6e-5 from it."""
+    if rel_err(got, want) <= 1e-5:
+        return
+    a64 = a.astype(np.float64)
+    truth = a64.sum(axis=axis, keepdims=True)
+    band = 1e-6 * np.abs(a64).sum(axis=axis, keepdims=True)
+    assert np.all(np.abs(got - truth) <= band), rel_err(got, want)
+    assert np.all(np.abs(want - truth) <= band), rel_err(got, want)

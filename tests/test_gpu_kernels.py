@@ -13,7 +13,8 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-from _helpers import SPECIALS, assert_within_ulp, rel_err, special_rows  # noqa: E402
+from _helpers import (SPECIALS, assert_sum_close, assert_within_ulp, rel_err,  # noqa: E402
+                      special_rows)
 
 
 def up(hip, arr):
@@ -303,8 +304,9 @@ REDUCE_CASES = [((300, 257), 0), ((300, 257), 1), ((4, 37, 5), 0), ((4, 37, 5), 
                 ((100, 4), 0),
                 # more outer slices than a grid's z extent
                 ((70000, 5, 4), 1),
-                # a cancelling one-wave sum (-0.129 from 1995 terms up to 3.8)
-                ((1995,), 0)]
+                # cancelling one-wave sums (-0.129 from 1995 terms up to 3.8,
+                # -0.454 from 2506 up to 3.4)
+                ((1995,), 0), ((2506,), 0)]
 
 
 @pytest.mark.parametrize("shape,axis", REDUCE_CASES, ids=str)
@@ -318,16 +320,7 @@ def test_reduce(hip, oracle, shape, axis):
     got = hip.reduce("sum", d, axis).numpy()
     want = oracle.reduce("sum", a, axis)
     assert got.shape == want.shape
-    truth = a.astype(np.float64).sum(axis=axis, keepdims=True)
-    # Within 1e-5 of float64, or no farther from it than the oracle's
-    # sequential float32 sum; and against that sum at 1e-5, or twice the
-    # oracle's own distance from float64 where that is larger.  Cancelling
-    # sums need both: a 1754-value row summing to -2.89 from terms up to 4 in
-    # size puts the sequential order 1.3e-5 from the truth and the tree order
-    # 6e-7; a 1995-value sum of -0.129 from terms up to 3.8 puts them 2.4e-4
-    # and 2.0e-5 from it.
-    assert rel_err(got, truth) <= max(1e-5, rel_err(want, truth))
-    assert rel_err(got, want) <= max(1e-5, 2 * rel_err(want, truth))
+    assert_sum_close(got, want, a, axis)
     small = (1.0 + 0.01 * a).astype(np.float32)
     got = hip.reduce("prod", up(hip, small), axis).numpy()
     assert rel_err(got, oracle.reduce("prod", small, axis)) <= 1e-5

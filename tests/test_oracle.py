@@ -280,6 +280,42 @@ def test_ulp_helpers_see_the_sign_of_zero():
                           np.array([0.0, -0.0], np.float32), 2)
 
 
+def _tree_sum_f32(v):
+    """A 64-lane strided then butterfly float32 sum (another valid order)."""
+    lanes = np.zeros(64, np.float32)
+    for j in range(0, len(v), 64):
+        chunk = np.zeros(64, np.float32)
+        chunk[:len(v) - j] = v[j:j + 64]
+        lanes = (lanes + chunk).astype(np.float32)
+    for s in (1, 2, 4, 8, 16, 32):
+        lanes = (lanes + lanes[np.arange(64) ^ s]).astype(np.float32)
+    return lanes[:1]
+
+
+def _seq_sum_f32(v):
+    acc = np.float32(0.0)
+    for x in v:
+        acc = np.float32(acc + x)
+    return np.array([acc], np.float32)
+
+
+@pytest.mark.parametrize("n", [1995, 2506, 4096])
+def test_sum_bound_accepts_other_orders_and_catches_term_errors(n):
+    """assert_sum_close (the GPU sum tests' bound) accepts a tree-order float32
+    sum against the sequential one, cancelling or not (the 1995- and 2506-term
+    vectors are the cancelling sums of test_reduce), and rejects a sum that
+    dropped or doubled one typical term."""
+    from _helpers import assert_sum_close
+    a = np.random.default_rng(zlib.crc32(repr(((n,), 0)).encode())).standard_normal(
+        n, dtype=np.float32)
+    want, got = _seq_sum_f32(a), _tree_sum_f32(a)
+    assert_sum_close(got, want, a, 0)
+    j = int(np.argsort(np.abs(a))[n // 2])  # a term of median size
+    for bad in (got - a[j], got + a[j]):
+        with pytest.raises(AssertionError):
+            assert_sum_close(bad.astype(np.float32), want, a, 0)
+
+
 @pytest.mark.parametrize("op,fn,x,want", [
     ("sin", math.sin, -0.0, -0.0), ("sin", math.sin, 0.0, 0.0),
     ("tan", math.tan, -0.0, -0.0), ("tan", math.tan, 0.0, 0.0),
